@@ -1,0 +1,168 @@
+/*
+ * mfhip.h -- C ABI of libmfhip.so, the MI355X (gfx950) transformer
+ * evaluation backend for MetalFish.
+ *
+ * This is the drop-in boundary below MetalFish's `NN::Network` interface
+ * (reference src/nn/network.h:38-51).  A C++ adapter (metalfish_amd/csrc/
+ * host/hip_network.{h,cpp}, class HipNetwork) implements NN::Network on top
+ * of these calls; Python binds them with ctypes (metalfish_amd/backend.py).
+ * Plain pointers and sizes only; no exceptions cross this boundary.  Every
+ * call returns MFH_OK or a negative status and leaves a message for
+ * mfh_last_error() (thread-local).
+ *
+ * Format enums take the values of the reference's NetworkFormat proto
+ * (reference src/nn/proto/net.proto:278-342) so an adapter can pass a loaded
+ * weights file's format fields through unchanged.
+ */
+#ifndef MFHIP_H
+#define MFHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MFH_OK = 0,
+  MFH_ERR_INVALID = -1,     /* bad argument, shape or missing tensor */
+  MFH_ERR_HIP = -2,         /* HIP runtime error */
+  MFH_ERR_UNSUPPORTED = -3, /* net structure outside what the kernels handle */
+  MFH_ERR_NO_DEVICE = -4,   /* no usable gfx950 device */
+  MFH_ERR_OUT_OF_MEMORY = -5
+};
+
+/* NetworkFormat.NetworkStructure (net.proto:278-287). */
+enum { MFH_NETWORK_ATTENTIONBODY_WITH_HEADFORMAT = 6,
+       MFH_NETWORK_ATTENTIONBODY_WITH_MULTIHEADFORMAT = 7 };
+/* NetworkFormat.PolicyFormat / ValueFormat (net.proto:293-305). */
+enum { MFH_POLICY_ATTENTION = 3 };
+enum { MFH_VALUE_CLASSICAL = 1, MFH_VALUE_WDL = 2 };
+/* NetworkFormat.InputEmbeddingFormat (net.proto:340-342). */
+enum { MFH_INPUT_EMBEDDING_PE_DENSE = 2 };
+/* NetworkFormat.ActivationFunction (net.proto:317-326). */
+enum {
+  MFH_ACTIVATION_DEFAULT = 0,
+  MFH_ACTIVATION_MISH = 1,
+  MFH_ACTIVATION_RELU = 2,
+  MFH_ACTIVATION_NONE = 3,
+  MFH_ACTIVATION_TANH = 4,
+  MFH_ACTIVATION_SIGMOID = 5,
+  MFH_ACTIVATION_SELU = 6,
+  MFH_ACTIVATION_SWISH = 7,
+  MFH_ACTIVATION_RELU_2 = 8
+};
+/* NetworkFormat.DefaultActivation (net.proto:331-332). */
+enum { MFH_DEFAULT_ACTIVATION_RELU = 0, MFH_DEFAULT_ACTIVATION_MISH = 1 };
+/* Storage of the GEMM weights on the device. */
+enum { MFH_WEIGHTS_BF16 = 0 };
+
+/* Network description: the format fields of the weights file plus the
+ * attention head count (Weights.headcount) and run-time sizing. */
+typedef struct {
+  int network;            /* MFH_NETWORK_ATTENTIONBODY_* */
+  int policy;             /* MFH_POLICY_ATTENTION */
+  int value;              /* MFH_VALUE_WDL or MFH_VALUE_CLASSICAL */
+  int moves_left;         /* must be 0: no moves-left head yet */
+  int input_embedding;    /* MFH_INPUT_EMBEDDING_PE_DENSE */
+  int default_activation; /* MFH_DEFAULT_ACTIVATION_* */
+  int ffn_activation;     /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
+  int smolgen_activation; /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
+  int headcount;          /* body attention heads; head depth must be 32 */
+  int weights_dtype;      /* MFH_WEIGHTS_BF16 */
+  int max_batch;          /* largest batch one eval call accepts (>= 1) */
+  int device;             /* HIP device ordinal, -1 = current device */
+} mfh_net_desc;
+
+/* One weight tensor, named as in the reference's weight inventory
+ * (e.g. "body.ip_emb_w", "body.encoder.3.mha.q_w", "policy.vanilla.ip4_pol_w",
+ * "value.winner.ip1_val_w"); matrices are row-major [out][in]. */
+typedef struct {
+  const char *name;
+  const float *data; /* host fp32 */
+  uint64_t count;    /* number of floats */
+} mfh_tensor;
+
+typedef struct mfh_net mfh_net;
+
+/* Shape inference, weight packing and upload, workspace allocation for
+ * desc->max_batch positions.  Replaces the backend constructor
+ * (reference src/nn/cuda/cuda_network.cpp:235-321) and its call from
+ * NN::CreateNetwork (reference src/nn/network.cpp:137-208). */
+int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors,
+                   int n_tensors, mfh_net **out);
+
+void mfh_net_destroy(mfh_net *net);
+
+/* Forward pass on host buffers in the reference's packed input contract
+ * (reference src/nn/input_plane_packing.h:61-83): masks[batch*112] and
+ * values[batch*112].  Outputs: policy[batch*1858] raw logits in the 1858
+ * order, wdl[batch*3] (WDL nets) or value[batch] (classical value head),
+ * moves_left must be NULL.  Inputs are staged through pinned buffers with
+ * asynchronous copies on the net's stream; the call returns when outputs are
+ * in place.  Calls on one net are serialised (reference
+ * src/nn/cuda/cuda_network.cpp:442).  batch must be 1..max_batch. */
+int mfh_net_eval(mfh_net *net, int batch, const uint64_t *masks,
+                 const float *values, float *policy, float *wdl,
+                 float *moves_left);
+
+/* Same, from unpacked planes[batch*112*64] (NN::InputPlanes layout,
+ * reference src/nn/input_planes.h:22-29); packing happens straight into the
+ * pinned staging buffer. */
+int mfh_net_eval_planes(mfh_net *net, int batch, const float *planes,
+                        float *policy, float *wdl, float *moves_left);
+
+/* Forward pass on device-resident buffers (no host copies, no
+ * synchronisation), enqueued on `stream` (a hipStream_t; NULL is the
+ * default stream).  Outputs are ready when that stream reaches this point. */
+int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
+                        const float *d_values, float *d_policy, float *d_wdl,
+                        void *stream);
+
+/* Human-readable description (GetNetworkInfo, reference network.h:47). */
+int mfh_net_info(const mfh_net *net, char *buf, size_t len);
+
+/* Capabilities (BackendCapabilities, reference network.h:21-36). */
+typedef struct {
+  int has_wdl;
+  int has_moves_left;
+  int max_batch_size;
+  int device;
+  char device_name[64];
+  char arch_name[32];
+  uint64_t weight_bytes;
+  uint64_t workspace_bytes;
+} mfh_capabilities;
+int mfh_net_capabilities(const mfh_net *net, mfh_capabilities *out);
+
+/* Number of visible devices (0 without a GPU). */
+int mfh_device_count(int *count);
+
+const char *mfh_last_error(void);
+
+/* ---- Parity hooks (used by the test suite) ---------------------------- */
+
+/* Unpacks packed inputs on the device into planes[batch*112*64] (host). */
+int mfh_debug_unpack_planes(int batch, const uint64_t *masks,
+                            const float *values, float *planes);
+
+/* C[M,N] = act(A[M,K] . W[N,K]^T + bias) with bf16 operands (host arrays of
+ * raw bf16 bits), fp32 output.  act is MFH_ACTIVATION_*. */
+int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A,
+                        const uint16_t *W, const float *bias, int act,
+                        float *C);
+
+/* Copies a named workspace tensor left by the last eval call to host
+ * memory: "body" (fp32 [B*64,E], encoder output; with no encoder layers
+ * the input-embedding output), "policy_qk" (bf16 [B*64,2Dp]),
+ * "value_hidden" (fp32 [B,Vh]).  bytes must equal the tensor's size for the
+ * last batch. */
+int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out,
+                         uint64_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MFHIP_H */

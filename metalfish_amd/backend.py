@@ -1,0 +1,236 @@
+"""Python binding of the C ABI in include/mfhip.h (libmfhip.so).
+
+``HipNetwork`` mirrors the reference's ``NN::Network`` operations
+(reference src/nn/network.h:38-51): ``evaluate`` / ``evaluate_batch`` return
+raw 1858 policy logits, WDL and value = W - L
+(reference src/nn/network_output_decoder.cpp:56-63); ``info()`` and
+``capabilities()`` stand for GetNetworkInfo / GetBackendCapabilities.
+There is no CPU fallback: without the library or a gfx950 device every call
+raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libmfhip.so")
+
+MFH_OK = 0
+ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid": 5,
+              "selu": 6, "swish": 7, "relu_2": 8}
+
+# Every symbol include/mfhip.h declares.
+EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_planes",
+           "mfh_net_eval_device", "mfh_net_info", "mfh_net_capabilities", "mfh_device_count",
+           "mfh_last_error", "mfh_debug_unpack_planes", "mfh_debug_gemm_bf16",
+           "mfh_net_debug_tensor")
+
+
+class MfhNetDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "network", "policy", "value", "moves_left", "input_embedding", "default_activation",
+        "ffn_activation", "smolgen_activation", "headcount", "weights_dtype", "max_batch",
+        "device")]
+
+
+class MfhTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("count", ctypes.c_uint64)]
+
+
+class MfhCapabilities(ctypes.Structure):
+    _fields_ = [("has_wdl", ctypes.c_int), ("has_moves_left", ctypes.c_int),
+                ("max_batch_size", ctypes.c_int), ("device", ctypes.c_int),
+                ("device_name", ctypes.c_char * 64), ("arch_name", ctypes.c_char * 32),
+                ("weight_bytes", ctypes.c_uint64), ("workspace_bytes", ctypes.c_uint64)]
+
+
+_lib = None
+
+
+def lib():
+    """Loads libmfhip.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"HIP backend library missing: {LIB_PATH} "
+                               "(run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i, u64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64
+        sig = {
+            "mfh_net_create": ([ctypes.POINTER(MfhNetDesc), vp, i, ctypes.POINTER(vp)], i),
+            "mfh_net_destroy": ([vp], None),
+            "mfh_net_eval": ([vp, i, vp, vp, vp, vp, vp], i),
+            "mfh_net_eval_planes": ([vp, i, vp, vp, vp, vp], i),
+            "mfh_net_eval_device": ([vp, i, vp, vp, vp, vp, vp], i),
+            "mfh_net_info": ([vp, ctypes.c_char_p, ctypes.c_size_t], i),
+            "mfh_net_capabilities": ([vp, ctypes.POINTER(MfhCapabilities)], i),
+            "mfh_device_count": ([ctypes.POINTER(i)], i),
+            "mfh_last_error": ([], ctypes.c_char_p),
+            "mfh_debug_unpack_planes": ([i, vp, vp, vp], i),
+            "mfh_debug_gemm_bf16": ([i, i, i, vp, vp, vp, i, vp], i),
+            "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def _check(rc, what):
+    if rc != MFH_OK:
+        msg = lib().mfh_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    _check(lib().mfh_device_count(ctypes.byref(n)), "mfh_device_count")
+    return n.value
+
+
+def _ptr(a):
+    return a.ctypes.data if a is not None else None
+
+
+class HipNetwork:
+    """Attention-body network resident on one MI355X."""
+
+    def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
+                 ffn_activation="default", smolgen_activation="swish", max_batch=256,
+                 device=-1):
+        self._weights = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+                         for k, v in weights.items()}
+        names = list(self._weights)
+        self._names = [n.encode() for n in names]
+        tensors = (MfhTensor * len(names))()
+        for j, n in enumerate(names):
+            a = self._weights[n]
+            tensors[j] = MfhTensor(self._names[j], a.ctypes.data, a.size)
+        desc = MfhNetDesc(network=6, policy=3, value=2 if wdl else 1, moves_left=0,
+                          input_embedding=2,
+                          default_activation=1 if default_activation == "mish" else 0,
+                          ffn_activation=ACTIVATION[ffn_activation],
+                          smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
+                          weights_dtype=0, max_batch=max_batch, device=device)
+        handle = ctypes.c_void_p()
+        self._h = None
+        _check(lib().mfh_net_create(ctypes.byref(desc), tensors, len(names),
+                                    ctypes.byref(handle)), "mfh_net_create")
+        self._h = handle
+        self.wdl = wdl
+        self.max_batch = max_batch
+        # Host weights are only needed for the upload.
+        self._weights = None
+
+    def close(self):
+        if self._h:
+            lib().mfh_net_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self) -> str:
+        buf = ctypes.create_string_buffer(1024)
+        _check(lib().mfh_net_info(self._h, buf, len(buf)), "mfh_net_info")
+        return buf.value.decode()
+
+    def capabilities(self) -> dict:
+        c = MfhCapabilities()
+        _check(lib().mfh_net_capabilities(self._h, ctypes.byref(c)), "mfh_net_capabilities")
+        return {"actual_backend": "hip", "has_wdl": bool(c.has_wdl),
+                "has_moves_left": bool(c.has_moves_left), "max_batch_size": c.max_batch_size,
+                "device": c.device, "device_name": c.device_name.decode(),
+                "arch": c.arch_name.decode(), "weight_bytes": c.weight_bytes,
+                "workspace_bytes": c.workspace_bytes}
+
+    def _outputs(self, b):
+        return (np.zeros((b, 1858), np.float32),
+                np.zeros((b, 3 if self.wdl else 1), np.float32))
+
+    def eval_packed(self, masks, values):
+        """Raw outputs (policy [B,1858], wdl [B,3] or value [B,1]) for packed
+        inputs, chunked by max_batch."""
+        masks = np.ascontiguousarray(masks, dtype=np.uint64).reshape(-1, 112)
+        values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1, 112)
+        b = masks.shape[0]
+        policy, value = self._outputs(b)
+        for s in range(0, b, self.max_batch):
+            e = min(b, s + self.max_batch)
+            _check(lib().mfh_net_eval(self._h, e - s, _ptr(masks[s:e]), _ptr(values[s:e]),
+                                      _ptr(policy[s:e]), _ptr(value[s:e]), None),
+                   "mfh_net_eval")
+        return policy, value
+
+    def eval_planes(self, planes):
+        planes = np.ascontiguousarray(planes, dtype=np.float32).reshape(-1, 112, 64)
+        b = planes.shape[0]
+        policy, value = self._outputs(b)
+        for s in range(0, b, self.max_batch):
+            e = min(b, s + self.max_batch)
+            _check(lib().mfh_net_eval_planes(self._h, e - s, _ptr(planes[s:e]),
+                                             _ptr(policy[s:e]), _ptr(value[s:e]), None),
+                   "mfh_net_eval_planes")
+        return policy, value
+
+    def evaluate_batch(self, planes):
+        """NetworkOutput fields for planes [B,112,64] (EvaluateBatch)."""
+        policy, raw = self.eval_planes(planes)
+        if self.wdl:
+            return {"policy": policy, "wdl": raw, "value": raw[:, 0] - raw[:, 2]}
+        return {"policy": policy, "wdl": np.zeros((raw.shape[0], 3), np.float32),
+                "value": raw[:, 0]}
+
+    def evaluate(self, planes):
+        out = self.evaluate_batch(np.asarray(planes).reshape(1, 112, 64))
+        return {k: v[0] for k, v in out.items()}
+
+    def eval_device(self, batch, d_masks, d_values, d_policy, d_wdl, stream=None):
+        """Device-resident forward (pointers are device addresses)."""
+        _check(lib().mfh_net_eval_device(self._h, batch, d_masks, d_values, d_policy, d_wdl,
+                                         stream), "mfh_net_eval_device")
+
+    def debug_tensor(self, name, shape, dtype):
+        out = np.zeros(shape, dtype=dtype)
+        _check(lib().mfh_net_debug_tensor(self._h, name.encode(), out.ctypes.data, out.nbytes),
+               "mfh_net_debug_tensor")
+        return out
+
+
+def unpack_planes(masks, values):
+    masks = np.ascontiguousarray(masks, dtype=np.uint64).reshape(-1, 112)
+    values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1, 112)
+    out = np.zeros((masks.shape[0], 112, 64), np.float32)
+    _check(lib().mfh_debug_unpack_planes(masks.shape[0], _ptr(masks), _ptr(values), _ptr(out)),
+           "mfh_debug_unpack_planes")
+    return out
+
+
+def gemm_bf16(a_bits, w_bits, bias=None, act="none"):
+    a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
+    w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    m, k = a_bits.shape
+    n = w_bits.shape[0]
+    out = np.zeros((m, n), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(lib().mfh_debug_gemm_bf16(m, n, k, _ptr(a_bits), _ptr(w_bits), _ptr(b),
+                                     ACTIVATION[act], _ptr(out)), "mfh_debug_gemm_bf16")
+    return out
+
+
+def create_network(spec, weights, max_batch=256, device=-1):
+    """HipNetwork for a synth.NetSpec and its weights."""
+    return HipNetwork(weights, spec.heads, wdl=spec.wdl,
+                      default_activation=spec.default_activation,
+                      ffn_activation=spec.ffn_activation,
+                      smolgen_activation=spec.smolgen_activation, max_batch=max_batch,
+                      device=device)

@@ -1,0 +1,1020 @@
+// C ABI of libmfhip.so (include/mfhip.h): shape inference, weight packing,
+// device arenas and the per-batch launch sequence of the transformer
+// forward pass on one MI355X.
+//
+// The launch sequence restates the step order of the reference CPU backend
+// for attention-body nets (reference src/nn/network_execution_plan.cpp:
+// 94-223 and src/nn/cpu/cpu_network.cpp:580-1491) with these fusions:
+//   * Q, K, V and the smolgen compression are one GEMM (one read of X);
+//   * the policy "output" dense and the value "output" dense share one GEMM;
+//   * the policy query and key denses (both fed by "output", reference
+//     cpu_network.cpp:570-573, 871-875) are one GEMM;
+//   * bias, activations and the scaled residual add run in GEMM epilogues,
+//     the input gates in the LayerNorm kernel.
+#include "../../../include/mfhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../host/policy_tables.h"
+#include "mfh_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int SetError(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+#define MFH_HIP_CHECK(expr)                                                    \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess)                                                      \
+      return SetError(MFH_ERR_HIP, std::string(#expr) + ": " +                 \
+                                       hipGetErrorString(e_));                 \
+  } while (0)
+
+constexpr int kSquares = 64;
+constexpr int kPlanes = 112;
+constexpr int kPolicy = 1858;
+
+std::uint16_t ToBf16(float f) {
+  std::uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<std::uint16_t>(u >> 16);
+}
+
+int ActFromProto(int proto_act, int default_act) {
+  switch (proto_act) {
+  case MFH_ACTIVATION_DEFAULT: return default_act;
+  case MFH_ACTIVATION_MISH: return mfh::ACT_MISH;
+  case MFH_ACTIVATION_RELU: return mfh::ACT_RELU;
+  case MFH_ACTIVATION_NONE: return mfh::ACT_NONE;
+  case MFH_ACTIVATION_TANH: return mfh::ACT_TANH;
+  case MFH_ACTIVATION_SIGMOID: return mfh::ACT_SIGMOID;
+  case MFH_ACTIVATION_SELU: return mfh::ACT_SELU;
+  case MFH_ACTIVATION_SWISH: return mfh::ACT_SWISH;
+  case MFH_ACTIVATION_RELU_2: return mfh::ACT_RELU2;
+  default: return mfh::ACT_RELU;
+  }
+}
+
+const char *ActName(int act) {
+  switch (act) {
+  case mfh::ACT_NONE: return "none";
+  case mfh::ACT_RELU: return "relu";
+  case mfh::ACT_RELU2: return "relu_2";
+  case mfh::ACT_TANH: return "tanh";
+  case mfh::ACT_SIGMOID: return "sigmoid";
+  case mfh::ACT_SWISH: return "swish";
+  case mfh::ACT_MISH: return "mish";
+  case mfh::ACT_SELU: return "selu";
+  default: return "?";
+  }
+}
+
+size_t AlignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Host-side staging of the packed weight blob before one upload.
+struct Blob {
+  std::vector<unsigned char> bytes;
+  size_t Add(const void *src, size_t n) {
+    const size_t off = AlignUp(bytes.size(), 256);
+    bytes.resize(off + n);
+    if (src)
+      std::memcpy(bytes.data() + off, src, n);
+    return off;
+  }
+};
+
+struct Layer {
+  size_t qkv_w, qkv_b, out_w, out_b, ln1_g, ln1_b, ffn1_w, ffn1_b, ffn2_w, ffn2_b,
+      ln2_g, ln2_b;
+  bool smolgen = false;
+  size_t sg_d1_w, sg_d1_b, sg_ln1_g, sg_ln1_b, sg_d2_w, sg_d2_b, sg_ln2_g, sg_ln2_b;
+};
+
+struct Dims {
+  int E = 0, H = 0, L = 0, F = 0, P = 0, Kin = 0, Fi = 0;
+  int C = 0, Hs = 0, HG = 0, G = 0;
+  int Dp = 0, Vd = 0, Vh = 0, Vout = 0;
+  bool gates = false, input_ffn = false, smolgen = false, wdl = true;
+  int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
+  float alpha = 1.f, eps_body = 1e-3f;
+};
+
+}  // namespace
+
+struct mfh_net {
+  std::mutex mu;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  Dims d;
+  int max_batch = 0;
+  std::string arch, device_name;
+
+  unsigned char *weights = nullptr;
+  size_t weight_bytes = 0;
+  // Offsets into `weights`.
+  size_t pre_w, pre_b, emb_w, emb_b, emb_ln_g, emb_ln_b, mult_gate, add_gate;
+  size_t in_ffn1_w, in_ffn1_b, in_ffn2_w, in_ffn2_b, in_ln_g, in_ln_b;
+  size_t global_w;
+  std::vector<Layer> layers;
+  size_t head_w, head_b, qk_w, qk_b, promo, val1_w, val1_b, val2_w, val2_b, gather;
+
+  unsigned char *ws = nullptr;
+  size_t ws_bytes = 0;
+  std::map<std::string, size_t> ws_off;
+
+  unsigned char *pin_in = nullptr;   // masks | values
+  unsigned char *pin_out = nullptr;  // policy | value
+  int last_batch = 0;
+
+  template <typename T> T *W(size_t off) const {
+    return reinterpret_cast<T *>(weights + off);
+  }
+  template <typename T> T *S(const char *name) const {
+    return reinterpret_cast<T *>(ws + ws_off.at(name));
+  }
+};
+
+namespace {
+
+struct TensorMap {
+  std::map<std::string, const mfh_tensor *> by_name;
+  const mfh_tensor *Get(const std::string &n) const {
+    auto it = by_name.find(n);
+    return it == by_name.end() ? nullptr : it->second;
+  }
+};
+
+// Reads a tensor of the given size; *ok cleared with a message if absent or
+// mis-sized.
+struct Loader {
+  const TensorMap &tm;
+  std::string error;
+  const float *Need(const std::string &name, size_t count) {
+    const mfh_tensor *t = tm.Get(name);
+    if (!t) {
+      if (error.empty())
+        error = "missing tensor " + name;
+      return nullptr;
+    }
+    if (t->count != count || !t->data) {
+      if (error.empty()) {
+        std::ostringstream o;
+        o << "tensor " << name << " has " << t->count << " values, expected " << count;
+        error = o.str();
+      }
+      return nullptr;
+    }
+    return t->data;
+  }
+  size_t Count(const std::string &name) const {
+    const mfh_tensor *t = tm.Get(name);
+    return t ? static_cast<size_t>(t->count) : 0;
+  }
+};
+
+// Appends rows x cols fp32 (row-major) as bf16 padded to ld columns.
+size_t AddBf16(Blob &blob, const std::vector<const float *> &parts,
+               const std::vector<int> &part_rows, int cols, int ld) {
+  size_t rows = 0;
+  for (int r : part_rows)
+    rows += r;
+  std::vector<std::uint16_t> buf(rows * ld, 0);
+  size_t row = 0;
+  for (size_t p = 0; p < parts.size(); ++p) {
+    for (int r = 0; r < part_rows[p]; ++r, ++row)
+      for (int c = 0; c < cols; ++c)
+        buf[row * ld + c] = parts[p] ? ToBf16(parts[p][static_cast<size_t>(r) * cols + c]) : 0;
+  }
+  return blob.Add(buf.data(), buf.size() * 2);
+}
+
+size_t AddF32(Blob &blob, const std::vector<const float *> &parts,
+              const std::vector<int> &counts) {
+  std::vector<float> buf;
+  for (size_t p = 0; p < parts.size(); ++p)
+    for (int i = 0; i < counts[p]; ++i)
+      buf.push_back(parts[p] ? parts[p][i] : 0.f);
+  return blob.Add(buf.data(), buf.size() * 4);
+}
+
+int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
+  if (desc.network != MFH_NETWORK_ATTENTIONBODY_WITH_HEADFORMAT &&
+      desc.network != MFH_NETWORK_ATTENTIONBODY_WITH_MULTIHEADFORMAT)
+    return SetError(MFH_ERR_UNSUPPORTED, "HIP backend supports attention-body nets only");
+  if (desc.policy != MFH_POLICY_ATTENTION)
+    return SetError(MFH_ERR_UNSUPPORTED, "HIP backend supports the attention policy head only");
+  if (desc.value != MFH_VALUE_WDL && desc.value != MFH_VALUE_CLASSICAL)
+    return SetError(MFH_ERR_UNSUPPORTED, "HIP backend supports WDL or classical value heads");
+  if (desc.moves_left)
+    return SetError(MFH_ERR_UNSUPPORTED, "HIP backend has no moves-left head yet");
+  if (desc.input_embedding != MFH_INPUT_EMBEDDING_PE_DENSE)
+    return SetError(MFH_ERR_UNSUPPORTED,
+                    "HIP backend supports INPUT_EMBEDDING_PE_DENSE only (as the reference CPU backend)");
+  if (desc.weights_dtype != MFH_WEIGHTS_BF16)
+    return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
+  d.wdl = desc.value == MFH_VALUE_WDL;
+  d.act_default = desc.default_activation == MFH_DEFAULT_ACTIVATION_MISH ? mfh::ACT_MISH
+                                                                         : mfh::ACT_RELU;
+  d.act_ffn = ActFromProto(desc.ffn_activation, d.act_default);
+  d.act_smolgen = ActFromProto(desc.smolgen_activation, d.act_default);
+
+  // Shapes follow from bias sizes, as in the reference's shape inference
+  // (network_execution_plan.cpp:279-289).
+  d.E = static_cast<int>(ld.Count("body.ip_emb_b"));
+  d.P = static_cast<int>(ld.Count("body.ip_emb_preproc_b")) / kSquares;
+  d.H = desc.headcount;
+  while (ld.Count("body.encoder." + std::to_string(d.L) + ".mha.q_b"))
+    ++d.L;
+  d.F = d.L ? static_cast<int>(ld.Count("body.encoder.0.ffn.dense1_b")) : 0;
+  d.Fi = static_cast<int>(ld.Count("body.ip_emb_ffn.dense1_b"));
+  d.input_ffn = d.Fi > 0;
+  d.gates = ld.Count("body.ip_mult_gate") || ld.Count("body.ip_add_gate");
+  d.C = d.L ? static_cast<int>(ld.Count("body.encoder.0.mha.smolgen.compress")) /
+                  (d.E ? d.E : 1)
+            : 0;
+  d.smolgen = d.C > 0;
+  if (d.smolgen) {
+    d.Hs = static_cast<int>(ld.Count("body.encoder.0.mha.smolgen.dense1_b"));
+    d.HG = static_cast<int>(ld.Count("body.encoder.0.mha.smolgen.dense2_b"));
+    d.G = d.H ? d.HG / d.H : 0;
+  }
+  d.Dp = static_cast<int>(ld.Count("policy.vanilla.ip2_pol_b"));
+  d.Vd = static_cast<int>(ld.Count("value.winner.ip_val_b"));
+  d.Vh = static_cast<int>(ld.Count("value.winner.ip1_val_b"));
+  d.Vout = static_cast<int>(ld.Count("value.winner.ip2_val_b"));
+  d.Kin = static_cast<int>(AlignUp(kPlanes + d.P, 64));
+
+  std::ostringstream why;
+  if (d.E <= 0 || d.P <= 0)
+    why << "missing input embedding (body.ip_emb_*, body.ip_emb_preproc_*); ";
+  if (d.E % 64)
+    why << "embedding width " << d.E << " is not a multiple of 64; ";
+  if (d.H <= 0 || d.E != d.H * 32)
+    why << "head depth must be 32 (embedding " << d.E << ", heads " << d.H << "); ";
+  if (d.H % 4)
+    why << "head count must be a multiple of 4; ";
+  if (d.L && d.F % 64)
+    why << "FFN width must be a multiple of 64; ";
+  if (d.input_ffn && d.Fi % 64)
+    why << "input FFN width must be a multiple of 64; ";
+  if (d.smolgen && (d.Hs % 64 || d.G % 64 || d.HG != d.G * d.H || d.C % 8))
+    why << "smolgen widths must be multiples of 64 with dense2 = heads x gen; ";
+  if (d.Dp <= 0 || d.Dp % 64)
+    why << "policy width must be a positive multiple of 64; ";
+  if (d.Vd <= 0 || d.Vh <= 0 || d.Vout != (d.wdl ? 3 : 1))
+    why << "value head needs ip_val, ip1_val and ip2_val with " << (d.wdl ? 3 : 1)
+        << " outputs; ";
+  if (!ld.Count("body.ip_emb_ln_gammas"))
+    why << "body.ip_emb_ln is required; ";
+  if (ld.Count("policy.vanilla.encoder.0.mha.q_b") || ld.Count("policy.vanilla.ip_pol_b") == 0)
+    why << "policy head must be ip_pol/ip2_pol/ip3_pol/ip4_pol without encoder layers; ";
+  if (ld.Count("value.winner.ip_val_err_b"))
+    why << "value-error head is not supported; ";
+  const std::string w = why.str();
+  if (!w.empty())
+    return SetError(MFH_ERR_UNSUPPORTED, "HIP backend cannot run this net: " + w);
+  const int n_layers = d.L;
+  d.alpha = std::pow(2.0f * static_cast<float>(n_layers), -0.25f);
+  if (n_layers == 0)
+    d.alpha = 1.0f;
+  d.eps_body = 1e-3f;  // PE_DENSE nets (network_execution_plan.cpp:1164-1193)
+  return MFH_OK;
+}
+
+int Pack(mfh_net *net, Loader &ld, Blob &blob) {
+  const Dims &d = net->d;
+  const int E = d.E, S = kSquares;
+  auto need = [&](const std::string &n, size_t c) { return ld.Need(n, c); };
+  const float *pre_w = need("body.ip_emb_preproc_w", static_cast<size_t>(S) * d.P * S * 12);
+  const float *pre_b = need("body.ip_emb_preproc_b", static_cast<size_t>(S) * d.P);
+  const float *emb_w = need("body.ip_emb_w", static_cast<size_t>(E) * (kPlanes + d.P));
+  const float *emb_b = need("body.ip_emb_b", E);
+  const float *ln_g = need("body.ip_emb_ln_gammas", E);
+  const float *ln_b = need("body.ip_emb_ln_betas", E);
+  if (!ld.error.empty())
+    return SetError(MFH_ERR_INVALID, ld.error);
+  net->pre_w = AddBf16(blob, {pre_w}, {S * d.P}, S * 12, S * 12);
+  net->pre_b = AddF32(blob, {pre_b}, {S * d.P});
+  net->emb_w = AddBf16(blob, {emb_w}, {E}, kPlanes + d.P, d.Kin);
+  net->emb_b = AddF32(blob, {emb_b}, {E});
+  net->emb_ln_g = AddF32(blob, {ln_g}, {E});
+  net->emb_ln_b = AddF32(blob, {ln_b}, {E});
+  net->mult_gate = net->add_gate = 0;
+  if (ld.Count("body.ip_mult_gate")) {
+    const float *g = need("body.ip_mult_gate", static_cast<size_t>(E) * S);
+    if (g)
+      net->mult_gate = AddF32(blob, {g}, {E * S});
+  }
+  if (ld.Count("body.ip_add_gate")) {
+    const float *g = need("body.ip_add_gate", static_cast<size_t>(E) * S);
+    if (g)
+      net->add_gate = AddF32(blob, {g}, {E * S});
+  }
+  if (d.input_ffn) {
+    const float *w1 = need("body.ip_emb_ffn.dense1_w", static_cast<size_t>(d.Fi) * E);
+    const float *b1 = need("body.ip_emb_ffn.dense1_b", d.Fi);
+    const float *w2 = need("body.ip_emb_ffn.dense2_w", static_cast<size_t>(E) * d.Fi);
+    const float *b2 = need("body.ip_emb_ffn.dense2_b", E);
+    const float *g = need("body.ip_emb_ffn_ln_gammas", E);
+    const float *b = need("body.ip_emb_ffn_ln_betas", E);
+    if (!ld.error.empty())
+      return SetError(MFH_ERR_INVALID, ld.error);
+    net->in_ffn1_w = AddBf16(blob, {w1}, {d.Fi}, E, E);
+    net->in_ffn1_b = AddF32(blob, {b1}, {d.Fi});
+    net->in_ffn2_w = AddBf16(blob, {w2}, {E}, d.Fi, d.Fi);
+    net->in_ffn2_b = AddF32(blob, {b2}, {E});
+    net->in_ln_g = AddF32(blob, {g}, {E});
+    net->in_ln_b = AddF32(blob, {b}, {E});
+  }
+  if (d.smolgen) {
+    const float *g = need("body.smolgen_w", static_cast<size_t>(S) * S * d.G);
+    if (!g)
+      return SetError(MFH_ERR_INVALID, ld.error);
+    net->global_w = AddBf16(blob, {g}, {S * S}, d.G, d.G);
+  }
+  net->layers.resize(d.L);
+  for (int i = 0; i < d.L; ++i) {
+    const std::string p = "body.encoder." + std::to_string(i);
+    Layer &L = net->layers[i];
+    const size_t EE = static_cast<size_t>(E) * E;
+    const float *qw = need(p + ".mha.q_w", EE), *qb = need(p + ".mha.q_b", E);
+    const float *kw = need(p + ".mha.k_w", EE), *kb = need(p + ".mha.k_b", E);
+    const float *vw = need(p + ".mha.v_w", EE), *vb = need(p + ".mha.v_b", E);
+    const float *ow = need(p + ".mha.dense_w", EE), *ob = need(p + ".mha.dense_b", E);
+    const float *l1g = need(p + ".ln1_gammas", E), *l1b = need(p + ".ln1_betas", E);
+    const float *f1w = need(p + ".ffn.dense1_w", static_cast<size_t>(d.F) * E);
+    const float *f1b = need(p + ".ffn.dense1_b", d.F);
+    const float *f2w = need(p + ".ffn.dense2_w", static_cast<size_t>(E) * d.F);
+    const float *f2b = need(p + ".ffn.dense2_b", E);
+    const float *l2g = need(p + ".ln2_gammas", E), *l2b = need(p + ".ln2_betas", E);
+    const float *cw = nullptr;
+    if (d.smolgen)
+      cw = need(p + ".mha.smolgen.compress", static_cast<size_t>(d.C) * E);
+    if (!ld.error.empty())
+      return SetError(MFH_ERR_INVALID, ld.error);
+    L.qkv_w = AddBf16(blob, {qw, kw, vw, cw}, {E, E, E, d.smolgen ? d.C : 0}, E, E);
+    L.qkv_b = AddF32(blob, {qb, kb, vb, nullptr}, {E, E, E, d.smolgen ? d.C : 0});
+    L.out_w = AddBf16(blob, {ow}, {E}, E, E);
+    L.out_b = AddF32(blob, {ob}, {E});
+    L.ln1_g = AddF32(blob, {l1g}, {E});
+    L.ln1_b = AddF32(blob, {l1b}, {E});
+    L.ffn1_w = AddBf16(blob, {f1w}, {d.F}, E, E);
+    L.ffn1_b = AddF32(blob, {f1b}, {d.F});
+    L.ffn2_w = AddBf16(blob, {f2w}, {E}, d.F, d.F);
+    L.ffn2_b = AddF32(blob, {f2b}, {E});
+    L.ln2_g = AddF32(blob, {l2g}, {E});
+    L.ln2_b = AddF32(blob, {l2b}, {E});
+    L.smolgen = d.smolgen;
+    if (d.smolgen) {
+      const std::string s = p + ".mha.smolgen";
+      const float *d1w = need(s + ".dense1_w", static_cast<size_t>(d.Hs) * S * d.C);
+      const float *d1b = need(s + ".dense1_b", d.Hs);
+      const float *d2w = need(s + ".dense2_w", static_cast<size_t>(d.HG) * d.Hs);
+      const float *d2b = need(s + ".dense2_b", d.HG);
+      const float *g1 = need(s + ".ln1_gammas", d.Hs), *b1 = need(s + ".ln1_betas", d.Hs);
+      const float *g2 = need(s + ".ln2_gammas", d.HG), *b2 = need(s + ".ln2_betas", d.HG);
+      if (!ld.error.empty())
+        return SetError(MFH_ERR_INVALID, ld.error);
+      L.sg_d1_w = AddBf16(blob, {d1w}, {d.Hs}, S * d.C, S * d.C);
+      L.sg_d1_b = AddF32(blob, {d1b}, {d.Hs});
+      L.sg_ln1_g = AddF32(blob, {g1}, {d.Hs});
+      L.sg_ln1_b = AddF32(blob, {b1}, {d.Hs});
+      L.sg_d2_w = AddBf16(blob, {d2w}, {d.HG}, d.Hs, d.Hs);
+      L.sg_d2_b = AddF32(blob, {d2b}, {d.HG});
+      L.sg_ln2_g = AddF32(blob, {g2}, {d.HG});
+      L.sg_ln2_b = AddF32(blob, {b2}, {d.HG});
+    }
+  }
+  const std::string pp = "policy.vanilla.", vp = "value.winner.";
+  const float *pw = need(pp + "ip_pol_w", static_cast<size_t>(d.Dp) * E);
+  const float *pb = need(pp + "ip_pol_b", d.Dp);
+  const float *vw = need(vp + "ip_val_w", static_cast<size_t>(d.Vd) * E);
+  const float *vb = need(vp + "ip_val_b", d.Vd);
+  const float *q2w = need(pp + "ip2_pol_w", static_cast<size_t>(d.Dp) * d.Dp);
+  const float *q2b = need(pp + "ip2_pol_b", d.Dp);
+  const float *k3w = need(pp + "ip3_pol_w", static_cast<size_t>(d.Dp) * d.Dp);
+  const float *k3b = need(pp + "ip3_pol_b", d.Dp);
+  const float *p4 = need(pp + "ip4_pol_w", static_cast<size_t>(4) * d.Dp);
+  const float *v1w = need(vp + "ip1_val_w", static_cast<size_t>(d.Vh) * S * d.Vd);
+  const float *v1b = need(vp + "ip1_val_b", d.Vh);
+  const float *v2w = need(vp + "ip2_val_w", static_cast<size_t>(d.Vout) * d.Vh);
+  const float *v2b = need(vp + "ip2_val_b", d.Vout);
+  if (!ld.error.empty())
+    return SetError(MFH_ERR_INVALID, ld.error);
+  net->head_w = AddBf16(blob, {pw, vw}, {d.Dp, d.Vd}, E, E);
+  net->head_b = AddF32(blob, {pb, vb}, {d.Dp, d.Vd});
+  net->qk_w = AddBf16(blob, {q2w, k3w}, {d.Dp, d.Dp}, d.Dp, d.Dp);
+  net->qk_b = AddF32(blob, {q2b, k3b}, {d.Dp, d.Dp});
+  net->promo = AddF32(blob, {p4}, {4 * d.Dp});
+  net->val1_w = AddBf16(blob, {v1w}, {d.Vh}, S * d.Vd, S * d.Vd);
+  net->val1_b = AddF32(blob, {v1b}, {d.Vh});
+  net->val2_w = AddF32(blob, {v2w}, {d.Vout * d.Vh});
+  net->val2_b = AddF32(blob, {v2b}, {d.Vout});
+  const auto &gather = mfh_policy::AttentionGather();
+  net->gather = blob.Add(gather.data(), gather.size() * sizeof(std::int16_t));
+  return MFH_OK;
+}
+
+void PlanWorkspace(mfh_net *net) {
+  const Dims &d = net->d;
+  const size_t B = static_cast<size_t>(net->max_batch);
+  const size_t M = B * kSquares;
+  size_t off = 0;
+  auto add = [&](const char *name, size_t bytes) {
+    off = AlignUp(off, 256);
+    net->ws_off[name] = off;
+    off += bytes;
+  };
+  add("masks", B * kPlanes * 8);
+  add("values", B * kPlanes * 4);
+  add("emb_in", M * d.Kin * 2);
+  add("pos_in", B * kSquares * 12 * 2);
+  add("pe", B * kSquares * d.P * 4);
+  add("pre", M * d.E * 4);
+  add("resid", M * d.E * 4);
+  add("act", M * d.E * 2);
+  add("qkv", M * 3 * d.E * 2);
+  add("comp", M * (d.C ? d.C : 1) * 2);
+  add("sg1", B * (d.Hs ? d.Hs : 1) * 4);
+  add("sg1n", B * (d.Hs ? d.Hs : 1) * 2);
+  add("sg2", B * (d.HG ? d.HG : 1) * 4);
+  add("sg2n", B * (d.HG ? d.HG : 1) * 2);
+  add("bias", d.smolgen ? B * d.H * kSquares * kSquares * 2 : 256);
+  add("ctx", M * d.E * 2);
+  const int hid = d.F > d.Fi ? d.F : d.Fi;
+  add("hid", M * (hid ? hid : 1) * 2);
+  add("pol_emb", M * d.Dp * 2);
+  add("val_emb", M * d.Vd * 2);
+  add("polqk", M * 2 * d.Dp * 2);
+  add("val1", B * d.Vh * 4);
+  add("policy", B * kPolicy * 4);
+  add("wdl", B * 3 * 4);
+  net->ws_bytes = AlignUp(off, 256);
+}
+
+int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
+            float *policy, float *wdl, hipStream_t st) {
+  const Dims &d = net->d;
+  const int M = B * kSquares;
+  const int E = d.E;
+  std::string err_;
+  auto gemm = [&](const std::uint16_t *A, int lda, size_t w_off, int ldw, int m, int n, int k,
+                  const float *bias, int act, int mode, void *C, int ldc) {
+    mfh::GemmParams p;
+    p.A = A;
+    p.lda = lda;
+    p.W = net->W<std::uint16_t>(w_off);
+    p.ldw = ldw;
+    p.M = m;
+    p.N = n;
+    p.K = k;
+    p.bias = bias;
+    p.act = act;
+    p.out_mode = mode;
+    p.C = C;
+    p.ldc = ldc;
+    return p;
+  };
+  auto run = [&](const mfh::GemmParams &p) { return mfh::LaunchGemm(p, st, &err_); };
+  auto fail = [&](hipError_t e) {
+    return SetError(e == hipErrorInvalidValue ? MFH_ERR_INVALID : MFH_ERR_HIP,
+                    err_.empty() ? std::string(hipGetErrorString(e)) : err_);
+  };
+#define MFH_RUN(expr)                                                          \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess)                                                      \
+      return fail(e_);                                                         \
+  } while (0)
+
+  auto *emb_in = net->S<std::uint16_t>("emb_in");
+  auto *pos_in = net->S<std::uint16_t>("pos_in");
+  auto *pe = net->S<float>("pe");
+  auto *pre = net->S<float>("pre");
+  auto *resid = net->S<float>("resid");
+  auto *act = net->S<std::uint16_t>("act");
+  auto *qkv = net->S<std::uint16_t>("qkv");
+  auto *comp = net->S<std::uint16_t>("comp");
+  auto *sg1 = net->S<float>("sg1");
+  auto *sg1n = net->S<std::uint16_t>("sg1n");
+  auto *sg2 = net->S<float>("sg2");
+  auto *sg2n = net->S<std::uint16_t>("sg2n");
+  auto *bias = net->S<std::uint16_t>("bias");
+  auto *ctx = net->S<std::uint16_t>("ctx");
+  auto *hid = net->S<std::uint16_t>("hid");
+  auto *pol_emb = net->S<std::uint16_t>("pol_emb");
+  auto *val_emb = net->S<std::uint16_t>("val_emb");
+  auto *polqk = net->S<std::uint16_t>("polqk");
+  auto *val1 = net->S<float>("val1");
+
+  // Input planes, dynamic positional encoding, embedding (cpu_network.cpp:
+  // 691-890), embedding LayerNorm + gates (1399-1457, 1268-1316).
+  MFH_RUN(mfh::LaunchExpandInputs(masks, values, B, emb_in, d.Kin, pos_in, st, &err_));
+  MFH_RUN(run(gemm(pos_in, kSquares * 12, net->pre_w, kSquares * 12, B, kSquares * d.P,
+                   kSquares * 12, net->W<float>(net->pre_b), mfh::ACT_NONE, mfh::GEMM_OUT_F32,
+                   pe, kSquares * d.P)));
+  MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, emb_in, d.Kin, st, &err_));
+  MFH_RUN(run(gemm(emb_in, d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
+                   d.act_default, mfh::GEMM_OUT_F32, pre, E)));
+  MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, 1e-3f, net->W<float>(net->emb_ln_g),
+                               net->W<float>(net->emb_ln_b),
+                               net->mult_gate ? net->W<float>(net->mult_gate) : nullptr,
+                               net->add_gate ? net->W<float>(net->add_gate) : nullptr, resid,
+                               act, st, &err_));
+  if (d.input_ffn) {
+    MFH_RUN(run(gemm(act, E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
+                     d.act_ffn, mfh::GEMM_OUT_BF16, hid, d.Fi)));
+    mfh::GemmParams p = gemm(hid, d.Fi, net->in_ffn2_w, d.Fi, M, E, d.Fi,
+                             net->W<float>(net->in_ffn2_b), mfh::ACT_NONE,
+                             mfh::GEMM_OUT_RESID_F32, pre, E);
+    p.resid = resid;
+    p.ldr = E;
+    p.alpha = d.alpha;
+    MFH_RUN(run(p));
+    MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
+                                 net->W<float>(net->in_ln_b), nullptr, nullptr, resid, act, st,
+                                 &err_));
+  }
+
+  // Encoder layers (cpu_network.cpp:1027-1266, 1318-1457).
+  for (const Layer &L : net->layers) {
+    mfh::GemmParams p = gemm(act, E, L.qkv_w, E, M, 3 * E + (L.smolgen ? d.C : 0), E,
+                             net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16, qkv,
+                             3 * E);
+    if (L.smolgen) {
+      p.split_n = 3 * E;
+      p.C2 = comp;
+      p.ldc2 = d.C;
+    }
+    MFH_RUN(run(p));
+    const std::uint16_t *bias_ptr = nullptr;
+    if (L.smolgen) {
+      const int flat = kSquares * d.C;
+      MFH_RUN(run(gemm(comp, flat, L.sg_d1_w, flat, B, d.Hs, flat,
+                       net->W<float>(L.sg_d1_b), d.act_smolgen, mfh::GEMM_OUT_F32, sg1,
+                       d.Hs)));
+      MFH_RUN(mfh::LaunchLayerNorm(sg1, B, d.Hs, 1e-3f, net->W<float>(L.sg_ln1_g),
+                                   net->W<float>(L.sg_ln1_b), nullptr, nullptr, nullptr, sg1n,
+                                   st, &err_));
+      MFH_RUN(run(gemm(sg1n, d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs,
+                       net->W<float>(L.sg_d2_b), d.act_smolgen, mfh::GEMM_OUT_F32, sg2,
+                       d.HG)));
+      MFH_RUN(mfh::LaunchLayerNorm(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
+                                   net->W<float>(L.sg_ln2_b), nullptr, nullptr, nullptr, sg2n,
+                                   st, &err_));
+      MFH_RUN(run(gemm(sg2n, d.G, net->global_w, d.G, B * d.H, kSquares * kSquares, d.G,
+                       nullptr, mfh::ACT_NONE, mfh::GEMM_OUT_BF16, bias,
+                       kSquares * kSquares)));
+      bias_ptr = bias;
+    }
+    MFH_RUN(mfh::LaunchAttention(qkv, bias_ptr, B, d.H, ctx, st, &err_));
+    mfh::GemmParams po = gemm(ctx, E, L.out_w, E, M, E, E, net->W<float>(L.out_b),
+                              mfh::ACT_NONE, mfh::GEMM_OUT_RESID_F32, pre, E);
+    po.resid = resid;
+    po.ldr = E;
+    po.alpha = d.alpha;
+    MFH_RUN(run(po));
+    MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, d.eps_body, net->W<float>(L.ln1_g),
+                                 net->W<float>(L.ln1_b), nullptr, nullptr, resid, act, st,
+                                 &err_));
+    MFH_RUN(run(gemm(act, E, L.ffn1_w, E, M, d.F, E, net->W<float>(L.ffn1_b), d.act_ffn,
+                     mfh::GEMM_OUT_BF16, hid, d.F)));
+    mfh::GemmParams pf = gemm(hid, d.F, L.ffn2_w, d.F, M, E, d.F, net->W<float>(L.ffn2_b),
+                              mfh::ACT_NONE, mfh::GEMM_OUT_RESID_F32, pre, E);
+    pf.resid = resid;
+    pf.ldr = E;
+    pf.alpha = d.alpha;
+    MFH_RUN(run(pf));
+    MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, d.eps_body, net->W<float>(L.ln2_g),
+                                 net->W<float>(L.ln2_b), nullptr, nullptr, resid, act, st,
+                                 &err_));
+  }
+
+  // Heads: policy "output" | value "output" (default activation), policy
+  // Q | K, attention policy map, value dense1 (flattened squares) and dense2.
+  mfh::GemmParams ph = gemm(act, E, net->head_w, E, M, d.Dp + d.Vd, E,
+                            net->W<float>(net->head_b), d.act_default, mfh::GEMM_OUT_BF16,
+                            pol_emb, d.Dp);
+  ph.split_n = d.Dp;
+  ph.C2 = val_emb;
+  ph.ldc2 = d.Vd;
+  MFH_RUN(run(ph));
+  MFH_RUN(run(gemm(pol_emb, d.Dp, net->qk_w, d.Dp, M, 2 * d.Dp, d.Dp,
+                   net->W<float>(net->qk_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16, polqk,
+                   2 * d.Dp)));
+  MFH_RUN(mfh::LaunchPolicyMap(polqk, B, d.Dp, net->W<float>(net->promo),
+                               net->W<std::int16_t>(net->gather), policy, st, &err_));
+  const int vflat = kSquares * d.Vd;
+  MFH_RUN(run(gemm(val_emb, vflat, net->val1_w, vflat, B, d.Vh, vflat,
+                   net->W<float>(net->val1_b), d.act_default, mfh::GEMM_OUT_F32, val1, d.Vh)));
+  MFH_RUN(mfh::LaunchValueHead(val1, B, d.Vh, net->W<float>(net->val2_w),
+                               net->W<float>(net->val2_b), d.wdl ? 1 : 0, wdl, st, &err_));
+#undef MFH_RUN
+  return MFH_OK;
+}
+
+void PackPlanes(const float *planes, int batch, std::uint64_t *masks, float *values) {
+  // PackInputPlanesRaw (reference src/nn/input_plane_packing.h:30-83).
+  for (int b = 0; b < batch; ++b)
+    for (int p = 0; p < kPlanes; ++p) {
+      const float *plane = planes + (static_cast<size_t>(b) * kPlanes + p) * kSquares;
+      const size_t idx = static_cast<size_t>(b) * kPlanes + p;
+      const bool uniform = (p < 104 && p % 13 == 12) || p == 106 || p == 107 || p >= 109;
+      if (uniform) {
+        values[idx] = plane[0];
+        masks[idx] = plane[0] != 0.0f ? ~0ULL : 0ULL;
+        continue;
+      }
+      std::uint64_t mask = 0;
+      float value = 0.0f;
+      for (int sq = 0; sq < kSquares; ++sq) {
+        const float v = plane[sq];
+        if (v != 0.0f) {
+          if (mask == 0)
+            value = v;
+          mask |= 1ULL << sq;
+        }
+      }
+      masks[idx] = mask;
+      values[idx] = value;
+    }
+}
+
+int CheckBatch(const mfh_net *net, int batch) {
+  if (!net)
+    return SetError(MFH_ERR_INVALID, "null net");
+  if (batch < 1 || batch > net->max_batch) {
+    std::ostringstream o;
+    o << "batch " << batch << " outside 1.." << net->max_batch;
+    return SetError(MFH_ERR_INVALID, o.str());
+  }
+  return MFH_OK;
+}
+
+// Runs the staged batch in pin_in through the device and leaves outputs in
+// pin_out.  Caller holds net->mu.
+int RunStaged(mfh_net *net, int batch) {
+  const size_t n_in = static_cast<size_t>(batch) * kPlanes;
+  auto *pin_masks = reinterpret_cast<std::uint64_t *>(net->pin_in);
+  auto *pin_values =
+      reinterpret_cast<float *>(net->pin_in + static_cast<size_t>(net->max_batch) * kPlanes * 8);
+  auto *d_masks = net->S<std::uint64_t>("masks");
+  auto *d_values = net->S<float>("values");
+  auto *d_policy = net->S<float>("policy");
+  auto *d_wdl = net->S<float>("wdl");
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  MFH_HIP_CHECK(hipMemcpyAsync(d_masks, pin_masks, n_in * 8, hipMemcpyHostToDevice, net->stream));
+  MFH_HIP_CHECK(hipMemcpyAsync(d_values, pin_values, n_in * 4, hipMemcpyHostToDevice, net->stream));
+  const int rc = Forward(net, batch, d_masks, d_values, d_policy, d_wdl, net->stream);
+  if (rc != MFH_OK) {
+    (void)hipStreamSynchronize(net->stream);
+    return rc;
+  }
+  auto *pin_policy = reinterpret_cast<float *>(net->pin_out);
+  auto *pin_value = pin_policy + static_cast<size_t>(net->max_batch) * kPolicy;
+  MFH_HIP_CHECK(hipMemcpyAsync(pin_policy, d_policy, static_cast<size_t>(batch) * kPolicy * 4,
+                               hipMemcpyDeviceToHost, net->stream));
+  MFH_HIP_CHECK(hipMemcpyAsync(pin_value, d_wdl, static_cast<size_t>(batch) * net->d.Vout * 4,
+                               hipMemcpyDeviceToHost, net->stream));
+  MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
+  net->last_batch = batch;
+  return MFH_OK;
+}
+
+int CopyOut(mfh_net *net, int batch, float *policy, float *wdl) {
+  const auto *pin_policy = reinterpret_cast<const float *>(net->pin_out);
+  const auto *pin_value = pin_policy + static_cast<size_t>(net->max_batch) * kPolicy;
+  if (policy)
+    std::memcpy(policy, pin_policy, static_cast<size_t>(batch) * kPolicy * 4);
+  if (wdl)
+    std::memcpy(wdl, pin_value, static_cast<size_t>(batch) * net->d.Vout * 4);
+  return MFH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mfh_last_error(void) { return g_last_error.c_str(); }
+
+int mfh_device_count(int *count) {
+  if (!count)
+    return SetError(MFH_ERR_INVALID, "null count");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess)
+    n = 0;
+  *count = n;
+  return MFH_OK;
+}
+
+int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_tensors,
+                   mfh_net **out) {
+  if (!desc || !out || (n_tensors > 0 && !tensors) || n_tensors < 0)
+    return SetError(MFH_ERR_INVALID, "mfh_net_create: null argument");
+  *out = nullptr;
+  if (desc->max_batch < 1)
+    return SetError(MFH_ERR_INVALID, "max_batch must be >= 1");
+  TensorMap tm;
+  for (int i = 0; i < n_tensors; ++i) {
+    if (!tensors[i].name)
+      return SetError(MFH_ERR_INVALID, "tensor without a name");
+    tm.by_name[tensors[i].name] = &tensors[i];
+  }
+  Loader ld{tm, {}};
+  Dims dims;
+  int rc = Infer(*desc, ld, dims);
+  if (rc != MFH_OK)
+    return rc;
+
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  int dev = desc->device;
+  if (dev < 0)
+    MFH_HIP_CHECK(hipGetDevice(&dev));
+  if (dev >= ndev)
+    return SetError(MFH_ERR_NO_DEVICE, "device ordinal out of range");
+  hipDeviceProp_t prop;
+  MFH_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+  const std::string arch = prop.gcnArchName;
+  if (arch.rfind("gfx950", 0) != 0)
+    return SetError(MFH_ERR_NO_DEVICE, "device " + arch + " is not gfx950 (MI355X)");
+
+  auto net = std::make_unique<mfh_net>();
+  net->device = dev;
+  net->d = dims;
+  net->max_batch = desc->max_batch;
+  net->arch = arch;
+  net->device_name = prop.name;
+  Blob blob;
+  rc = Pack(net.get(), ld, blob);
+  if (rc != MFH_OK)
+    return rc;
+  PlanWorkspace(net.get());
+
+  MFH_HIP_CHECK(hipSetDevice(dev));
+  net->weight_bytes = blob.bytes.size();
+  if (hipMalloc(&net->weights, net->weight_bytes) != hipSuccess)
+    return SetError(MFH_ERR_OUT_OF_MEMORY, "weight upload allocation failed");
+  mfh_net *raw = net.get();
+  auto cleanup = [raw]() {
+    if (raw->weights) (void)hipFree(raw->weights);
+    if (raw->ws) (void)hipFree(raw->ws);
+    if (raw->pin_in) (void)hipHostFree(raw->pin_in);
+    if (raw->pin_out) (void)hipHostFree(raw->pin_out);
+    if (raw->stream) (void)hipStreamDestroy(raw->stream);
+    raw->weights = raw->ws = raw->pin_in = raw->pin_out = nullptr;
+    raw->stream = nullptr;
+  };
+  if (hipMemcpy(net->weights, blob.bytes.data(), net->weight_bytes, hipMemcpyHostToDevice) !=
+      hipSuccess) {
+    cleanup();
+    return SetError(MFH_ERR_HIP, "weight upload failed");
+  }
+  if (hipMalloc(&net->ws, net->ws_bytes) != hipSuccess) {
+    cleanup();
+    return SetError(MFH_ERR_OUT_OF_MEMORY, "workspace allocation failed");
+  }
+  const size_t in_bytes = static_cast<size_t>(net->max_batch) * kPlanes * 12;
+  const size_t out_bytes = static_cast<size_t>(net->max_batch) * (kPolicy + 3) * 4;
+  if (hipHostMalloc(reinterpret_cast<void **>(&net->pin_in), in_bytes, hipHostMallocDefault) !=
+          hipSuccess ||
+      hipHostMalloc(reinterpret_cast<void **>(&net->pin_out), out_bytes,
+                    hipHostMallocDefault) != hipSuccess) {
+    cleanup();
+    return SetError(MFH_ERR_OUT_OF_MEMORY, "pinned staging allocation failed");
+  }
+  if (hipStreamCreateWithFlags(&net->stream, hipStreamNonBlocking) != hipSuccess) {
+    cleanup();
+    return SetError(MFH_ERR_HIP, "stream creation failed");
+  }
+  *out = net.release();
+  return MFH_OK;
+}
+
+void mfh_net_destroy(mfh_net *net) {
+  if (!net)
+    return;
+  (void)hipSetDevice(net->device);
+  if (net->stream) {
+    (void)hipStreamSynchronize(net->stream);
+    (void)hipStreamDestroy(net->stream);
+  }
+  if (net->weights) (void)hipFree(net->weights);
+  if (net->ws) (void)hipFree(net->ws);
+  if (net->pin_in) (void)hipHostFree(net->pin_in);
+  if (net->pin_out) (void)hipHostFree(net->pin_out);
+  delete net;
+}
+
+int mfh_net_eval(mfh_net *net, int batch, const uint64_t *masks, const float *values,
+                 float *policy, float *wdl, float *moves_left) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (!masks || !values || !policy || !wdl || moves_left)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval: bad output/input pointers");
+  std::lock_guard<std::mutex> lock(net->mu);
+  const size_t n_in = static_cast<size_t>(batch) * kPlanes;
+  std::memcpy(net->pin_in, masks, n_in * 8);
+  std::memcpy(net->pin_in + static_cast<size_t>(net->max_batch) * kPlanes * 8, values, n_in * 4);
+  rc = RunStaged(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  return CopyOut(net, batch, policy, wdl);
+}
+
+int mfh_net_eval_planes(mfh_net *net, int batch, const float *planes, float *policy,
+                        float *wdl, float *moves_left) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (!planes || !policy || !wdl || moves_left)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_planes: bad output/input pointers");
+  std::lock_guard<std::mutex> lock(net->mu);
+  PackPlanes(planes, batch, reinterpret_cast<std::uint64_t *>(net->pin_in),
+             reinterpret_cast<float *>(net->pin_in +
+                                       static_cast<size_t>(net->max_batch) * kPlanes * 8));
+  rc = RunStaged(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  return CopyOut(net, batch, policy, wdl);
+}
+
+int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
+                        const float *d_values, float *d_policy, float *d_wdl, void *stream) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (!d_masks || !d_values || !d_policy || !d_wdl)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_device: null pointer");
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = Forward(net, batch, d_masks, d_values, d_policy, d_wdl, st);
+  if (rc == MFH_OK)
+    net->last_batch = batch;
+  return rc;
+}
+
+int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
+  if (!net || !buf || !len)
+    return SetError(MFH_ERR_INVALID, "mfh_net_info: null argument");
+  const Dims &d = net->d;
+  std::ostringstream o;
+  o << "HIP transformer backend (" << net->arch << ", " << net->device_name
+    << "): attention body E=" << d.E << " L=" << d.L << " H=" << d.H << " FFN=" << d.F
+    << " PE=" << d.P << (d.gates ? " gates" : "") << (d.input_ffn ? " input-ffn" : "");
+  if (d.smolgen)
+    o << " smolgen C=" << d.C << "/" << d.Hs << "/" << d.G;
+  o << ", policy attention Dp=" << d.Dp << ", value " << (d.wdl ? "wdl" : "scalar") << " "
+    << d.Vd << "/" << d.Vh << ", activations " << ActName(d.act_default) << "/"
+    << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", weights bf16 "
+    << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
+    << net->max_batch;
+  const std::string s = o.str();
+  std::snprintf(buf, len, "%s", s.c_str());
+  return MFH_OK;
+}
+
+int mfh_net_capabilities(const mfh_net *net, mfh_capabilities *out) {
+  if (!net || !out)
+    return SetError(MFH_ERR_INVALID, "mfh_net_capabilities: null argument");
+  std::memset(out, 0, sizeof(*out));
+  out->has_wdl = net->d.wdl ? 1 : 0;
+  out->has_moves_left = 0;
+  out->max_batch_size = net->max_batch;
+  out->device = net->device;
+  std::snprintf(out->device_name, sizeof(out->device_name), "%s", net->device_name.c_str());
+  std::snprintf(out->arch_name, sizeof(out->arch_name), "%s", net->arch.c_str());
+  out->weight_bytes = net->weight_bytes;
+  out->workspace_bytes = net->ws_bytes;
+  return MFH_OK;
+}
+
+int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t bytes) {
+  if (!net || !name || !out)
+    return SetError(MFH_ERR_INVALID, "mfh_net_debug_tensor: null argument");
+  std::lock_guard<std::mutex> lock(net->mu);
+  const size_t B = static_cast<size_t>(net->last_batch);
+  const Dims &d = net->d;
+  const char *ws_name = nullptr;
+  size_t size = 0;
+  const std::string n = name;
+  if (n == "body") {
+    ws_name = "resid";
+    size = B * kSquares * d.E * 4;
+  } else if (n == "policy_qk") {
+    ws_name = "polqk";
+    size = B * kSquares * 2 * d.Dp * 2;
+  } else if (n == "value_hidden") {
+    ws_name = "val1";
+    size = B * d.Vh * 4;
+  } else {
+    return SetError(MFH_ERR_INVALID, "unknown debug tensor " + n);
+  }
+  if (B == 0 || bytes != size)
+    return SetError(MFH_ERR_INVALID, "debug tensor size mismatch");
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
+  MFH_HIP_CHECK(hipMemcpy(out, net->ws + net->ws_off.at(ws_name), size, hipMemcpyDeviceToHost));
+  return MFH_OK;
+}
+
+int mfh_debug_unpack_planes(int batch, const uint64_t *masks, const float *values,
+                            float *planes) {
+  if (batch <= 0 || !masks || !values || !planes)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_unpack_planes: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  const size_t n = static_cast<size_t>(batch) * kPlanes;
+  const size_t np = n * kSquares;
+  std::uint64_t *dm = nullptr;
+  float *dv = nullptr, *dp = nullptr;
+  MFH_HIP_CHECK(hipMalloc(&dm, n * 8));
+  MFH_HIP_CHECK(hipMalloc(&dv, n * 4));
+  MFH_HIP_CHECK(hipMalloc(&dp, np * 4));
+  int rc = MFH_OK;
+  std::string err;
+  if (hipMemcpy(dm, masks, n * 8, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dv, values, n * 4, hipMemcpyHostToDevice) != hipSuccess)
+    rc = SetError(MFH_ERR_HIP, "copy failed");
+  else if (mfh::LaunchUnpackPlanes(dm, dv, batch, dp, nullptr, &err) != hipSuccess)
+    rc = SetError(MFH_ERR_HIP, err);
+  else if (hipMemcpy(planes, dp, np * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = SetError(MFH_ERR_HIP, "copy back failed");
+  (void)hipFree(dm);
+  (void)hipFree(dv);
+  (void)hipFree(dp);
+  return rc;
+}
+
+int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A, const uint16_t *W,
+                        const float *bias, int act, float *C) {
+  if (M <= 0 || N <= 0 || K <= 0 || !A || !W || !C)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_gemm_bf16: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  std::uint16_t *dA = nullptr, *dW = nullptr;
+  float *dB = nullptr, *dC = nullptr;
+  const size_t na = static_cast<size_t>(M) * K, nw = static_cast<size_t>(N) * K,
+               nc = static_cast<size_t>(M) * N;
+  MFH_HIP_CHECK(hipMalloc(&dA, na * 2));
+  MFH_HIP_CHECK(hipMalloc(&dW, nw * 2));
+  MFH_HIP_CHECK(hipMalloc(&dC, nc * 4));
+  if (bias)
+    MFH_HIP_CHECK(hipMalloc(&dB, static_cast<size_t>(N) * 4));
+  int rc = MFH_OK;
+  std::string err;
+  mfh::GemmParams p;
+  p.A = dA;
+  p.lda = K;
+  p.W = dW;
+  p.ldw = K;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.bias = dB;
+  p.act = ActFromProto(act, mfh::ACT_RELU);
+  if (act == MFH_ACTIVATION_NONE || act == MFH_ACTIVATION_DEFAULT)
+    p.act = mfh::ACT_NONE;
+  p.out_mode = mfh::GEMM_OUT_F32;
+  p.C = dC;
+  p.ldc = N;
+  if (hipMemcpy(dA, A, na * 2, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dW, W, nw * 2, hipMemcpyHostToDevice) != hipSuccess ||
+      (bias && hipMemcpy(dB, bias, static_cast<size_t>(N) * 4, hipMemcpyHostToDevice) !=
+                   hipSuccess))
+    rc = SetError(MFH_ERR_HIP, "copy failed");
+  else if (mfh::LaunchGemm(p, nullptr, &err) != hipSuccess)
+    rc = SetError(MFH_ERR_INVALID, err);
+  else if (hipDeviceSynchronize() != hipSuccess ||
+           hipMemcpy(C, dC, nc * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    rc = SetError(MFH_ERR_HIP, "gemm execution failed");
+  (void)hipFree(dA);
+  (void)hipFree(dW);
+  (void)hipFree(dC);
+  if (dB)
+    (void)hipFree(dB);
+  return rc;
+}
+
+}  // extern "C"

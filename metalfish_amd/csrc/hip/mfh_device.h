@@ -1,0 +1,79 @@
+// Shared device-side definitions for the gfx950 kernels of libmfhip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "mfh_kernels.h"
+
+namespace mfh {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(std::uint16_t h) {
+  return __uint_as_float(static_cast<std::uint32_t>(h) << 16);
+}
+
+// Round to nearest even (inputs here are finite).
+__device__ __forceinline__ std::uint16_t f32_to_bf16(float f) {
+  std::uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<std::uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ std::uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<std::uint32_t>(f32_to_bf16(lo)) |
+         (static_cast<std::uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Activations (reference src/nn/cpu/cpu_network.cpp:302-323).  Mish uses the
+// identity tanh(log1p(e^x)) = n / (n + 2) with n = e^x (e^x + 2), which needs
+// one exponential; for x > 20 the ratio is 1 to fp32 precision.
+__device__ __forceinline__ float activate(float x, int act) {
+  switch (act) {
+  case ACT_RELU:
+    return x > 0.f ? x : 0.f;
+  case ACT_RELU2: {
+    const float r = x > 0.f ? x : 0.f;
+    return r * r;
+  }
+  case ACT_TANH:
+    return tanhf(x);
+  case ACT_SIGMOID:
+    return 1.f / (1.f + __expf(-x));
+  case ACT_SWISH:
+    return x / (1.f + __expf(-x));
+  case ACT_MISH: {
+    if (x > 20.f)
+      return x;
+    const float e = __expf(x);
+    const float n = e * (e + 2.f);
+    return x * __fdividef(n, n + 2.f);
+  }
+  case ACT_SELU:
+    return 1.05070098f * (x > 0.f ? x : 1.67326324f * (__expf(x) - 1.f));
+  default:
+    return x;
+  }
+}
+
+// Wave-wide (64 lanes) reductions.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+    v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+    v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace mfh

@@ -1,0 +1,110 @@
+// Host-side launch wrappers for the gfx950 kernels of libmfhip.  Every
+// wrapper validates the shapes and alignment its kernel and grid assume
+// before launching, and returns hipErrorInvalidValue with a message in *err
+// when they do not hold.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace mfh {
+
+// Activation ids used by kernel epilogues (the C ABI maps the
+// reference's ActivationFunction values onto these).
+enum Act : int {
+  ACT_NONE = -1,
+  ACT_RELU = 0,
+  ACT_RELU2 = 1,
+  ACT_TANH = 2,
+  ACT_SIGMOID = 3,
+  ACT_SWISH = 4,
+  ACT_MISH = 5,
+  ACT_SELU = 6,
+};
+
+
+enum GemmOut : int {
+  GEMM_OUT_BF16 = 0,       // C = act(A.W^T + b) as bf16
+  GEMM_OUT_F32 = 1,        // C = act(A.W^T + b) as fp32
+  GEMM_OUT_RESID_F32 = 2,  // C = resid + alpha * (A.W^T + b) as fp32
+};
+
+// C[M,N] = A[M,K] . W[N,K]^T with bf16 operands and fp32 accumulation.
+// Columns >= split_n are written to C2 (column index minus split_n) so one
+// launch can fill two tensors that share an input (e.g. Q|K|V and the
+// smolgen compression).
+struct GemmParams {
+  const std::uint16_t *A = nullptr;
+  int lda = 0;
+  const std::uint16_t *W = nullptr;
+  int ldw = 0;
+  int M = 0, N = 0, K = 0;
+  const float *bias = nullptr;
+  int act = -1;
+  int out_mode = GEMM_OUT_BF16;
+  void *C = nullptr;
+  int ldc = 0;
+  void *C2 = nullptr;
+  int ldc2 = 0;
+  int split_n = 1 << 30;
+  const float *resid = nullptr;
+  int ldr = 0;
+  float alpha = 1.0f;
+};
+
+hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
+
+// Packed planes -> embedding input rows and the dynamic-PE input.
+//   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values, rest zero (the PE
+//   columns are filled by LaunchScatterPe).
+//   pos_in [B, 64*12] bf16: square-major first 12 planes.
+hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
+                              int batch, std::uint16_t *emb_in, int emb_ld,
+                              std::uint16_t *pos_in, hipStream_t stream,
+                              std::string *err);
+
+// Debug view: packed planes -> fp32 planes [B,112,64].
+hipError_t LaunchUnpackPlanes(const std::uint64_t *masks, const float *values,
+                              int batch, float *planes, hipStream_t stream,
+                              std::string *err);
+
+// pe [B, 64*P] fp32 -> emb_in[b*64+sq][112 + c] (bf16).
+hipError_t LaunchScatterPe(const float *pe, int batch, int pe_channels,
+                           std::uint16_t *emb_in, int emb_ld,
+                           hipStream_t stream, std::string *err);
+
+// Row LayerNorm: y = (x - mean) * rstd * gamma + beta with the reference's
+// E[x^2] - mean^2 variance (cpu_network.cpp:424-460), optionally followed by
+// the input gates y = y * mult[c][sq] + add[c][sq] (cpu_network.cpp:
+// 1268-1316, gate layout [width][64], sq = row % 64).  Writes fp32 and/or
+// bf16 copies.
+hipError_t LaunchLayerNorm(const float *x, int rows, int width, float eps,
+                           const float *gamma, const float *beta,
+                           const float *mult_gate, const float *add_gate,
+                           float *y_f32, std::uint16_t *y_bf16,
+                           hipStream_t stream, std::string *err);
+
+// Multi-head 64x64 attention per (position, head), head depth 32:
+//   ctx = softmax(Q K^T / sqrt(32) + bias) V
+// qkv [B*64, 3E] bf16 (Q | K | V, head h at columns h*32..), bias [B,H,64,64]
+// bf16 or null, ctx [B*64, E] bf16.
+hipError_t LaunchAttention(const std::uint16_t *qkv, const std::uint16_t *bias,
+                           int batch, int heads, std::uint16_t *ctx,
+                           hipStream_t stream, std::string *err);
+
+// Attention policy map: raw[q,k] = Q_q.K_k / sqrt(Dp), the 8x24 promotion
+// logits, and the 1858-entry gather (cpu_network.cpp:892-1025).
+// qk [B*64, 2*Dp] bf16 (Q | K), promo [4, Dp] fp32, policy [B, 1858] fp32.
+hipError_t LaunchPolicyMap(const std::uint16_t *qk, int batch, int dp,
+                           const float *promo, const std::int16_t *gather,
+                           float *policy, hipStream_t stream, std::string *err);
+
+// Value head output: hidden [B, vh] fp32 -> dense2 + softmax (WDL, 3 outputs)
+// or tanh (scalar, 1 output).
+hipError_t LaunchValueHead(const float *hidden, int batch, int vh,
+                           const float *w2, const float *b2, int wdl,
+                           float *out, hipStream_t stream, std::string *err);
+
+}  // namespace mfh

@@ -1,0 +1,100 @@
+// Attention policy head for gfx950: the 64x64 query-key logits, the 8x24
+// promotion logits and the gather into the 1858-move policy
+// (reference src/nn/cpu/cpu_network.cpp:892-1025, gather table 91-103).
+//
+// One workgroup per position.  Wave w computes query rows 16w..16w+15 of
+// raw = Q K^T / sqrt(Dp) with v_mfma_f32_16x16x32_bf16 straight from global
+// memory (Q and K rows are K-contiguous); the 64x64 fp32 block goes to LDS.
+// The promotion logit for p in [0,192) is, as in the reference,
+//   raw[48 + (p%64)/8][56 + (p%64)%8] + K[56 + (p%24)/3] . (promo[p%3] + promo[3]).
+// The 24 promotion-offset dot products are formed once per position.
+#include "mfh_device.h"
+#include "mfh_kernels.h"
+
+namespace mfh {
+namespace {
+
+constexpr int kSq = 64;
+constexpr int kOutputs = 1858;
+
+__global__ __launch_bounds__(256) void PolicyMapKernel(
+    const std::uint16_t *__restrict__ qk, int dp, float scale,
+    const float *__restrict__ promo, const std::int16_t *__restrict__ gather,
+    float *__restrict__ policy) {
+  __shared__ float raw[kSq * kSq];
+  __shared__ float pk_term[24];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int b = blockIdx.x;
+  const size_t ld = static_cast<size_t>(2) * dp;
+  const std::uint16_t *base = qk + static_cast<size_t>(b) * kSq * ld;
+  const int fr = lane & 15, fc = (lane >> 4) * 8;
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const std::uint16_t *qrow = base + (wave * 16 + fr) * ld + fc;
+  for (int k0 = 0; k0 < dp; k0 += 32) {
+    const bf16x8 a = *reinterpret_cast<const bf16x8 *>(qrow + k0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8 kb =
+          *reinterpret_cast<const bf16x8 *>(base + (j * 16 + fr) * ld + dp + fc + k0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kb, acc[j], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      raw[(wave * 16 + (lane >> 4) * 4 + r) * kSq + j * 16 + fr] = acc[j][r] * scale;
+
+  // Promotion offsets: term[t][tf] = K[56+tf] . (promo[t] + promo[3]),
+  // six dot products per wave.
+  for (int d = wave; d < 24; d += 4) {
+    const int t = d / 8, tf = d % 8;
+    const std::uint16_t *krow = base + (56 + tf) * ld + dp;
+    float s = 0.f;
+    for (int c = lane; c < dp; c += 64)
+      s += bf16_to_f32(krow[c]) *
+           (promo[static_cast<size_t>(t) * dp + c] + promo[static_cast<size_t>(3) * dp + c]);
+    s = wave_sum(s);
+    if (lane == 0)
+      pk_term[t * 8 + tf] = s;
+  }
+  __syncthreads();
+
+  float *out = policy + static_cast<size_t>(b) * kOutputs;
+  for (int i = threadIdx.x; i < kOutputs; i += 256) {
+    const int r = gather[i];
+    float v = 0.f;
+    if (r >= 0 && r < kSq * kSq) {
+      v = raw[r];
+    } else if (r >= kSq * kSq) {
+      const int p = r - kSq * kSq;
+      const int pair = p % kSq;
+      v = raw[(48 + pair / 8) * kSq + 56 + pair % 8] + pk_term[(p % 3) * 8 + (p % 24) / 3];
+    }
+    out[i] = v;
+  }
+}
+
+}  // namespace
+
+hipError_t LaunchPolicyMap(const std::uint16_t *qk, int batch, int dp, const float *promo,
+                           const std::int16_t *gather, float *policy, hipStream_t stream,
+                           std::string *err) {
+  if (batch <= 0 || dp <= 0 || dp % 32 || !qk || !promo || !gather || !policy ||
+      (reinterpret_cast<std::uintptr_t>(qk) & 15u)) {
+    if (err)
+      *err = "policy_map: needs batch > 0, Dp % 32 == 0 and 16-byte aligned Q|K";
+    return hipErrorInvalidValue;
+  }
+  const float scale = 1.0f / sqrtf(static_cast<float>(dp));
+  hipLaunchKernelGGL(PolicyMapKernel, dim3(batch), dim3(256), 0, stream, qk, dp, scale,
+                     promo, gather, policy);
+  return hipGetLastError();
+}
+
+}  // namespace mfh

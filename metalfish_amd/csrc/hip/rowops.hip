@@ -1,0 +1,235 @@
+// Memory-bound row kernels: input plane expansion, LayerNorm (+ input gates)
+// and the WDL value head.
+#include "mfh_device.h"
+#include "mfh_kernels.h"
+
+namespace mfh {
+namespace {
+
+constexpr int kPlanes = 112;
+constexpr int kSquares = 64;
+constexpr int kPePlanes = 12;
+
+// One thread per (position, square, 8-column chunk) of the embedding input,
+// plus the square-major 12-plane PE input.  Unpacking follows the packed
+// plane contract of reference src/nn/input_plane_packing.h:30-58: square sq
+// of plane p holds values[p] when bit sq of masks[p] is set, else 0
+// (cpu_network.cpp:711-731, 777-790).
+__global__ void ExpandInputsKernel(const std::uint64_t *__restrict__ masks,
+                                   const float *__restrict__ values, int batch,
+                                   std::uint16_t *__restrict__ emb_in, int emb_ld,
+                                   std::uint16_t *__restrict__ pos_in) {
+  const int chunks = emb_ld / 8;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int total = batch * kSquares * chunks;
+  if (idx < total) {
+    const int chunk = idx % chunks;
+    const int row = idx / chunks;
+    const int b = row / kSquares, sq = row % kSquares;
+    std::uint16_t out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int col = chunk * 8 + e;
+      float v = 0.f;
+      if (col < kPlanes) {
+        const std::uint64_t m = masks[static_cast<size_t>(b) * kPlanes + col];
+        v = ((m >> sq) & 1ull) ? values[static_cast<size_t>(b) * kPlanes + col] : 0.f;
+      }
+      out[e] = f32_to_bf16(v);
+    }
+    uint4 packed;
+    packed.x = out[0] | (static_cast<std::uint32_t>(out[1]) << 16);
+    packed.y = out[2] | (static_cast<std::uint32_t>(out[3]) << 16);
+    packed.z = out[4] | (static_cast<std::uint32_t>(out[5]) << 16);
+    packed.w = out[6] | (static_cast<std::uint32_t>(out[7]) << 16);
+    *reinterpret_cast<uint4 *>(emb_in + static_cast<size_t>(row) * emb_ld + chunk * 8) =
+        packed;
+  }
+  // PE input: [b][sq*12 + p] for p < 12.
+  const int pos_total = batch * kSquares * kPePlanes;
+  if (idx < pos_total) {
+    const int p = idx % kPePlanes;
+    const int sq = (idx / kPePlanes) % kSquares;
+    const int b = idx / (kPePlanes * kSquares);
+    const std::uint64_t m = masks[static_cast<size_t>(b) * kPlanes + p];
+    const float v = ((m >> sq) & 1ull) ? values[static_cast<size_t>(b) * kPlanes + p] : 0.f;
+    pos_in[idx] = f32_to_bf16(v);
+  }
+}
+
+__global__ void UnpackPlanesKernel(const std::uint64_t *__restrict__ masks,
+                                   const float *__restrict__ values, int batch,
+                                   float *__restrict__ planes) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= batch * kPlanes * kSquares)
+    return;
+  const int sq = idx % kSquares;
+  const int bp = idx / kSquares;
+  const std::uint64_t m = masks[bp];
+  planes[idx] = ((m >> sq) & 1ull) ? values[bp] : 0.f;
+}
+
+__global__ void ScatterPeKernel(const float *__restrict__ pe, int batch, int pe_ch,
+                                std::uint16_t *__restrict__ emb_in, int emb_ld) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= batch * kSquares * pe_ch)
+    return;
+  const int c = idx % pe_ch;
+  const int row = idx / pe_ch;  // b*64 + sq, and pe is [b][sq*pe_ch + c]
+  emb_in[static_cast<size_t>(row) * emb_ld + kPlanes + c] = f32_to_bf16(pe[idx]);
+}
+
+// One wave per row.  Statistics in fp32 with the reference formula
+// var = E[x^2] - mean^2 clamped at 0, inv_std = 1 / sqrt(var + eps).
+__global__ __launch_bounds__(256) void LayerNormKernel(
+    const float *__restrict__ x, int rows, int width, float eps,
+    const float *__restrict__ gamma, const float *__restrict__ beta,
+    const float *__restrict__ mult, const float *__restrict__ add,
+    float *__restrict__ y32, std::uint16_t *__restrict__ y16) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows)
+    return;
+  const float *xr = x + static_cast<size_t>(row) * width;
+  float s = 0.f, ss = 0.f;
+  for (int c = lane; c < width; c += 64) {
+    const float v = xr[c];
+    s += v;
+    ss += v * v;
+  }
+  s = wave_sum(s);
+  ss = wave_sum(ss);
+  const float mean = s / static_cast<float>(width);
+  float var = ss / static_cast<float>(width) - mean * mean;
+  var = var < 0.f ? 0.f : var;
+  const float inv_std = 1.f / sqrtf(var + eps);
+  const int sq = row % kSquares;
+  for (int c = lane; c < width; c += 64) {
+    float v = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
+    if (mult)
+      v = v * mult[static_cast<size_t>(c) * kSquares + sq];
+    if (add)
+      v = v + add[static_cast<size_t>(c) * kSquares + sq];
+    if (y32)
+      y32[static_cast<size_t>(row) * width + c] = v;
+    if (y16)
+      y16[static_cast<size_t>(row) * width + c] = f32_to_bf16(v);
+  }
+}
+
+// One wave per position: dense2 (vh -> 3 or 1) then softmax or tanh
+// (reference network_execution_plan.cpp:1098-1106, cpu_network.cpp:336-351).
+__global__ __launch_bounds__(256) void ValueHeadKernel(
+    const float *__restrict__ hidden, int batch, int vh,
+    const float *__restrict__ w2, const float *__restrict__ b2, int wdl,
+    float *__restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= batch)
+    return;
+  const int outs = wdl ? 3 : 1;
+  const float *h = hidden + static_cast<size_t>(b) * vh;
+  float acc[3] = {0.f, 0.f, 0.f};
+  for (int c = lane; c < vh; c += 64) {
+    const float v = h[c];
+    for (int o = 0; o < outs; ++o)
+      acc[o] += v * w2[static_cast<size_t>(o) * vh + c];
+  }
+  for (int o = 0; o < outs; ++o)
+    acc[o] = wave_sum(acc[o]) + b2[o];
+  if (lane != 0)
+    return;
+  if (wdl) {
+    const float m = fmaxf(acc[0], fmaxf(acc[1], acc[2]));
+    const float e0 = expf(acc[0] - m), e1 = expf(acc[1] - m), e2 = expf(acc[2] - m);
+    const float inv = 1.f / (e0 + e1 + e2);
+    out[static_cast<size_t>(b) * 3 + 0] = e0 * inv;
+    out[static_cast<size_t>(b) * 3 + 1] = e1 * inv;
+    out[static_cast<size_t>(b) * 3 + 2] = e2 * inv;
+  } else {
+    out[b] = tanhf(acc[0]);
+  }
+}
+
+std::string Fail(std::string *err, const char *what) {
+  if (err)
+    *err = what;
+  return what;
+}
+
+}  // namespace
+
+hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
+                              int batch, std::uint16_t *emb_in, int emb_ld,
+                              std::uint16_t *pos_in, hipStream_t stream,
+                              std::string *err) {
+  if (batch <= 0 || emb_ld % 8 || emb_ld < kPlanes || !masks || !values || !emb_in ||
+      !pos_in || (reinterpret_cast<std::uintptr_t>(emb_in) & 15u)) {
+    Fail(err, "expand_inputs: invalid arguments");
+    return hipErrorInvalidValue;
+  }
+  const int total = batch * kSquares * (emb_ld / 8);
+  const int pos_total = batch * kSquares * kPePlanes;
+  const int n = total > pos_total ? total : pos_total;
+  hipLaunchKernelGGL(ExpandInputsKernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                     masks, values, batch, emb_in, emb_ld, pos_in);
+  return hipGetLastError();
+}
+
+hipError_t LaunchUnpackPlanes(const std::uint64_t *masks, const float *values,
+                              int batch, float *planes, hipStream_t stream,
+                              std::string *err) {
+  if (batch <= 0 || !masks || !values || !planes) {
+    Fail(err, "unpack_planes: invalid arguments");
+    return hipErrorInvalidValue;
+  }
+  const int n = batch * kPlanes * kSquares;
+  hipLaunchKernelGGL(UnpackPlanesKernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                     masks, values, batch, planes);
+  return hipGetLastError();
+}
+
+hipError_t LaunchScatterPe(const float *pe, int batch, int pe_channels,
+                           std::uint16_t *emb_in, int emb_ld, hipStream_t stream,
+                           std::string *err) {
+  if (batch <= 0 || pe_channels <= 0 || kPlanes + pe_channels > emb_ld || !pe || !emb_in) {
+    Fail(err, "scatter_pe: invalid arguments");
+    return hipErrorInvalidValue;
+  }
+  const int n = batch * kSquares * pe_channels;
+  hipLaunchKernelGGL(ScatterPeKernel, dim3((n + 255) / 256), dim3(256), 0, stream, pe,
+                     batch, pe_channels, emb_in, emb_ld);
+  return hipGetLastError();
+}
+
+hipError_t LaunchLayerNorm(const float *x, int rows, int width, float eps,
+                           const float *gamma, const float *beta,
+                           const float *mult_gate, const float *add_gate,
+                           float *y_f32, std::uint16_t *y_bf16, hipStream_t stream,
+                           std::string *err) {
+  if (rows <= 0 || width <= 0 || !x || !gamma || !beta || (!y_f32 && !y_bf16)) {
+    Fail(err, "layernorm: invalid arguments");
+    return hipErrorInvalidValue;
+  }
+  if ((mult_gate || add_gate) && rows % kSquares) {
+    Fail(err, "layernorm: gates need square rows");
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(LayerNormKernel, dim3((rows + 3) / 4), dim3(256), 0, stream, x, rows,
+                     width, eps, gamma, beta, mult_gate, add_gate, y_f32, y_bf16);
+  return hipGetLastError();
+}
+
+hipError_t LaunchValueHead(const float *hidden, int batch, int vh, const float *w2,
+                           const float *b2, int wdl, float *out, hipStream_t stream,
+                           std::string *err) {
+  if (batch <= 0 || vh <= 0 || !hidden || !w2 || !b2 || !out) {
+    Fail(err, "value_head: invalid arguments");
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(ValueHeadKernel, dim3((batch + 3) / 4), dim3(256), 0, stream, hidden,
+                     batch, vh, w2, b2, wdl, out);
+  return hipGetLastError();
+}
+
+}  // namespace mfh

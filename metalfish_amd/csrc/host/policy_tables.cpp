@@ -1,0 +1,86 @@
+#include "policy_tables.h"
+
+namespace mfh_policy {
+namespace {
+
+bool QueenLine(int from, int to) {
+  const int df = (to & 7) - (from & 7), dr = (to >> 3) - (from >> 3);
+  if (from == to)
+    return false;
+  return df == 0 || dr == 0 || df == dr || df == -dr;
+}
+
+bool KnightJump(int from, int to) {
+  int df = (to & 7) - (from & 7), dr = (to >> 3) - (from >> 3);
+  df = df < 0 ? -df : df;
+  dr = dr < 0 ? -dr : dr;
+  return (df == 1 && dr == 2) || (df == 2 && dr == 1);
+}
+
+struct Built {
+  std::array<PolicyMove, kPolicyOutputs> moves{};
+  std::array<std::int16_t, kAttentionRaw> attention{};
+  std::array<std::int16_t, kPolicyOutputs> gather{};
+  std::array<std::int16_t, 64 * 64> regular{};      // from*64+to -> index
+  std::array<std::int16_t, 8 * 8 * 3> promotion{};  // ff*24+tf*3+p -> index
+  Built() {
+    regular.fill(-1);
+    promotion.fill(-1);
+    int n = 0;
+    for (int from = 0; from < 64; ++from)
+      for (int to = 0; to < 64; ++to)
+        if (QueenLine(from, to) || KnightJump(from, to)) {
+          regular[from * 64 + to] = static_cast<std::int16_t>(n);
+          moves[n++] = PolicyMove{static_cast<std::int16_t>(from),
+                                  static_cast<std::int16_t>(to), 0};
+        }
+    static const char kPromo[3] = {'q', 'r', 'b'};
+    for (int ff = 0; ff < 8; ++ff)
+      for (int tf = ff - 1; tf <= ff + 1; ++tf) {
+        if (tf < 0 || tf > 7)
+          continue;
+        for (int p = 0; p < 3; ++p) {
+          promotion[ff * 24 + tf * 3 + p] = static_cast<std::int16_t>(n);
+          moves[n++] = PolicyMove{static_cast<std::int16_t>(48 + ff),
+                                  static_cast<std::int16_t>(56 + tf), kPromo[p]};
+        }
+      }
+    for (int i = 0; i < 64 * 64; ++i)
+      attention[i] = regular[i];
+    for (int i = 0; i < 8 * 24; ++i)
+      attention[64 * 64 + i] = promotion[i];
+    gather.fill(-1);
+    for (int raw = 0; raw < kAttentionRaw; ++raw)
+      if (attention[raw] >= 0)
+        gather[attention[raw]] = static_cast<std::int16_t>(raw);
+  }
+};
+
+const Built &B() {
+  static const Built b;
+  return b;
+}
+
+}  // namespace
+
+const std::array<PolicyMove, kPolicyOutputs> &MoveList() { return B().moves; }
+const std::array<std::int16_t, kAttentionRaw> &AttentionMap() {
+  return B().attention;
+}
+const std::array<std::int16_t, kPolicyOutputs> &AttentionGather() {
+  return B().gather;
+}
+
+int MoveToIndex(int from, int to, char promo) {
+  if (from < 0 || from > 63 || to < 0 || to > 63)
+    return -1;
+  if (promo == 'q' || promo == 'r' || promo == 'b') {
+    if ((from >> 3) != 6 || (to >> 3) != 7)
+      return -1;
+    const int p = promo == 'q' ? 0 : (promo == 'r' ? 1 : 2);
+    return B().promotion[(from & 7) * 24 + (to & 7) * 3 + p];
+  }
+  return B().regular[from * 64 + to];
+}
+
+}  // namespace mfh_policy

@@ -1,0 +1,138 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Gates: input planes and the policy index map bit-exact;
+policy logits max-abs <= 2e-2 and the same top-1 move on >= 99.5% of
+positions; WDL max-abs <= 5e-3 (the reference's cross-backend gate,
+tools/compare_nn_backend_outputs.py:21-22).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from metalfish_amd import backend, synth
+
+pytestmark = pytest.mark.gpu
+
+POLICY_TOL = 2e-2
+WDL_TOL = 5e-3
+
+
+def _bf16_bits(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _bits_to_f32(b):
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if backend.device_count() < 1:
+        pytest.fail("GPU tests need an MI355X; none visible")
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 64), (100, 40, 128), (256, 3104, 1024),
+                                   (4096, 1024, 1536), (2112, 200, 256)])
+def test_gemm_bf16_against_fp64(m, n, k):
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    a = _bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    w = _bf16_bits((rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
+    bias = rng.standard_normal(n).astype(np.float32)
+    got = backend.gemm_bf16(a, w, bias)
+    ref = _bits_to_f32(a).astype(np.float64) @ _bits_to_f32(w).astype(np.float64).T + bias
+    # fp32 accumulation of k bf16 products: error well under 1e-4 relative.
+    assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max() + 1e-5
+
+
+def test_gemm_mish_epilogue():
+    rng = np.random.default_rng(5)
+    a = _bf16_bits(rng.standard_normal((128, 256)).astype(np.float32))
+    w = _bf16_bits((rng.standard_normal((192, 256)) / 16).astype(np.float32))
+    got = backend.gemm_bf16(a, w, None, act="mish")
+    x = _bits_to_f32(a).astype(np.float64) @ _bits_to_f32(w).astype(np.float64).T
+    ref = x * np.tanh(np.log1p(np.exp(x)))
+    assert np.abs(got - ref).max() <= 2e-5 * max(1.0, np.abs(ref).max())
+
+
+def test_unpacked_planes_bit_exact():
+    planes, _ = synth.playout_positions(64, seed=11)
+    masks, values = oracle.pack_planes(planes)
+    got = backend.unpack_planes(masks, values)
+    # Classical planes are 0/1 or uniform, so packing is lossless.
+    assert np.array_equal(got.view(np.uint32), planes.view(np.uint32))
+
+
+def _compare(spec_name, n, seed=0, first_game=0, check_packed=True):
+    spec = synth.SPECS[spec_name]
+    weights = synth.make_weights(spec, seed=seed)
+    planes, legal = synth.playout_positions(n, seed=seed, first_game=first_game)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads), weights).evaluate_batch(
+        planes)
+    net = backend.create_network(spec, weights, max_batch=max(n, 1), device=0)
+    gpu = net.evaluate_batch(planes)
+    if check_packed:
+        masks, values = oracle.pack_planes(planes)
+        p2, v2 = net.eval_packed(masks, values)
+        # Host packing in the C ABI matches the reference packing bit for bit.
+        assert np.array_equal(p2, gpu["policy"]) and np.array_equal(v2, gpu["wdl"])
+    net.close()
+    return gpu, ref, legal
+
+
+def _top1_agreement(gpu_policy, ref_policy, legal):
+    agree = 0
+    for i in range(gpu_policy.shape[0]):
+        idx = legal[i][legal[i] >= 0]
+        agree += int(idx[np.argmax(gpu_policy[i, idx])] == idx[np.argmax(ref_policy[i, idx])])
+    return agree / gpu_policy.shape[0]
+
+
+def test_cpu_plumbing_net_parity():
+    gpu, ref, legal = _compare("cpu_plumbing", 16)
+    perr = np.abs(gpu["policy"] - ref["policy"]).max()
+    werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
+    print(f"cpu_plumbing: policy max-abs {perr:.3e} wdl max-abs {werr:.3e}")
+    assert perr <= POLICY_TOL
+    assert werr <= WDL_TOL
+    assert _top1_agreement(gpu["policy"], ref["policy"], legal) >= 0.995
+    assert np.allclose(gpu["value"], gpu["wdl"][:, 0] - gpu["wdl"][:, 2])
+
+
+def test_bt4_net_parity_16_positions():
+    gpu, ref, legal = _compare("bt4", 16, check_packed=False)
+    perr = np.abs(gpu["policy"] - ref["policy"]).max()
+    werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
+    top1 = _top1_agreement(gpu["policy"], ref["policy"], legal)
+    print(f"bt4: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}")
+    assert perr <= POLICY_TOL
+    assert werr <= WDL_TOL
+    assert top1 >= 0.995
+
+
+def test_batch_invariance_and_chunking():
+    """Each position's outputs do not depend on its batch neighbours or on
+    chunking (reference single-vs-batched parity, test_nn_comparison.cpp:
+    796-1480)."""
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=3)
+    planes, _ = synth.playout_positions(40, seed=3)
+    net = backend.create_network(spec, weights, max_batch=16, device=0)
+    full = net.evaluate_batch(planes)  # chunks 16 + 16 + 8
+    single = np.stack([net.evaluate(planes[i])["policy"] for i in (0, 17, 39)])
+    assert np.allclose(single, full["policy"][[0, 17, 39]], atol=1e-5)
+    net.close()
+
+
+def test_bad_batch_rejected():
+    spec = synth.SPECS["cpu_plumbing"]
+    net = backend.create_network(spec, synth.make_weights(spec), max_batch=4, device=0)
+    masks = np.zeros((5, 112), np.uint64)
+    values = np.zeros((5, 112), np.float32)
+    out = np.zeros((5, 1858), np.float32)
+    wdl = np.zeros((5, 3), np.float32)
+    rc = backend.lib().mfh_net_eval(net._h, 5, masks.ctypes.data, values.ctypes.data,
+                                    out.ctypes.data, wdl.ctypes.data, None)
+    assert rc == -1 and b"batch" in backend.lib().mfh_last_error()
+    net.close()
