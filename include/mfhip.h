@@ -57,6 +57,12 @@ enum {
 enum { MFH_DEFAULT_ACTIVATION_RELU = 0, MFH_DEFAULT_ACTIVATION_MISH = 1 };
 /* Storage of the GEMM weights on the device. */
 enum { MFH_WEIGHTS_BF16 = 0 };
+/* Activation precision.  BF16: every MFMA operand is one bf16 value (fastest).
+ * BF16X2: activations are carried as a bf16 pair hi + lo (lo = bf16(x - hi))
+ * and every product takes two (GEMMs) or three (attention, policy map)
+ * bf16 MFMAs, giving ~16-bit activation precision against the exact bf16
+ * weights at twice the MFMA work. */
+enum { MFH_PRECISION_BF16 = 0, MFH_PRECISION_BF16X2 = 1 };
 
 /* Network description: the format fields of the weights file plus the
  * attention head count (Weights.headcount) and run-time sizing. */
@@ -71,6 +77,7 @@ typedef struct {
   int smolgen_activation; /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
   int headcount;          /* body attention heads; head depth must be 32 */
   int weights_dtype;      /* MFH_WEIGHTS_BF16 */
+  int precision;          /* MFH_PRECISION_BF16 or MFH_PRECISION_BF16X2 */
   int max_batch;          /* largest batch one eval call accepts (>= 1) */
   int device;             /* HIP device ordinal, -1 = current device */
 } mfh_net_desc;
@@ -136,6 +143,30 @@ typedef struct {
 } mfh_capabilities;
 int mfh_net_capabilities(const mfh_net *net, mfh_capabilities *out);
 
+/* Stage profiler (the counterpart of the reference's METALFISH_CUDA_PROFILE
+ * stage timers, reference src/nn/cuda/cuda_stage_executor.cpp:421-482):
+ * while enabled, every kernel launch of an eval call is bracketed by HIP
+ * events recorded on the stream it is launched on.  mfh_net_profile
+ * synchronises and returns, per kernel kind, the launch count, summed
+ * duration and the algorithmic work of those launches (GEMM/attention
+ * FLOPs = 2*M*N*K of the useful products, bytes = minimal HBM traffic). */
+typedef struct {
+  char name[48];
+  int launches;
+  double milliseconds;
+  double flops;
+  double bytes;
+} mfh_profile_entry;
+int mfh_net_set_profiling(mfh_net *net, int enabled);
+int mfh_net_profile(mfh_net *net, mfh_profile_entry *out, int capacity,
+                    int *count);
+int mfh_net_profile_reset(mfh_net *net);
+
+/* PackInputPlanesRaw (reference src/nn/input_plane_packing.h:61-83):
+ * planes[batch*112*64] -> masks[batch*112], values[batch*112]. */
+int mfh_pack_planes(int batch, const float *planes, uint64_t *masks,
+                    float *values);
+
 /* Number of visible devices (0 without a GPU). */
 int mfh_device_count(int *count);
 
@@ -155,9 +186,9 @@ int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A,
 
 /* Copies a named workspace tensor left by the last eval call to host
  * memory: "body" (fp32 [B*64,E], encoder output; with no encoder layers
- * the input-embedding output), "policy_qk" (bf16 [B*64,2Dp]),
- * "value_hidden" (fp32 [B,Vh]).  bytes must equal the tensor's size for the
- * last batch. */
+ * the input-embedding output) or "policy_qk" (bf16 [B*64,2Dp], the hi plane
+ * in split precision).  bytes must equal the tensor's size for the last
+ * batch. */
 int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out,
                          uint64_t bytes);
 

@@ -20,25 +20,33 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libmfhip.so")
 
 MFH_OK = 0
+PRECISION = {"bf16": 0, "bf16x2": 1}
 ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid": 5,
               "selu": 6, "swish": 7, "relu_2": 8}
 
 # Every symbol include/mfhip.h declares.
 EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_planes",
-           "mfh_net_eval_device", "mfh_net_info", "mfh_net_capabilities", "mfh_device_count",
-           "mfh_last_error", "mfh_debug_unpack_planes", "mfh_debug_gemm_bf16",
-           "mfh_net_debug_tensor")
+           "mfh_net_eval_device", "mfh_net_info", "mfh_net_capabilities",
+           "mfh_net_set_profiling", "mfh_net_profile", "mfh_net_profile_reset",
+           "mfh_pack_planes", "mfh_device_count", "mfh_last_error", "mfh_debug_unpack_planes",
+           "mfh_debug_gemm_bf16", "mfh_net_debug_tensor")
 
 
 class MfhNetDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "network", "policy", "value", "moves_left", "input_embedding", "default_activation",
-        "ffn_activation", "smolgen_activation", "headcount", "weights_dtype", "max_batch",
-        "device")]
+        "ffn_activation", "smolgen_activation", "headcount", "weights_dtype", "precision",
+        "max_batch", "device")]
 
 
 class MfhTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("count", ctypes.c_uint64)]
+
+
+class MfhProfileEntry(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 48), ("launches", ctypes.c_int),
+                ("milliseconds", ctypes.c_double), ("flops", ctypes.c_double),
+                ("bytes", ctypes.c_double)]
 
 
 class MfhCapabilities(ctypes.Structure):
@@ -68,6 +76,10 @@ def lib():
             "mfh_net_eval_device": ([vp, i, vp, vp, vp, vp, vp], i),
             "mfh_net_info": ([vp, ctypes.c_char_p, ctypes.c_size_t], i),
             "mfh_net_capabilities": ([vp, ctypes.POINTER(MfhCapabilities)], i),
+            "mfh_net_set_profiling": ([vp, i], i),
+            "mfh_net_profile": ([vp, ctypes.POINTER(MfhProfileEntry), i, ctypes.POINTER(i)], i),
+            "mfh_net_profile_reset": ([vp], i),
+            "mfh_pack_planes": ([i, vp, vp, vp], i),
             "mfh_device_count": ([ctypes.POINTER(i)], i),
             "mfh_last_error": ([], ctypes.c_char_p),
             "mfh_debug_unpack_planes": ([i, vp, vp, vp], i),
@@ -103,7 +115,7 @@ class HipNetwork:
 
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
-                 device=-1):
+                 device=-1, precision="bf16x2"):
         self._weights = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
                          for k, v in weights.items()}
         names = list(self._weights)
@@ -117,7 +129,8 @@ class HipNetwork:
                           default_activation=1 if default_activation == "mish" else 0,
                           ffn_activation=ACTIVATION[ffn_activation],
                           smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
-                          weights_dtype=0, max_batch=max_batch, device=device)
+                          weights_dtype=0, precision=PRECISION[precision],
+                          max_batch=max_batch, device=device)
         handle = ctypes.c_void_p()
         self._h = None
         _check(lib().mfh_net_create(ctypes.byref(desc), tensors, len(names),
@@ -125,6 +138,7 @@ class HipNetwork:
         self._h = handle
         self.wdl = wdl
         self.max_batch = max_batch
+        self.precision = precision
         # Host weights are only needed for the upload.
         self._weights = None
 
@@ -199,11 +213,38 @@ class HipNetwork:
         _check(lib().mfh_net_eval_device(self._h, batch, d_masks, d_values, d_policy, d_wdl,
                                          stream), "mfh_net_eval_device")
 
+    def set_profiling(self, enabled: bool):
+        _check(lib().mfh_net_set_profiling(self._h, 1 if enabled else 0), "mfh_net_set_profiling")
+
+    def profile_reset(self):
+        _check(lib().mfh_net_profile_reset(self._h), "mfh_net_profile_reset")
+
+    def profile(self) -> dict:
+        """{kernel kind: {launches, ms, flops, bytes}} accumulated since reset."""
+        n = ctypes.c_int(0)
+        _check(lib().mfh_net_profile(self._h, None, 0, ctypes.byref(n)), "mfh_net_profile")
+        entries = (MfhProfileEntry * max(1, n.value))()
+        _check(lib().mfh_net_profile(self._h, entries, n.value, ctypes.byref(n)),
+               "mfh_net_profile")
+        return {e.name.decode(): {"launches": e.launches, "ms": e.milliseconds,
+                                  "flops": e.flops, "bytes": e.bytes}
+                for e in entries[:n.value]}
+
     def debug_tensor(self, name, shape, dtype):
         out = np.zeros(shape, dtype=dtype)
         _check(lib().mfh_net_debug_tensor(self._h, name.encode(), out.ctypes.data, out.nbytes),
                "mfh_net_debug_tensor")
         return out
+
+
+def pack_planes(planes):
+    """Reference packed-input contract (input_plane_packing.h:61-83)."""
+    planes = np.ascontiguousarray(planes, dtype=np.float32).reshape(-1, 112, 64)
+    b = planes.shape[0]
+    masks = np.zeros((b, 112), np.uint64)
+    values = np.zeros((b, 112), np.float32)
+    _check(lib().mfh_pack_planes(b, _ptr(planes), _ptr(masks), _ptr(values)), "mfh_pack_planes")
+    return masks, values
 
 
 def unpack_planes(masks, values):
@@ -227,10 +268,12 @@ def gemm_bf16(a_bits, w_bits, bias=None, act="none"):
     return out
 
 
-def create_network(spec, weights, max_batch=256, device=-1):
-    """HipNetwork for a synth.NetSpec and its weights."""
+def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2"):
+    """HipNetwork for a synth.NetSpec and its weights.  ``precision`` is
+    "bf16x2" (split activations, default: meets every parity gate) or "bf16"
+    (single-pass, twice the MFMA throughput)."""
     return HipNetwork(weights, spec.heads, wdl=spec.wdl,
                       default_activation=spec.default_activation,
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,
-                      device=device)
+                      device=device, precision=precision)

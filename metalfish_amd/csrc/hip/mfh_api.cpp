@@ -111,6 +111,7 @@ struct Dims {
   int C = 0, Hs = 0, HG = 0, G = 0;
   int Dp = 0, Vd = 0, Vh = 0, Vout = 0;
   bool gates = false, input_ffn = false, smolgen = false, wdl = true;
+  bool split = false;  // MFH_PRECISION_BF16X2
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -142,11 +143,31 @@ struct mfh_net {
   unsigned char *pin_out = nullptr;  // policy | value
   int last_batch = 0;
 
+  // Stage profiler.
+  struct Pending {
+    std::string name;
+    double flops, bytes;
+    hipEvent_t start, stop;
+  };
+  struct Totals {
+    int launches = 0;
+    double ms = 0, flops = 0, bytes = 0;
+  };
+  bool profiling = false;
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> event_pool;
+  std::map<std::string, Totals> totals;
+
   template <typename T> T *W(size_t off) const {
     return reinterpret_cast<T *>(weights + off);
   }
-  template <typename T> T *S(const char *name) const {
+  template <typename T> T *S(const std::string &name) const {
     return reinterpret_cast<T *>(ws + ws_off.at(name));
+  }
+  // Residual plane of a bf16 activation, or null in single precision.
+  std::uint16_t *Lo(const std::string &name) const {
+    auto it = ws_off.find(name + "_lo");
+    return it == ws_off.end() ? nullptr : reinterpret_cast<std::uint16_t *>(ws + it->second);
   }
 };
 
@@ -228,6 +249,9 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
                     "HIP backend supports INPUT_EMBEDDING_PE_DENSE only (as the reference CPU backend)");
   if (desc.weights_dtype != MFH_WEIGHTS_BF16)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
+  if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2)
+    return SetError(MFH_ERR_UNSUPPORTED, "unsupported precision mode");
+  d.split = desc.precision == MFH_PRECISION_BF16X2;
   d.wdl = desc.value == MFH_VALUE_WDL;
   d.act_default = desc.default_activation == MFH_DEFAULT_ACTIVATION_MISH ? mfh::ACT_MISH
                                                                          : mfh::ACT_RELU;
@@ -431,41 +455,119 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   return MFH_OK;
 }
 
+// Split-K factor for the small-M GEMMs whose consumer sums partials
+// (smolgen dense1 -> LayerNorm, value dense1 -> value head).  It depends on K
+// only, so every position's result is bit-identical whatever the batch size
+// or the batch it shares a call with.
+int SplitK(int k) {
+  int s = 1;
+  while (s < 8 && k % (2 * s * 64) == 0 && k / (2 * s) >= 256)
+    s *= 2;
+  return s;
+}
+
 void PlanWorkspace(mfh_net *net) {
   const Dims &d = net->d;
   const size_t B = static_cast<size_t>(net->max_batch);
   const size_t M = B * kSquares;
   size_t off = 0;
-  auto add = [&](const char *name, size_t bytes) {
+  auto add = [&](const std::string &name, size_t bytes) {
     off = AlignUp(off, 256);
     net->ws_off[name] = off;
     off += bytes;
   };
+  // bf16 activations that feed MFMAs get a residual ("_lo") plane in split
+  // precision.
+  auto add16 = [&](const std::string &name, size_t elems) {
+    add(name, elems * 2);
+    if (d.split)
+      add(name + "_lo", elems * 2);
+  };
+  const int hid = d.F > d.Fi ? d.F : d.Fi;
+  const int sk1 = d.smolgen ? SplitK(kSquares * d.C) : 1;
+  const int skv = SplitK(kSquares * d.Vd);
   add("masks", B * kPlanes * 8);
   add("values", B * kPlanes * 4);
-  add("emb_in", M * d.Kin * 2);
+  add16("emb_in", M * d.Kin);
   add("pos_in", B * kSquares * 12 * 2);
   add("pe", B * kSquares * d.P * 4);
   add("pre", M * d.E * 4);
   add("resid", M * d.E * 4);
-  add("act", M * d.E * 2);
-  add("qkv", M * 3 * d.E * 2);
-  add("comp", M * (d.C ? d.C : 1) * 2);
-  add("sg1", B * (d.Hs ? d.Hs : 1) * 4);
-  add("sg1n", B * (d.Hs ? d.Hs : 1) * 2);
+  add16("act", M * d.E);
+  add16("qkv", M * 3 * d.E);
+  add16("comp", M * (d.C ? d.C : 1));
+  add("sg1", sk1 * B * (d.Hs ? d.Hs : 1) * 4);
+  add16("sg1n", B * (d.Hs ? d.Hs : 1));
   add("sg2", B * (d.HG ? d.HG : 1) * 4);
-  add("sg2n", B * (d.HG ? d.HG : 1) * 2);
-  add("bias", d.smolgen ? B * d.H * kSquares * kSquares * 2 : 256);
-  add("ctx", M * d.E * 2);
-  const int hid = d.F > d.Fi ? d.F : d.Fi;
-  add("hid", M * (hid ? hid : 1) * 2);
-  add("pol_emb", M * d.Dp * 2);
-  add("val_emb", M * d.Vd * 2);
-  add("polqk", M * 2 * d.Dp * 2);
-  add("val1", B * d.Vh * 4);
+  add16("sg2n", B * (d.HG ? d.HG : 1));
+  add("bias", d.smolgen ? B * d.H * kSquares * kSquares * (d.split ? 4 : 2) : 256);
+  add16("ctx", M * d.E);
+  add16("hid", M * (hid ? hid : 1));
+  add16("pol_emb", M * d.Dp);
+  add16("val_emb", M * d.Vd);
+  add16("polqk", M * 2 * d.Dp);
+  add("val1", skv * B * d.Vh * 4);
   add("policy", B * kPolicy * 4);
   add("wdl", B * 3 * 4);
   net->ws_bytes = AlignUp(off, 256);
+}
+
+hipEvent_t TakeEvent(mfh_net *net) {
+  if (!net->event_pool.empty()) {
+    hipEvent_t e = net->event_pool.back();
+    net->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDefault) != hipSuccess)
+    return nullptr;
+  return e;
+}
+
+// Brackets one launch with events on its stream when profiling is on.
+struct StageTimer {
+  mfh_net *net;
+  hipStream_t st;
+  mfh_net::Pending rec;
+  bool on = false;
+  StageTimer(mfh_net *n, hipStream_t s, const char *name, double flops, double bytes)
+      : net(n), st(s) {
+    if (!net->profiling)
+      return;
+    rec.name = name;
+    rec.flops = flops;
+    rec.bytes = bytes;
+    rec.start = TakeEvent(net);
+    rec.stop = TakeEvent(net);
+    on = rec.start && rec.stop && hipEventRecord(rec.start, st) == hipSuccess;
+  }
+  ~StageTimer() {
+    if (on && hipEventRecord(rec.stop, st) == hipSuccess)
+      net->pending.push_back(rec);
+  }
+};
+
+int CollectProfile(mfh_net *net) {
+  for (auto &p : net->pending) {
+    MFH_HIP_CHECK(hipEventSynchronize(p.stop));
+    float ms = 0.f;
+    MFH_HIP_CHECK(hipEventElapsedTime(&ms, p.start, p.stop));
+    auto &t = net->totals[p.name];
+    t.launches += 1;
+    t.ms += ms;
+    t.flops += p.flops;
+    t.bytes += p.bytes;
+    net->event_pool.push_back(p.start);
+    net->event_pool.push_back(p.stop);
+  }
+  net->pending.clear();
+  return MFH_OK;
+}
+
+const char *GemmKind(const mfh::GemmParams &p) {
+  if (p.k_splits > 1)
+    return "gemm_bf16_splitk";
+  return "gemm_bf16";
 }
 
 int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
@@ -474,24 +576,6 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   const int M = B * kSquares;
   const int E = d.E;
   std::string err_;
-  auto gemm = [&](const std::uint16_t *A, int lda, size_t w_off, int ldw, int m, int n, int k,
-                  const float *bias, int act, int mode, void *C, int ldc) {
-    mfh::GemmParams p;
-    p.A = A;
-    p.lda = lda;
-    p.W = net->W<std::uint16_t>(w_off);
-    p.ldw = ldw;
-    p.M = m;
-    p.N = n;
-    p.K = k;
-    p.bias = bias;
-    p.act = act;
-    p.out_mode = mode;
-    p.C = C;
-    p.ldc = ldc;
-    return p;
-  };
-  auto run = [&](const mfh::GemmParams &p) { return mfh::LaunchGemm(p, st, &err_); };
   auto fail = [&](hipError_t e) {
     return SetError(e == hipErrorInvalidValue ? MFH_ERR_INVALID : MFH_ERR_HIP,
                     err_.empty() ? std::string(hipGetErrorString(e)) : err_);
@@ -502,129 +586,207 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     if (e_ != hipSuccess)                                                      \
       return fail(e_);                                                         \
   } while (0)
+  // GEMM with A from workspace tensor `a` (its residual plane when split).
+  auto gemm = [&](const std::string &a, int lda, size_t w_off, int ldw, int m, int n, int k,
+                  const float *bias, int act, int mode, void *C, void *C_lo, int ldc) {
+    mfh::GemmParams p;
+    p.A = net->S<std::uint16_t>(a);
+    p.A_lo = net->Lo(a);
+    p.lda = lda;
+    p.W = net->W<std::uint16_t>(w_off);
+    p.ldw = ldw;
+    p.M = m;
+    p.N = n;
+    p.K = k;
+    p.bias = bias;
+    p.act = act;
+    p.out_mode = mode;
+    p.C = C;
+    p.C_lo = C_lo;
+    p.ldc = ldc;
+    return p;
+  };
+  const double plane_mult = d.split ? 2.0 : 1.0;  // bytes of a bf16 activation
+  auto run = [&](const mfh::GemmParams &p) {
+    const double flops = 2.0 * p.M * p.N * p.K;
+    const double out_bytes = p.out_mode == mfh::GEMM_OUT_BF16 ? 2.0 * plane_mult : 4.0;
+    const double bytes = 2.0 * p.M * p.K * (p.A_lo ? 2.0 : 1.0) + 2.0 * p.N * p.K +
+                         out_bytes * p.M * p.N * p.k_splits +
+                         (p.out_mode == mfh::GEMM_OUT_RESID_F32 ? 4.0 * p.M * p.N : 0.0);
+    StageTimer t(net, st, GemmKind(p), flops, bytes);
+    return mfh::LaunchGemm(p, st, &err_);
+  };
+  auto run_ln = [&](const mfh::LayerNormParams &lp) {
+    const double n = static_cast<double>(lp.rows) * lp.width;
+    const double bytes = 4.0 * n * lp.parts + (lp.y_f32 ? 4.0 * n : 0.0) +
+                         (lp.y_bf16 ? 2.0 * n * (lp.y_bf16_lo ? 2.0 : 1.0) : 0.0);
+    StageTimer t(net, st, "layernorm", 0.0, bytes);
+    return mfh::LaunchLayerNorm(lp, st, &err_);
+  };
+  auto ln = [&](const float *x, int rows, int width, float eps, const float *g, const float *b,
+                float *y32, const std::string &y16) {
+    mfh::LayerNormParams lp;
+    lp.x = x;
+    lp.rows = rows;
+    lp.width = width;
+    lp.eps = eps;
+    lp.gamma = g;
+    lp.beta = b;
+    lp.y_f32 = y32;
+    lp.y_bf16 = net->S<std::uint16_t>(y16);
+    lp.y_bf16_lo = net->Lo(y16);
+    return lp;
+  };
 
-  auto *emb_in = net->S<std::uint16_t>("emb_in");
-  auto *pos_in = net->S<std::uint16_t>("pos_in");
   auto *pe = net->S<float>("pe");
   auto *pre = net->S<float>("pre");
   auto *resid = net->S<float>("resid");
-  auto *act = net->S<std::uint16_t>("act");
-  auto *qkv = net->S<std::uint16_t>("qkv");
-  auto *comp = net->S<std::uint16_t>("comp");
   auto *sg1 = net->S<float>("sg1");
-  auto *sg1n = net->S<std::uint16_t>("sg1n");
   auto *sg2 = net->S<float>("sg2");
-  auto *sg2n = net->S<std::uint16_t>("sg2n");
-  auto *bias = net->S<std::uint16_t>("bias");
-  auto *ctx = net->S<std::uint16_t>("ctx");
-  auto *hid = net->S<std::uint16_t>("hid");
-  auto *pol_emb = net->S<std::uint16_t>("pol_emb");
-  auto *val_emb = net->S<std::uint16_t>("val_emb");
-  auto *polqk = net->S<std::uint16_t>("polqk");
   auto *val1 = net->S<float>("val1");
 
   // Input planes, dynamic positional encoding, embedding (cpu_network.cpp:
   // 691-890), embedding LayerNorm + gates (1399-1457, 1268-1316).
-  MFH_RUN(mfh::LaunchExpandInputs(masks, values, B, emb_in, d.Kin, pos_in, st, &err_));
-  MFH_RUN(run(gemm(pos_in, kSquares * 12, net->pre_w, kSquares * 12, B, kSquares * d.P,
-                   kSquares * 12, net->W<float>(net->pre_b), mfh::ACT_NONE, mfh::GEMM_OUT_F32,
-                   pe, kSquares * d.P)));
-  MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, emb_in, d.Kin, st, &err_));
-  MFH_RUN(run(gemm(emb_in, d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
-                   d.act_default, mfh::GEMM_OUT_F32, pre, E)));
-  MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, 1e-3f, net->W<float>(net->emb_ln_g),
-                               net->W<float>(net->emb_ln_b),
-                               net->mult_gate ? net->W<float>(net->mult_gate) : nullptr,
-                               net->add_gate ? net->W<float>(net->add_gate) : nullptr, resid,
-                               act, st, &err_));
-  if (d.input_ffn) {
-    MFH_RUN(run(gemm(act, E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
-                     d.act_ffn, mfh::GEMM_OUT_BF16, hid, d.Fi)));
-    mfh::GemmParams p = gemm(hid, d.Fi, net->in_ffn2_w, d.Fi, M, E, d.Fi,
-                             net->W<float>(net->in_ffn2_b), mfh::ACT_NONE,
-                             mfh::GEMM_OUT_RESID_F32, pre, E);
+  {
+    StageTimer t(net, st, "input_expand", 0.0, 12.0 * B * kPlanes + 2.0 * M * d.Kin * plane_mult);
+    MFH_RUN(mfh::LaunchExpandInputs(masks, values, B, net->S<std::uint16_t>("emb_in"),
+                                    net->Lo("emb_in"), d.Kin, net->S<std::uint16_t>("pos_in"),
+                                    st, &err_));
+  }
+  {
+    // The PE input holds exact plane values: single precision suffices.
+    mfh::GemmParams p = gemm("pos_in", kSquares * 12, net->pre_w, kSquares * 12, B,
+                             kSquares * d.P, kSquares * 12, net->W<float>(net->pre_b),
+                             mfh::ACT_NONE, mfh::GEMM_OUT_F32, pe, nullptr, kSquares * d.P);
+    MFH_RUN(run(p));
+  }
+  {
+    StageTimer tpe(net, st, "pe_scatter", 0.0, 4.0 * B * kSquares * d.P);
+    MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, net->S<std::uint16_t>("emb_in"), net->Lo("emb_in"),
+                                 d.Kin, st, &err_));
+  }
+  MFH_RUN(run(gemm("emb_in", d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
+                   d.act_default, mfh::GEMM_OUT_F32, pre, nullptr, E)));
+  {
+    mfh::LayerNormParams lp = ln(pre, M, E, 1e-3f, net->W<float>(net->emb_ln_g),
+                                 net->W<float>(net->emb_ln_b), resid, "act");
+    lp.mult_gate = net->mult_gate ? net->W<float>(net->mult_gate) : nullptr;
+    lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;
+    MFH_RUN(run_ln(lp));
+  }
+  auto residual_gemm = [&](const std::string &a, int k, size_t w_off, const float *bias) {
+    mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
+                             mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
     p.resid = resid;
     p.ldr = E;
     p.alpha = d.alpha;
-    MFH_RUN(run(p));
-    MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
-                                 net->W<float>(net->in_ln_b), nullptr, nullptr, resid, act, st,
-                                 &err_));
+    return run(p);
+  };
+  if (d.input_ffn) {
+    MFH_RUN(run(gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
+                     d.act_ffn, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"),
+                     net->Lo("hid"), d.Fi)));
+    MFH_RUN(residual_gemm("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b)));
+    MFH_RUN(run_ln(ln(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
+                      net->W<float>(net->in_ln_b), resid, "act")));
   }
 
   // Encoder layers (cpu_network.cpp:1027-1266, 1318-1457).
   for (const Layer &L : net->layers) {
-    mfh::GemmParams p = gemm(act, E, L.qkv_w, E, M, 3 * E + (L.smolgen ? d.C : 0), E,
-                             net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16, qkv,
-                             3 * E);
+    mfh::GemmParams p = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen ? d.C : 0), E,
+                             net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
+                             net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
     if (L.smolgen) {
       p.split_n = 3 * E;
-      p.C2 = comp;
+      p.C2 = net->S<std::uint16_t>("comp");
+      p.C2_lo = net->Lo("comp");
       p.ldc2 = d.C;
     }
     MFH_RUN(run(p));
-    const std::uint16_t *bias_ptr = nullptr;
+    mfh::AttentionParams ap;
+    ap.qkv = net->S<std::uint16_t>("qkv");
+    ap.qkv_lo = net->Lo("qkv");
+    ap.batch = B;
+    ap.heads = d.H;
+    ap.ctx = net->S<std::uint16_t>("ctx");
+    ap.ctx_lo = net->Lo("ctx");
     if (L.smolgen) {
+      // Smolgen (cpu_network.cpp:1065-1173): dense1 on the flattened
+      // compression (split-K partials summed by the LayerNorm kernel with
+      // bias and activation), dense2, then the shared global projection.
       const int flat = kSquares * d.C;
-      MFH_RUN(run(gemm(comp, flat, L.sg_d1_w, flat, B, d.Hs, flat,
-                       net->W<float>(L.sg_d1_b), d.act_smolgen, mfh::GEMM_OUT_F32, sg1,
-                       d.Hs)));
-      MFH_RUN(mfh::LaunchLayerNorm(sg1, B, d.Hs, 1e-3f, net->W<float>(L.sg_ln1_g),
-                                   net->W<float>(L.sg_ln1_b), nullptr, nullptr, nullptr, sg1n,
-                                   st, &err_));
-      MFH_RUN(run(gemm(sg1n, d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs,
-                       net->W<float>(L.sg_d2_b), d.act_smolgen, mfh::GEMM_OUT_F32, sg2,
-                       d.HG)));
-      MFH_RUN(mfh::LaunchLayerNorm(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
-                                   net->W<float>(L.sg_ln2_b), nullptr, nullptr, nullptr, sg2n,
-                                   st, &err_));
-      MFH_RUN(run(gemm(sg2n, d.G, net->global_w, d.G, B * d.H, kSquares * kSquares, d.G,
-                       nullptr, mfh::ACT_NONE, mfh::GEMM_OUT_BF16, bias,
-                       kSquares * kSquares)));
-      bias_ptr = bias;
+      mfh::GemmParams p1 = gemm("comp", flat, L.sg_d1_w, flat, B, d.Hs, flat, nullptr,
+                                mfh::ACT_NONE, mfh::GEMM_OUT_F32, sg1, nullptr, d.Hs);
+      p1.k_splits = SplitK(flat);
+      MFH_RUN(run(p1));
+      mfh::LayerNormParams l1 = ln(sg1, B, d.Hs, 1e-3f, net->W<float>(L.sg_ln1_g),
+                                   net->W<float>(L.sg_ln1_b), nullptr, "sg1n");
+      l1.parts = p1.k_splits;
+      l1.bias = net->W<float>(L.sg_d1_b);
+      l1.act = d.act_smolgen;
+      MFH_RUN(run_ln(l1));
+      MFH_RUN(run(gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr, mfh::ACT_NONE,
+                       mfh::GEMM_OUT_F32, sg2, nullptr, d.HG)));
+      mfh::LayerNormParams l2 = ln(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
+                                   net->W<float>(L.sg_ln2_b), nullptr, "sg2n");
+      l2.bias = net->W<float>(L.sg_d2_b);
+      l2.act = d.act_smolgen;
+      MFH_RUN(run_ln(l2));
+      void *bias = net->S<void>("bias");
+      MFH_RUN(run(gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares, d.G,
+                       nullptr, mfh::ACT_NONE, d.split ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
+                       bias, nullptr, kSquares * kSquares)));
+      ap.bias = bias;
+      ap.bias_f32 = d.split ? 1 : 0;
     }
-    MFH_RUN(mfh::LaunchAttention(qkv, bias_ptr, B, d.H, ctx, st, &err_));
-    mfh::GemmParams po = gemm(ctx, E, L.out_w, E, M, E, E, net->W<float>(L.out_b),
-                              mfh::ACT_NONE, mfh::GEMM_OUT_RESID_F32, pre, E);
-    po.resid = resid;
-    po.ldr = E;
-    po.alpha = d.alpha;
-    MFH_RUN(run(po));
-    MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, d.eps_body, net->W<float>(L.ln1_g),
-                                 net->W<float>(L.ln1_b), nullptr, nullptr, resid, act, st,
-                                 &err_));
-    MFH_RUN(run(gemm(act, E, L.ffn1_w, E, M, d.F, E, net->W<float>(L.ffn1_b), d.act_ffn,
-                     mfh::GEMM_OUT_BF16, hid, d.F)));
-    mfh::GemmParams pf = gemm(hid, d.F, L.ffn2_w, d.F, M, E, d.F, net->W<float>(L.ffn2_b),
-                              mfh::ACT_NONE, mfh::GEMM_OUT_RESID_F32, pre, E);
-    pf.resid = resid;
-    pf.ldr = E;
-    pf.alpha = d.alpha;
-    MFH_RUN(run(pf));
-    MFH_RUN(mfh::LaunchLayerNorm(pre, M, E, d.eps_body, net->W<float>(L.ln2_g),
-                                 net->W<float>(L.ln2_b), nullptr, nullptr, resid, act, st,
-                                 &err_));
+    {
+      const double heads_total = static_cast<double>(B) * d.H;
+      const double flops = heads_total * 2.0 * (2.0 * kSquares * kSquares * 32);
+      const double bytes = 2.0 * plane_mult * (3.0 * M * E + M * E) +
+                           (ap.bias ? heads_total * kSquares * kSquares * (d.split ? 4.0 : 2.0)
+                                    : 0.0);
+      StageTimer t(net, st, "attention", flops, bytes);
+      MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
+    }
+    MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b)));
+    MFH_RUN(run_ln(ln(pre, M, E, d.eps_body, net->W<float>(L.ln1_g),
+                      net->W<float>(L.ln1_b), resid, "act")));
+    MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, d.F, E, net->W<float>(L.ffn1_b), d.act_ffn,
+                     mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), d.F)));
+    MFH_RUN(residual_gemm("hid", d.F, L.ffn2_w, net->W<float>(L.ffn2_b)));
+    MFH_RUN(run_ln(ln(pre, M, E, d.eps_body, net->W<float>(L.ln2_g),
+                      net->W<float>(L.ln2_b), resid, "act")));
   }
 
   // Heads: policy "output" | value "output" (default activation), policy
   // Q | K, attention policy map, value dense1 (flattened squares) and dense2.
-  mfh::GemmParams ph = gemm(act, E, net->head_w, E, M, d.Dp + d.Vd, E,
+  mfh::GemmParams ph = gemm("act", E, net->head_w, E, M, d.Dp + d.Vd, E,
                             net->W<float>(net->head_b), d.act_default, mfh::GEMM_OUT_BF16,
-                            pol_emb, d.Dp);
+                            net->S<std::uint16_t>("pol_emb"), net->Lo("pol_emb"), d.Dp);
   ph.split_n = d.Dp;
-  ph.C2 = val_emb;
+  ph.C2 = net->S<std::uint16_t>("val_emb");
+  ph.C2_lo = net->Lo("val_emb");
   ph.ldc2 = d.Vd;
   MFH_RUN(run(ph));
-  MFH_RUN(run(gemm(pol_emb, d.Dp, net->qk_w, d.Dp, M, 2 * d.Dp, d.Dp,
-                   net->W<float>(net->qk_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16, polqk,
-                   2 * d.Dp)));
-  MFH_RUN(mfh::LaunchPolicyMap(polqk, B, d.Dp, net->W<float>(net->promo),
-                               net->W<std::int16_t>(net->gather), policy, st, &err_));
+  MFH_RUN(run(gemm("pol_emb", d.Dp, net->qk_w, d.Dp, M, 2 * d.Dp, d.Dp,
+                   net->W<float>(net->qk_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
+                   net->S<std::uint16_t>("polqk"), net->Lo("polqk"), 2 * d.Dp)));
+  {
+    StageTimer t(net, st, "policy_map", 2.0 * B * kSquares * kSquares * d.Dp,
+                 2.0 * plane_mult * M * 2.0 * d.Dp + 4.0 * B * kPolicy);
+    MFH_RUN(mfh::LaunchPolicyMap(net->S<std::uint16_t>("polqk"), net->Lo("polqk"), B, d.Dp,
+                                 net->W<float>(net->promo), net->W<std::int16_t>(net->gather),
+                                 policy, st, &err_));
+  }
   const int vflat = kSquares * d.Vd;
-  MFH_RUN(run(gemm(val_emb, vflat, net->val1_w, vflat, B, d.Vh, vflat,
-                   net->W<float>(net->val1_b), d.act_default, mfh::GEMM_OUT_F32, val1, d.Vh)));
-  MFH_RUN(mfh::LaunchValueHead(val1, B, d.Vh, net->W<float>(net->val2_w),
-                               net->W<float>(net->val2_b), d.wdl ? 1 : 0, wdl, st, &err_));
+  mfh::GemmParams pv = gemm("val_emb", vflat, net->val1_w, vflat, B, d.Vh, vflat, nullptr,
+                            mfh::ACT_NONE, mfh::GEMM_OUT_F32, val1, nullptr, d.Vh);
+  pv.k_splits = SplitK(vflat);
+  MFH_RUN(run(pv));
+  StageTimer tv(net, st, "value_head", 0.0, 4.0 * pv.k_splits * B * d.Vh);
+  MFH_RUN(mfh::LaunchValueHead(val1, pv.k_splits, net->W<float>(net->val1_b), d.act_default, B,
+                               d.Vh, net->W<float>(net->val2_w), net->W<float>(net->val2_b),
+                               d.wdl ? 1 : 0, wdl, st, &err_));
 #undef MFH_RUN
   return MFH_OK;
 }
@@ -816,6 +978,9 @@ void mfh_net_destroy(mfh_net *net) {
     (void)hipStreamSynchronize(net->stream);
     (void)hipStreamDestroy(net->stream);
   }
+  (void)CollectProfile(net);
+  for (hipEvent_t e : net->event_pool)
+    (void)hipEventDestroy(e);
   if (net->weights) (void)hipFree(net->weights);
   if (net->ws) (void)hipFree(net->ws);
   if (net->pin_in) (void)hipHostFree(net->pin_in);
@@ -885,7 +1050,8 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
     o << " smolgen C=" << d.C << "/" << d.Hs << "/" << d.G;
   o << ", policy attention Dp=" << d.Dp << ", value " << (d.wdl ? "wdl" : "scalar") << " "
     << d.Vd << "/" << d.Vh << ", activations " << ActName(d.act_default) << "/"
-    << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", weights bf16 "
+    << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", precision "
+    << (d.split ? "bf16x2" : "bf16") << ", weights bf16 "
     << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
     << net->max_batch;
   const std::string s = o.str();
@@ -923,9 +1089,6 @@ int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t byt
   } else if (n == "policy_qk") {
     ws_name = "polqk";
     size = B * kSquares * 2 * d.Dp * 2;
-  } else if (n == "value_hidden") {
-    ws_name = "val1";
-    size = B * d.Vh * 4;
   } else {
     return SetError(MFH_ERR_INVALID, "unknown debug tensor " + n);
   }
@@ -934,6 +1097,56 @@ int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t byt
   MFH_HIP_CHECK(hipSetDevice(net->device));
   MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
   MFH_HIP_CHECK(hipMemcpy(out, net->ws + net->ws_off.at(ws_name), size, hipMemcpyDeviceToHost));
+  return MFH_OK;
+}
+
+int mfh_net_set_profiling(mfh_net *net, int enabled) {
+  if (!net)
+    return SetError(MFH_ERR_INVALID, "null net");
+  std::lock_guard<std::mutex> lock(net->mu);
+  net->profiling = enabled != 0;
+  return MFH_OK;
+}
+
+int mfh_net_profile_reset(mfh_net *net) {
+  if (!net)
+    return SetError(MFH_ERR_INVALID, "null net");
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  const int rc = CollectProfile(net);
+  net->totals.clear();
+  return rc;
+}
+
+int mfh_net_profile(mfh_net *net, mfh_profile_entry *out, int capacity, int *count) {
+  if (!net || !count || (capacity > 0 && !out))
+    return SetError(MFH_ERR_INVALID, "mfh_net_profile: bad arguments");
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  const int rc = CollectProfile(net);
+  if (rc != MFH_OK)
+    return rc;
+  int n = 0;
+  for (const auto &kv : net->totals) {
+    if (n < capacity) {
+      mfh_profile_entry &e = out[n];
+      std::memset(&e, 0, sizeof(e));
+      std::snprintf(e.name, sizeof(e.name), "%s", kv.first.c_str());
+      e.launches = kv.second.launches;
+      e.milliseconds = kv.second.ms;
+      e.flops = kv.second.flops;
+      e.bytes = kv.second.bytes;
+    }
+    ++n;
+  }
+  *count = n;
+  return MFH_OK;
+}
+
+int mfh_pack_planes(int batch, const float *planes, uint64_t *masks, float *values) {
+  if (batch < 0 || (batch > 0 && (!planes || !masks || !values)))
+    return SetError(MFH_ERR_INVALID, "mfh_pack_planes: bad arguments");
+  PackPlanes(planes, batch, masks, values);
   return MFH_OK;
 }
 

@@ -34,9 +34,12 @@ enum GemmOut : int {
 // C[M,N] = A[M,K] . W[N,K]^T with bf16 operands and fp32 accumulation.
 // Columns >= split_n are written to C2 (column index minus split_n) so one
 // launch can fill two tensors that share an input (e.g. Q|K|V and the
-// smolgen compression).
+// smolgen compression).  Split precision: A_lo (same lda) holds the bf16
+// residual of each activation (x = A + A_lo); C_lo / C2_lo receive the
+// residuals of bf16 outputs.
 struct GemmParams {
   const std::uint16_t *A = nullptr;
+  const std::uint16_t *A_lo = nullptr;
   int lda = 0;
   const std::uint16_t *W = nullptr;
   int ldw = 0;
@@ -45,23 +48,30 @@ struct GemmParams {
   int act = -1;
   int out_mode = GEMM_OUT_BF16;
   void *C = nullptr;
+  void *C_lo = nullptr;
   int ldc = 0;
   void *C2 = nullptr;
+  void *C2_lo = nullptr;
   int ldc2 = 0;
   int split_n = 1 << 30;
   const float *resid = nullptr;
   int ldr = 0;
   float alpha = 1.0f;
+  // K split over blockIdx.y; each slice writes fp32 partials to
+  // C + slice * M * ldc (GEMM_OUT_F32, no bias/activation).
+  int k_splits = 1;
 };
 
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
 
 // Packed planes -> embedding input rows and the dynamic-PE input.
 //   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values, rest zero (the PE
-//   columns are filled by LaunchScatterPe).
-//   pos_in [B, 64*12] bf16: square-major first 12 planes.
+//   columns are filled by LaunchScatterPe); emb_in_lo (split precision, may
+//   be null) gets the zero residual of those exact values.
+//   pos_in [B, 64*12] bf16: square-major first 12 planes (exact in bf16).
 hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
-                              int batch, std::uint16_t *emb_in, int emb_ld,
+                              int batch, std::uint16_t *emb_in,
+                              std::uint16_t *emb_in_lo, int emb_ld,
                               std::uint16_t *pos_in, hipStream_t stream,
                               std::string *err);
 
@@ -70,41 +80,66 @@ hipError_t LaunchUnpackPlanes(const std::uint64_t *masks, const float *values,
                               int batch, float *planes, hipStream_t stream,
                               std::string *err);
 
-// pe [B, 64*P] fp32 -> emb_in[b*64+sq][112 + c] (bf16).
+// pe [B, 64*P] fp32 -> emb_in[b*64+sq][112 + c] (bf16, plus residual in
+// emb_in_lo when not null).
 hipError_t LaunchScatterPe(const float *pe, int batch, int pe_channels,
-                           std::uint16_t *emb_in, int emb_ld,
-                           hipStream_t stream, std::string *err);
+                           std::uint16_t *emb_in, std::uint16_t *emb_in_lo,
+                           int emb_ld, hipStream_t stream, std::string *err);
 
 // Row LayerNorm: y = (x - mean) * rstd * gamma + beta with the reference's
 // E[x^2] - mean^2 variance (cpu_network.cpp:424-460), optionally followed by
 // the input gates y = y * mult[c][sq] + add[c][sq] (cpu_network.cpp:
 // 1268-1316, gate layout [width][64], sq = row % 64).  Writes fp32 and/or
-// bf16 copies.
-hipError_t LaunchLayerNorm(const float *x, int rows, int width, float eps,
-                           const float *gamma, const float *beta,
-                           const float *mult_gate, const float *add_gate,
-                           float *y_f32, std::uint16_t *y_bf16,
-                           hipStream_t stream, std::string *err);
+// bf16 copies (y_bf16_lo: bf16 residual for split precision).  x may be a
+// stack of `parts` partial sums [parts][rows][width] (split-K GEMM output)
+// that are added together with `bias` and passed through `act` first.
+struct LayerNormParams {
+  const float *x = nullptr;
+  int parts = 1;
+  const float *bias = nullptr;
+  int act = -1;
+  int rows = 0, width = 0;
+  float eps = 1e-3f;
+  const float *gamma = nullptr, *beta = nullptr;
+  const float *mult_gate = nullptr, *add_gate = nullptr;
+  float *y_f32 = nullptr;
+  std::uint16_t *y_bf16 = nullptr;
+  std::uint16_t *y_bf16_lo = nullptr;
+};
+hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream,
+                           std::string *err);
 
 // Multi-head 64x64 attention per (position, head), head depth 32:
 //   ctx = softmax(Q K^T / sqrt(32) + bias) V
 // qkv [B*64, 3E] bf16 (Q | K | V, head h at columns h*32..), bias [B,H,64,64]
-// bf16 or null, ctx [B*64, E] bf16.
-hipError_t LaunchAttention(const std::uint16_t *qkv, const std::uint16_t *bias,
-                           int batch, int heads, std::uint16_t *ctx,
-                           hipStream_t stream, std::string *err);
+// (bf16, or fp32 when bias_f32) or null, ctx [B*64, E] bf16.  Split
+// precision when qkv_lo is set (then ctx_lo is required).
+struct AttentionParams {
+  const std::uint16_t *qkv = nullptr;
+  const std::uint16_t *qkv_lo = nullptr;
+  const void *bias = nullptr;
+  int bias_f32 = 0;
+  int batch = 0, heads = 0;
+  std::uint16_t *ctx = nullptr;
+  std::uint16_t *ctx_lo = nullptr;
+};
+hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream,
+                           std::string *err);
 
 // Attention policy map: raw[q,k] = Q_q.K_k / sqrt(Dp), the 8x24 promotion
 // logits, and the 1858-entry gather (cpu_network.cpp:892-1025).
-// qk [B*64, 2*Dp] bf16 (Q | K), promo [4, Dp] fp32, policy [B, 1858] fp32.
-hipError_t LaunchPolicyMap(const std::uint16_t *qk, int batch, int dp,
-                           const float *promo, const std::int16_t *gather,
-                           float *policy, hipStream_t stream, std::string *err);
+// qk [B*64, 2*Dp] bf16 (Q | K; qk_lo residual plane or null), promo [4, Dp]
+// fp32, policy [B, 1858] fp32.
+hipError_t LaunchPolicyMap(const std::uint16_t *qk, const std::uint16_t *qk_lo,
+                           int batch, int dp, const float *promo,
+                           const std::int16_t *gather, float *policy,
+                           hipStream_t stream, std::string *err);
 
-// Value head output: hidden [B, vh] fp32 -> dense2 + softmax (WDL, 3 outputs)
-// or tanh (scalar, 1 output).
-hipError_t LaunchValueHead(const float *hidden, int batch, int vh,
-                           const float *w2, const float *b2, int wdl,
-                           float *out, hipStream_t stream, std::string *err);
+// Value head output: hidden = act(sum of `parts` partials [parts][B][vh] + b1)
+// then dense2 + softmax (WDL, 3 outputs) or tanh (scalar, 1 output).
+hipError_t LaunchValueHead(const float *hidden, int parts, const float *b1,
+                           int act, int batch, int vh, const float *w2,
+                           const float *b2, int wdl, float *out,
+                           hipStream_t stream, std::string *err);
 
 }  // namespace mfh

@@ -8,6 +8,8 @@
 // The promotion logit for p in [0,192) is, as in the reference,
 //   raw[48 + (p%64)/8][56 + (p%64)%8] + K[56 + (p%24)/3] . (promo[p%3] + promo[3]).
 // The 24 promotion-offset dot products are formed once per position.
+// Split precision: Q and K arrive as hi + lo planes and each fragment product
+// takes three MFMAs (hi.hi + hi.lo + lo.hi).
 #include "mfh_device.h"
 #include "mfh_kernels.h"
 
@@ -17,9 +19,10 @@ namespace {
 constexpr int kSq = 64;
 constexpr int kOutputs = 1858;
 
+template <bool SPLIT>
 __global__ __launch_bounds__(256) void PolicyMapKernel(
-    const std::uint16_t *__restrict__ qk, int dp, float scale,
-    const float *__restrict__ promo, const std::int16_t *__restrict__ gather,
+    const std::uint16_t *__restrict__ qk, const std::uint16_t *__restrict__ qk_lo, int dp,
+    float scale, const float *__restrict__ promo, const std::int16_t *__restrict__ gather,
     float *__restrict__ policy) {
   __shared__ float raw[kSq * kSq];
   __shared__ float pk_term[24];
@@ -27,21 +30,30 @@ __global__ __launch_bounds__(256) void PolicyMapKernel(
   const int wave = threadIdx.x >> 6;
   const int b = blockIdx.x;
   const size_t ld = static_cast<size_t>(2) * dp;
-  const std::uint16_t *base = qk + static_cast<size_t>(b) * kSq * ld;
+  const size_t pos = static_cast<size_t>(b) * kSq * ld;
+  const std::uint16_t *base = qk + pos;
   const int fr = lane & 15, fc = (lane >> 4) * 8;
 
   f32x4 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const std::uint16_t *qrow = base + (wave * 16 + fr) * ld + fc;
+  const size_t qoff = (wave * 16 + fr) * ld + fc;
   for (int k0 = 0; k0 < dp; k0 += 32) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8 *>(qrow + k0);
+    const bf16x8 a = *reinterpret_cast<const bf16x8 *>(base + qoff + k0);
+    bf16x8 a_lo;
+    if constexpr (SPLIT)
+      a_lo = *reinterpret_cast<const bf16x8 *>(qk_lo + pos + qoff + k0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const bf16x8 kb =
-          *reinterpret_cast<const bf16x8 *>(base + (j * 16 + fr) * ld + dp + fc + k0);
+      const size_t koff = (j * 16 + fr) * ld + dp + fc + k0;
+      const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(base + koff);
       acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kb, acc[j], 0, 0, 0);
+      if constexpr (SPLIT) {
+        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(qk_lo + pos + koff);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kl, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, kb, acc[j], 0, 0, 0);
+      }
     }
   }
 #pragma unroll
@@ -54,11 +66,14 @@ __global__ __launch_bounds__(256) void PolicyMapKernel(
   // six dot products per wave.
   for (int d = wave; d < 24; d += 4) {
     const int t = d / 8, tf = d % 8;
-    const std::uint16_t *krow = base + (56 + tf) * ld + dp;
+    const size_t koff = (56 + tf) * ld + dp;
     float s = 0.f;
-    for (int c = lane; c < dp; c += 64)
-      s += bf16_to_f32(krow[c]) *
-           (promo[static_cast<size_t>(t) * dp + c] + promo[static_cast<size_t>(3) * dp + c]);
+    for (int c = lane; c < dp; c += 64) {
+      float kv = bf16_to_f32(base[koff + c]);
+      if constexpr (SPLIT)
+        kv += bf16_to_f32(qk_lo[pos + koff + c]);
+      s += kv * (promo[static_cast<size_t>(t) * dp + c] + promo[static_cast<size_t>(3) * dp + c]);
+    }
     s = wave_sum(s);
     if (lane == 0)
       pk_term[t * 8 + tf] = s;
@@ -82,18 +97,23 @@ __global__ __launch_bounds__(256) void PolicyMapKernel(
 
 }  // namespace
 
-hipError_t LaunchPolicyMap(const std::uint16_t *qk, int batch, int dp, const float *promo,
-                           const std::int16_t *gather, float *policy, hipStream_t stream,
-                           std::string *err) {
+hipError_t LaunchPolicyMap(const std::uint16_t *qk, const std::uint16_t *qk_lo, int batch,
+                           int dp, const float *promo, const std::int16_t *gather,
+                           float *policy, hipStream_t stream, std::string *err) {
   if (batch <= 0 || dp <= 0 || dp % 32 || !qk || !promo || !gather || !policy ||
-      (reinterpret_cast<std::uintptr_t>(qk) & 15u)) {
+      (reinterpret_cast<std::uintptr_t>(qk) & 15u) ||
+      (qk_lo && (reinterpret_cast<std::uintptr_t>(qk_lo) & 15u))) {
     if (err)
       *err = "policy_map: needs batch > 0, Dp % 32 == 0 and 16-byte aligned Q|K";
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(dp));
-  hipLaunchKernelGGL(PolicyMapKernel, dim3(batch), dim3(256), 0, stream, qk, dp, scale,
-                     promo, gather, policy);
+  if (qk_lo)
+    hipLaunchKernelGGL(PolicyMapKernel<true>, dim3(batch), dim3(256), 0, stream, qk, qk_lo, dp,
+                       scale, promo, gather, policy);
+  else
+    hipLaunchKernelGGL(PolicyMapKernel<false>, dim3(batch), dim3(256), 0, stream, qk, qk_lo, dp,
+                       scale, promo, gather, policy);
   return hipGetLastError();
 }
 

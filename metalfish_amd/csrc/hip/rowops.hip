@@ -17,7 +17,8 @@ constexpr int kPePlanes = 12;
 // (cpu_network.cpp:711-731, 777-790).
 __global__ void ExpandInputsKernel(const std::uint64_t *__restrict__ masks,
                                    const float *__restrict__ values, int batch,
-                                   std::uint16_t *__restrict__ emb_in, int emb_ld,
+                                   std::uint16_t *__restrict__ emb_in,
+                                   std::uint16_t *__restrict__ emb_in_lo, int emb_ld,
                                    std::uint16_t *__restrict__ pos_in) {
   const int chunks = emb_ld / 8;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -44,6 +45,12 @@ __global__ void ExpandInputsKernel(const std::uint64_t *__restrict__ masks,
     packed.w = out[6] | (static_cast<std::uint32_t>(out[7]) << 16);
     *reinterpret_cast<uint4 *>(emb_in + static_cast<size_t>(row) * emb_ld + chunk * 8) =
         packed;
+    if (emb_in_lo) {
+      // Plane values (0/1, small integers) are exact in bf16: zero residual.
+      const uint4 zero = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4 *>(emb_in_lo + static_cast<size_t>(row) * emb_ld + chunk * 8) =
+          zero;
+    }
   }
   // PE input: [b][sq*12 + p] for p < 12.
   const int pos_total = batch * kSquares * kPePlanes;
@@ -70,58 +77,101 @@ __global__ void UnpackPlanesKernel(const std::uint64_t *__restrict__ masks,
 }
 
 __global__ void ScatterPeKernel(const float *__restrict__ pe, int batch, int pe_ch,
-                                std::uint16_t *__restrict__ emb_in, int emb_ld) {
+                                std::uint16_t *__restrict__ emb_in,
+                                std::uint16_t *__restrict__ emb_in_lo, int emb_ld) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= batch * kSquares * pe_ch)
     return;
   const int c = idx % pe_ch;
   const int row = idx / pe_ch;  // b*64 + sq, and pe is [b][sq*pe_ch + c]
-  emb_in[static_cast<size_t>(row) * emb_ld + kPlanes + c] = f32_to_bf16(pe[idx]);
+  const size_t off = static_cast<size_t>(row) * emb_ld + kPlanes + c;
+  const std::uint16_t hi = f32_to_bf16(pe[idx]);
+  emb_in[off] = hi;
+  if (emb_in_lo)
+    emb_in_lo[off] = f32_to_bf16(pe[idx] - bf16_to_f32(hi));
 }
 
-// One wave per row.  Statistics in fp32 with the reference formula
-// var = E[x^2] - mean^2 clamped at 0, inv_std = 1 / sqrt(var + eps).
-__global__ __launch_bounds__(256) void LayerNormKernel(
-    const float *__restrict__ x, int rows, int width, float eps,
-    const float *__restrict__ gamma, const float *__restrict__ beta,
-    const float *__restrict__ mult, const float *__restrict__ add,
-    float *__restrict__ y32, std::uint16_t *__restrict__ y16) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows)
-    return;
-  const float *xr = x + static_cast<size_t>(row) * width;
+// Row LayerNorm.  T threads per row (64: one wave, 256: one workgroup);
+// each thread keeps its <= kMaxPerThread values in registers.  The input is
+// the sum of `parts` partial rows plus bias, through the activation, as
+// produced by a split-K GEMM; statistics in fp32 with the reference formula
+// var = E[x^2] - mean^2 clamped at 0, inv_std = 1 / sqrt(var + eps)
+// (cpu_network.cpp:424-460).
+constexpr int kMaxPerThread = 32;
+
+template <int T>
+__global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
+  constexpr int kRowsPerBlock = 256 / T;
+  __shared__ float red[2][4];
+  const int t = threadIdx.x % T;
+  const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / T;
+  const bool active = row < lp.rows;
+  const int width = lp.width;
+  const size_t plane = static_cast<size_t>(lp.rows) * width;
+  float v[kMaxPerThread];
   float s = 0.f, ss = 0.f;
-  for (int c = lane; c < width; c += 64) {
-    const float v = xr[c];
-    s += v;
-    ss += v * v;
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int c = i * T + t;
+    float x = 0.f;
+    if (active && c < width) {
+      const size_t off = static_cast<size_t>(row) * width + c;
+      x = lp.x[off];
+      for (int part = 1; part < lp.parts; ++part)
+        x += lp.x[part * plane + off];
+      if (lp.bias)
+        x += lp.bias[c];
+      x = activate(x, lp.act);
+      s += x;
+      ss += x * x;
+    }
+    v[i] = x;
   }
   s = wave_sum(s);
   ss = wave_sum(ss);
+  if (T == 256) {
+    if ((threadIdx.x & 63) == 0) {
+      red[0][threadIdx.x >> 6] = s;
+      red[1][threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    s = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    ss = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  }
+  if (!active)
+    return;
   const float mean = s / static_cast<float>(width);
   float var = ss / static_cast<float>(width) - mean * mean;
   var = var < 0.f ? 0.f : var;
-  const float inv_std = 1.f / sqrtf(var + eps);
+  const float inv_std = 1.f / sqrtf(var + lp.eps);
   const int sq = row % kSquares;
-  for (int c = lane; c < width; c += 64) {
-    float v = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
-    if (mult)
-      v = v * mult[static_cast<size_t>(c) * kSquares + sq];
-    if (add)
-      v = v + add[static_cast<size_t>(c) * kSquares + sq];
-    if (y32)
-      y32[static_cast<size_t>(row) * width + c] = v;
-    if (y16)
-      y16[static_cast<size_t>(row) * width + c] = f32_to_bf16(v);
+#pragma unroll
+  for (int i = 0; i < kMaxPerThread; ++i) {
+    const int c = i * T + t;
+    if (c >= width)
+      break;
+    float y = (v[i] - mean) * inv_std * lp.gamma[c] + lp.beta[c];
+    if (lp.mult_gate)
+      y = y * lp.mult_gate[static_cast<size_t>(c) * kSquares + sq];
+    if (lp.add_gate)
+      y = y + lp.add_gate[static_cast<size_t>(c) * kSquares + sq];
+    const size_t off = static_cast<size_t>(row) * width + c;
+    if (lp.y_f32)
+      lp.y_f32[off] = y;
+    if (lp.y_bf16) {
+      const std::uint16_t hi = f32_to_bf16(y);
+      lp.y_bf16[off] = hi;
+      if (lp.y_bf16_lo)
+        lp.y_bf16_lo[off] = f32_to_bf16(y - bf16_to_f32(hi));
+    }
   }
 }
 
 // One wave per position: dense2 (vh -> 3 or 1) then softmax or tanh
 // (reference network_execution_plan.cpp:1098-1106, cpu_network.cpp:336-351).
 __global__ __launch_bounds__(256) void ValueHeadKernel(
-    const float *__restrict__ hidden, int batch, int vh,
-    const float *__restrict__ w2, const float *__restrict__ b2, int wdl,
+    const float *__restrict__ hidden, int parts, const float *__restrict__ b1, int act,
+    int batch, int vh, const float *__restrict__ w2, const float *__restrict__ b2, int wdl,
     float *__restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -130,8 +180,14 @@ __global__ __launch_bounds__(256) void ValueHeadKernel(
   const int outs = wdl ? 3 : 1;
   const float *h = hidden + static_cast<size_t>(b) * vh;
   float acc[3] = {0.f, 0.f, 0.f};
+  const size_t plane = static_cast<size_t>(batch) * vh;
   for (int c = lane; c < vh; c += 64) {
-    const float v = h[c];
+    float v = h[c];
+    for (int part = 1; part < parts; ++part)
+      v += h[part * plane + c];
+    if (b1)
+      v += b1[c];
+    v = activate(v, act);
     for (int o = 0; o < outs; ++o)
       acc[o] += v * w2[static_cast<size_t>(o) * vh + c];
   }
@@ -160,8 +216,8 @@ std::string Fail(std::string *err, const char *what) {
 }  // namespace
 
 hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
-                              int batch, std::uint16_t *emb_in, int emb_ld,
-                              std::uint16_t *pos_in, hipStream_t stream,
+                              int batch, std::uint16_t *emb_in, std::uint16_t *emb_in_lo,
+                              int emb_ld, std::uint16_t *pos_in, hipStream_t stream,
                               std::string *err) {
   if (batch <= 0 || emb_ld % 8 || emb_ld < kPlanes || !masks || !values || !emb_in ||
       !pos_in || (reinterpret_cast<std::uintptr_t>(emb_in) & 15u)) {
@@ -172,7 +228,7 @@ hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
   const int pos_total = batch * kSquares * kPePlanes;
   const int n = total > pos_total ? total : pos_total;
   hipLaunchKernelGGL(ExpandInputsKernel, dim3((n + 255) / 256), dim3(256), 0, stream,
-                     masks, values, batch, emb_in, emb_ld, pos_in);
+                     masks, values, batch, emb_in, emb_in_lo, emb_ld, pos_in);
   return hipGetLastError();
 }
 
@@ -190,45 +246,50 @@ hipError_t LaunchUnpackPlanes(const std::uint64_t *masks, const float *values,
 }
 
 hipError_t LaunchScatterPe(const float *pe, int batch, int pe_channels,
-                           std::uint16_t *emb_in, int emb_ld, hipStream_t stream,
-                           std::string *err) {
+                           std::uint16_t *emb_in, std::uint16_t *emb_in_lo, int emb_ld,
+                           hipStream_t stream, std::string *err) {
   if (batch <= 0 || pe_channels <= 0 || kPlanes + pe_channels > emb_ld || !pe || !emb_in) {
     Fail(err, "scatter_pe: invalid arguments");
     return hipErrorInvalidValue;
   }
   const int n = batch * kSquares * pe_channels;
   hipLaunchKernelGGL(ScatterPeKernel, dim3((n + 255) / 256), dim3(256), 0, stream, pe,
-                     batch, pe_channels, emb_in, emb_ld);
+                     batch, pe_channels, emb_in, emb_in_lo, emb_ld);
   return hipGetLastError();
 }
 
-hipError_t LaunchLayerNorm(const float *x, int rows, int width, float eps,
-                           const float *gamma, const float *beta,
-                           const float *mult_gate, const float *add_gate,
-                           float *y_f32, std::uint16_t *y_bf16, hipStream_t stream,
-                           std::string *err) {
-  if (rows <= 0 || width <= 0 || !x || !gamma || !beta || (!y_f32 && !y_bf16)) {
+hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::string *err) {
+  if (lp.rows <= 0 || lp.width <= 0 || lp.parts < 1 || !lp.x || !lp.gamma || !lp.beta ||
+      (!lp.y_f32 && !lp.y_bf16)) {
     Fail(err, "layernorm: invalid arguments");
     return hipErrorInvalidValue;
   }
-  if ((mult_gate || add_gate) && rows % kSquares) {
+  if ((lp.mult_gate || lp.add_gate) && lp.rows % kSquares) {
     Fail(err, "layernorm: gates need square rows");
     return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(LayerNormKernel, dim3((rows + 3) / 4), dim3(256), 0, stream, x, rows,
-                     width, eps, gamma, beta, mult_gate, add_gate, y_f32, y_bf16);
+  // The thread count per row depends on the width only, so a row's
+  // reduction order (and result bits) never depends on the batch size.
+  if (lp.width <= 64 * kMaxPerThread) {
+    hipLaunchKernelGGL(LayerNormKernel<64>, dim3((lp.rows + 3) / 4), dim3(256), 0, stream, lp);
+  } else if (lp.width <= 256 * kMaxPerThread) {
+    hipLaunchKernelGGL(LayerNormKernel<256>, dim3(lp.rows), dim3(256), 0, stream, lp);
+  } else {
+    Fail(err, "layernorm: row wider than 8192");
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
-hipError_t LaunchValueHead(const float *hidden, int batch, int vh, const float *w2,
-                           const float *b2, int wdl, float *out, hipStream_t stream,
-                           std::string *err) {
-  if (batch <= 0 || vh <= 0 || !hidden || !w2 || !b2 || !out) {
+hipError_t LaunchValueHead(const float *hidden, int parts, const float *b1, int act,
+                           int batch, int vh, const float *w2, const float *b2, int wdl,
+                           float *out, hipStream_t stream, std::string *err) {
+  if (batch <= 0 || vh <= 0 || parts < 1 || !hidden || !w2 || !b2 || !out) {
     Fail(err, "value_head: invalid arguments");
     return hipErrorInvalidValue;
   }
   hipLaunchKernelGGL(ValueHeadKernel, dim3((batch + 3) / 4), dim3(256), 0, stream, hidden,
-                     batch, vh, w2, b2, wdl, out);
+                     parts, b1, act, batch, vh, w2, b2, wdl, out);
   return hipGetLastError();
 }
 

@@ -4,6 +4,12 @@ Gates (BASELINE north_star): input planes and the policy index map bit-exact;
 policy logits max-abs <= 2e-2 and the same top-1 move on >= 99.5% of
 positions; WDL max-abs <= 5e-3 (the reference's cross-backend gate,
 tools/compare_nn_backend_outputs.py:21-22).
+
+The default precision ("bf16x2": activations as bf16 hi + lo pairs) meets all
+of them.  The single-pass "bf16" mode meets the max-abs gates; on these
+random-init nets the legal-move logits of many positions are within a few
+1e-3 of each other, below single-bf16 rounding noise, so its top-1 agreement
+is reported rather than gated.
 """
 
 import numpy as np
@@ -64,13 +70,26 @@ def test_unpacked_planes_bit_exact():
     assert np.array_equal(got.view(np.uint32), planes.view(np.uint32))
 
 
-def _compare(spec_name, n, seed=0, first_game=0, check_packed=True):
+_REF_CACHE = {}
+
+
+def _reference(spec_name, n, seed, first_game):
+    key = (spec_name, n, seed, first_game)
+    if key not in _REF_CACHE:
+        spec = synth.SPECS[spec_name]
+        weights = synth.make_weights(spec, seed=seed)
+        planes, legal = synth.playout_positions(n, seed=seed, first_game=first_game)
+        ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads),
+                               weights).evaluate_batch(planes)
+        _REF_CACHE[key] = (weights, planes, legal, ref)
+    return _REF_CACHE[key]
+
+
+def _compare(spec_name, n, seed=0, first_game=0, check_packed=True, precision="bf16x2"):
     spec = synth.SPECS[spec_name]
-    weights = synth.make_weights(spec, seed=seed)
-    planes, legal = synth.playout_positions(n, seed=seed, first_game=first_game)
-    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads), weights).evaluate_batch(
-        planes)
-    net = backend.create_network(spec, weights, max_batch=max(n, 1), device=0)
+    weights, planes, legal, ref = _reference(spec_name, n, seed, first_game)
+    net = backend.create_network(spec, weights, max_batch=max(n, 1), device=0,
+                                 precision=precision)
     gpu = net.evaluate_batch(planes)
     if check_packed:
         masks, values = oracle.pack_planes(planes)
@@ -89,26 +108,33 @@ def _top1_agreement(gpu_policy, ref_policy, legal):
     return agree / gpu_policy.shape[0]
 
 
-def test_cpu_plumbing_net_parity():
-    gpu, ref, legal = _compare("cpu_plumbing", 16)
-    perr = np.abs(gpu["policy"] - ref["policy"]).max()
-    werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
-    print(f"cpu_plumbing: policy max-abs {perr:.3e} wdl max-abs {werr:.3e}")
-    assert perr <= POLICY_TOL
-    assert werr <= WDL_TOL
-    assert _top1_agreement(gpu["policy"], ref["policy"], legal) >= 0.995
-    assert np.allclose(gpu["value"], gpu["wdl"][:, 0] - gpu["wdl"][:, 2])
-
-
-def test_bt4_net_parity_16_positions():
-    gpu, ref, legal = _compare("bt4", 16, check_packed=False)
+@pytest.mark.parametrize("precision", ["bf16x2", "bf16"])
+def test_cpu_plumbing_net_parity(precision):
+    gpu, ref, legal = _compare("cpu_plumbing", 16, precision=precision)
     perr = np.abs(gpu["policy"] - ref["policy"]).max()
     werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
     top1 = _top1_agreement(gpu["policy"], ref["policy"], legal)
-    print(f"bt4: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}")
+    print(f"cpu_plumbing {precision}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} "
+          f"top1 {top1:.3f}")
     assert perr <= POLICY_TOL
     assert werr <= WDL_TOL
-    assert top1 >= 0.995
+    if precision == "bf16x2":
+        assert perr <= 1e-3
+        assert top1 >= 0.995
+    assert np.allclose(gpu["value"], gpu["wdl"][:, 0] - gpu["wdl"][:, 2])
+
+
+@pytest.mark.parametrize("precision", ["bf16x2", "bf16"])
+def test_bt4_net_parity_16_positions(precision):
+    gpu, ref, legal = _compare("bt4", 16, check_packed=False, precision=precision)
+    perr = np.abs(gpu["policy"] - ref["policy"]).max()
+    werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
+    top1 = _top1_agreement(gpu["policy"], ref["policy"], legal)
+    print(f"bt4 {precision}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}")
+    assert perr <= POLICY_TOL
+    assert werr <= WDL_TOL
+    if precision == "bf16x2":
+        assert top1 >= 0.995
 
 
 def test_batch_invariance_and_chunking():
@@ -120,8 +146,11 @@ def test_batch_invariance_and_chunking():
     planes, _ = synth.playout_positions(40, seed=3)
     net = backend.create_network(spec, weights, max_batch=16, device=0)
     full = net.evaluate_batch(planes)  # chunks 16 + 16 + 8
-    single = np.stack([net.evaluate(planes[i])["policy"] for i in (0, 17, 39)])
-    assert np.allclose(single, full["policy"][[0, 17, 39]], atol=1e-5)
+    single = [net.evaluate(planes[i]) for i in (0, 17, 39)]
+    # Per-position arithmetic never depends on the batch: bit-identical.
+    for k, i in enumerate((0, 17, 39)):
+        assert np.array_equal(single[k]["policy"], full["policy"][i])
+        assert np.array_equal(single[k]["wdl"], full["wdl"][i])
     net.close()
 
 
