@@ -1,0 +1,149 @@
+#include "hip_network.h"
+
+#include <cmath>
+#include <stdexcept>
+
+namespace MetalFish {
+namespace NN {
+namespace Hip {
+namespace {
+
+std::string LastError(const char *what, int rc) {
+  return std::string("HIP backend ") + what + " failed (" + std::to_string(rc) +
+         "): " + mfh_last_error();
+}
+
+// Output sanity check, as the CUDA backend applies before trusting a batch
+// (reference src/nn/cuda/cuda_network.cpp:199-231): finite logits and WDL
+// probabilities that sum to about one.
+bool OutputsValid(const float *policy, const float *value, int count, bool wdl) {
+  for (int i = 0; i < count * kPolicyOutputs; ++i)
+    if (!std::isfinite(policy[i]))
+      return false;
+  for (int b = 0; b < count; ++b) {
+    if (wdl) {
+      const float *v = value + 3 * b;
+      const float sum = v[0] + v[1] + v[2];
+      if (!std::isfinite(sum) || sum < 0.5f || sum > 1.5f)
+        return false;
+    } else if (!std::isfinite(value[b])) {
+      return false;
+    }
+  }
+  return true;
+}
+
+}  // namespace
+
+HipNetwork::HipNetwork(const std::vector<WeightTensor> &weights,
+                       const HipNetworkConfig &config) {
+  std::vector<mfh_tensor> tensors;
+  tensors.reserve(weights.size());
+  for (const auto &w : weights)
+    tensors.push_back(mfh_tensor{w.name.c_str(), w.data, static_cast<std::uint64_t>(w.elements)});
+  mfh_net_desc desc{};
+  desc.network = config.network;
+  desc.policy = config.policy;
+  desc.value = config.value;
+  desc.moves_left = config.moves_left;
+  desc.input_embedding = config.input_embedding;
+  desc.default_activation = config.default_activation;
+  desc.ffn_activation = config.ffn_activation;
+  desc.smolgen_activation = config.smolgen_activation;
+  desc.headcount = config.headcount;
+  desc.weights_dtype = MFH_WEIGHTS_BF16;
+  desc.precision = config.precision;
+  desc.max_batch = config.max_batch;
+  desc.device = config.device;
+  const int rc = mfh_net_create(&desc, tensors.data(), static_cast<int>(tensors.size()), &net_);
+  if (rc != MFH_OK)
+    throw std::runtime_error(LastError("initialisation", rc));
+  wdl_ = config.value == MFH_VALUE_WDL;
+  max_batch_ = config.max_batch;
+  policy_.resize(static_cast<std::size_t>(max_batch_) * kPolicyOutputs);
+  value_.resize(static_cast<std::size_t>(max_batch_) * 3);
+}
+
+HipNetwork::~HipNetwork() { mfh_net_destroy(net_); }
+
+void HipNetwork::RunChunk(const InputPlanes *inputs, int count, NetworkOutput *outputs) {
+  // InputPlanes is a contiguous 112x64 float array, so a run of them is the
+  // planes[count*112*64] layout the C ABI takes.
+  const float *planes = inputs[0][0].data();
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    const int rc = mfh_net_eval_planes(net_, count, planes, policy_.data(), value_.data(), nullptr);
+    if (rc != MFH_OK) {
+      if (attempt == 0)
+        continue;
+      throw std::runtime_error(LastError("evaluation", rc));
+    }
+    if (!OutputsValid(policy_.data(), value_.data(), count, wdl_)) {
+      if (attempt == 0)
+        continue;
+      throw std::runtime_error("HIP backend produced invalid outputs (non-finite or WDL "
+                               "not normalised) twice");
+    }
+    break;
+  }
+  // DecodeNetworkOutputBatch (reference src/nn/network_output_decoder.cpp:
+  // 31-78): raw logits, WDL, value = W - L.
+  for (int b = 0; b < count; ++b) {
+    NetworkOutput &out = outputs[b];
+    const float *p = policy_.data() + static_cast<std::size_t>(b) * kPolicyOutputs;
+    for (int i = 0; i < kPolicyOutputs; ++i)
+      out.policy[i] = p[i];
+    if (wdl_) {
+      out.has_wdl = true;
+      out.wdl[0] = value_[3 * b];
+      out.wdl[1] = value_[3 * b + 1];
+      out.wdl[2] = value_[3 * b + 2];
+      out.value = out.wdl[0] - out.wdl[2];
+    } else {
+      out.has_wdl = false;
+      out.value = value_[b];
+      out.wdl[0] = out.wdl[1] = out.wdl[2] = 0.0f;
+    }
+    out.has_moves_left = false;
+    out.moves_left = 0.0f;
+  }
+}
+
+NetworkOutput HipNetwork::Evaluate(const InputPlanes &input) {
+  NetworkOutput out;
+  RunChunk(&input, 1, &out);
+  return out;
+}
+
+std::vector<NetworkOutput> HipNetwork::EvaluateBatch(const std::vector<InputPlanes> &inputs) {
+  std::vector<NetworkOutput> outputs(inputs.size());
+  for (std::size_t start = 0; start < inputs.size(); start += max_batch_) {
+    const int count = static_cast<int>(std::min<std::size_t>(max_batch_, inputs.size() - start));
+    RunChunk(inputs.data() + start, count, outputs.data() + start);
+  }
+  return outputs;
+}
+
+std::string HipNetwork::GetNetworkInfo() const {
+  char buf[1024];
+  if (mfh_net_info(net_, buf, sizeof(buf)) != MFH_OK)
+    return "HIP transformer backend";
+  return buf;
+}
+
+BackendCapabilities HipNetwork::GetBackendCapabilities() const {
+  BackendCapabilities caps;
+  mfh_capabilities c{};
+  caps.actual_backend = "hip";
+  if (mfh_net_capabilities(net_, &c) == MFH_OK) {
+    caps.has_wdl = c.has_wdl != 0;
+    caps.has_moves_left = c.has_moves_left != 0;
+    caps.max_batch_size = c.max_batch_size;
+    caps.stable_execution_batch_size = c.max_batch_size;
+    caps.device_name = std::string(c.device_name) + " (" + c.arch_name + ")";
+  }
+  return caps;
+}
+
+}  // namespace Hip
+}  // namespace NN
+}  // namespace MetalFish

@@ -1,0 +1,73 @@
+// HipNetwork: MetalFish's NN::Network implemented on the MI355X C ABI
+// (include/mfhip.h).  Counterpart of the CUDA backend's CudaNetwork
+// (reference src/nn/cuda/cuda_network.h, cuda_network.cpp:235-459): the
+// constructor packs and uploads the weights, EvaluateBatch chunks the batch
+// to the device's maximum, packs planes into pinned staging buffers and runs
+// the forward on the net's stream, and a failed or invalid result is retried
+// once before a std::runtime_error is thrown.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "mfhip.h"
+#include "nn_network.h"
+
+namespace MetalFish {
+namespace NN {
+namespace Hip {
+
+// One weight tensor as the reference's NetworkWeightTensorView exposes it
+// (reference src/nn/network_weight_inventory.h:33-44): inventory name, fp32
+// data, element count.
+struct WeightTensor {
+  std::string name;
+  const float *data = nullptr;
+  std::size_t elements = 0;
+};
+
+// Format fields of the weights file (reference NetworkFormat, values as in
+// net.proto) and the HIP-specific knobs a BackendConfig would carry.
+struct HipNetworkConfig {
+  int network = MFH_NETWORK_ATTENTIONBODY_WITH_MULTIHEADFORMAT;
+  int policy = MFH_POLICY_ATTENTION;
+  int value = MFH_VALUE_WDL;
+  int moves_left = 0;
+  int input_embedding = MFH_INPUT_EMBEDDING_PE_DENSE;
+  int default_activation = MFH_DEFAULT_ACTIVATION_MISH;
+  int ffn_activation = MFH_ACTIVATION_DEFAULT;
+  int smolgen_activation = MFH_ACTIVATION_SWISH;
+  int headcount = 0;
+  int precision = MFH_PRECISION_BF16X2;
+  int max_batch = 256;  // stable execution batch; larger batches are chunked
+  int device = -1;
+};
+
+class HipNetwork : public Network {
+public:
+  HipNetwork(const std::vector<WeightTensor> &weights, const HipNetworkConfig &config);
+  ~HipNetwork() override;
+  HipNetwork(const HipNetwork &) = delete;
+  HipNetwork &operator=(const HipNetwork &) = delete;
+
+  NetworkOutput Evaluate(const InputPlanes &input) override;
+  std::vector<NetworkOutput> EvaluateBatch(const std::vector<InputPlanes> &inputs) override;
+  std::string GetNetworkInfo() const override;
+  bool HasWDL() const override { return wdl_; }
+  bool HasMovesLeft() const override { return false; }
+  BackendCapabilities GetBackendCapabilities() const override;
+
+private:
+  void RunChunk(const InputPlanes *inputs, int count, NetworkOutput *outputs);
+
+  mfh_net *net_ = nullptr;
+  bool wdl_ = true;
+  int max_batch_ = 0;
+  std::vector<float> policy_;
+  std::vector<float> value_;
+};
+
+}  // namespace Hip
+}  // namespace NN
+}  // namespace MetalFish
