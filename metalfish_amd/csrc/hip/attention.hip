@@ -3,18 +3,28 @@
 // restating reference src/nn/cpu/cpu_network.cpp:1175-1254.
 //
 // One wave owns one (position, head); a workgroup holds 4 heads of one
-// position.  S = Q K^T is 16 v_mfma_f32_16x16x32_bf16 (the K dimension of the
-// MFMA is exactly the head depth); the softmax runs on the accumulator layout
-// with 16-lane shuffles; P (bf16) and V^T are staged in LDS and O = P V is 16
-// more MFMAs.  Scores, softmax statistics and accumulation stay in fp32.
+// position.  The wave computes the transposed scores S^T = K Q^T with
+// v_mfma_f32_16x16x32_bf16 (the MFMA's K dimension is exactly the head
+// depth), K and Q fragments coming straight from HBM as 16-byte loads.  In
+// that layout a lane holds, for one query, four consecutive keys of every
+// 16-key tile, so:
+//   * the smolgen bias for those keys is one 16-byte (fp32) or 8-byte (bf16)
+//     load;
+//   * the softmax over a query's 64 keys is 16 values in the lane plus two
+//     cross-lane shuffles;
+//   * the probabilities never leave registers: the eight keys a lane holds
+//     for a pair of key tiles are exactly the eight K-slots that lane feeds
+//     to the next MFMA (the MFMA sums over K, so only the pairing of P and V
+//     slots matters), and ctx^T = V^T P^T takes them as its B operand.
+// Only V^T goes through LDS (4 KiB per head, two 8-byte reads per fragment).
+// ctx^T leaves each lane with four consecutive depths of one query: one
+// 8-byte store.  Scores, softmax statistics and accumulation stay in fp32.
 //
 // Split precision: Q, K, V and the context arrive/leave as hi + lo bf16
-// planes, P is staged as hi + lo, and each product takes three MFMAs
-// (hi.hi + hi.lo + lo.hi; the lo.lo term is below fp32 resolution).
+// planes, P is split the same way in registers, and each product takes three
+// MFMAs (hi.hi + hi.lo + lo.hi; the lo.lo term is below fp32 resolution).
 #include "mfh_device.h"
 #include "mfh_kernels.h"
-
-#include <mutex>
 
 namespace mfh {
 namespace {
@@ -22,27 +32,26 @@ namespace {
 constexpr int kSq = 64;
 constexpr int kDepth = 32;
 constexpr int kHeadsPerBlock = 4;
+// V^T rows: 64 keys plus 8 of padding, so the two halves of a wave writing
+// depths d and d + 16 land on different banks.
+constexpr int kVtStride = kSq + 8;
 
-// 64-column bf16 tiles in LDS: 8 chunks of 16 bytes per row, chunk index
-// XOR-swizzled by row for conflict-free ds_read_b128 fragment loads.
-__device__ __forceinline__ int Swz(int row, int col) {
-  return row * 64 + ((((col >> 3) ^ (row & 7))) << 3) + (col & 7);
-}
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 Mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ bf16x8 Join(u32x2 a, u32x2 b) {
+  const u32x4 v{a[0], a[1], b[0], b[1]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 template <bool SPLIT, bool BIAS_F32>
 __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   constexpr int PLANES = SPLIT ? 2 : 1;
-  // Dynamic LDS: P planes [4][PLANES][64*64] then V^T planes [4][PLANES][32*64].
-  extern __shared__ __attribute__((aligned(16))) std::uint16_t smem[];
-  typedef std::uint16_t PTile[PLANES][kSq * kSq];
-  typedef std::uint16_t VTile[PLANES][kDepth * kSq];
-  PTile *p_lds = reinterpret_cast<PTile *>(smem);
-  VTile *vt_lds = reinterpret_cast<VTile *>(smem + kHeadsPerBlock * PLANES * kSq * kSq);
-
+  __shared__ __attribute__((aligned(16))) std::uint16_t vt_lds[kHeadsPerBlock][PLANES]
+                                                                [kDepth * kVtStride];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int heads = ap.heads;
@@ -53,166 +62,197 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   const size_t ld = static_cast<size_t>(3) * E;
   const size_t pos = static_cast<size_t>(b) * kSq * ld;
   const int qcol = h * kDepth, kcol = E + h * kDepth, vcol = 2 * E + h * kDepth;
+  const int fr = lane & 15, g = lane >> 4;
 
-  // V^T into LDS: each lane moves 4 chunks of 8 depths for one key.
+  // V^T into LDS.  Lane l handles the key pair 2 (l % 32), 2 (l % 32) + 1
+  // and depths 16 (l / 32) .. + 16, writing one packed dword per depth.
+  {
+    const int kp = lane & 31, dh = (lane >> 5) * 16;
 #pragma unroll
-  for (int pl = 0; pl < PLANES; ++pl) {
-    const std::uint16_t *base = (pl ? ap.qkv_lo : ap.qkv) + pos;
-    std::uint16_t *vt = vt_lds[wave][pl];
+    for (int pl = 0; pl < PLANES; ++pl) {
+      const std::uint16_t *base = (pl ? ap.qkv_lo : ap.qkv) + pos + vcol + dh;
+      const u32x4 *r0 = reinterpret_cast<const u32x4 *>(base + (2 * kp) * ld);
+      const u32x4 *r1 = reinterpret_cast<const u32x4 *>(base + (2 * kp + 1) * ld);
+      const u32x4 a0 = r0[0], a1 = r0[1], c0 = r1[0], c1 = r1[1];
+      std::uint32_t *vt = reinterpret_cast<std::uint32_t *>(vt_lds[wave][pl]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = lane + i * 64;  // 256 chunks = 64 keys x 4 chunks
-      const int key = c >> 2, d0 = (c & 3) * 8;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(base + key * ld + vcol + d0);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        vt[Swz(d0 + e, key)] = static_cast<std::uint16_t>(v[e >> 1] >> ((e & 1) * 16));
+      for (int e = 0; e < 16; ++e) {
+        const std::uint32_t x = (e < 8 ? a0 : a1)[(e & 7) >> 1];
+        const std::uint32_t y = (e < 8 ? c0 : c1)[(e & 7) >> 1];
+        const std::uint32_t lo = (e & 1) ? (x >> 16) : (x & 0xFFFFu);
+        const std::uint32_t hi = (e & 1) ? (y >> 16) : (y & 0xFFFFu);
+        vt[((dh + e) * kVtStride) / 2 + kp] = lo | (hi << 16);
+      }
     }
   }
 
-  // S = Q K^T.
-  const int fr = lane & 15, fc = (lane >> 4) * 8;
+  // S^T = K Q^T: tile (t, s) holds keys 16 t + 4 g + r (rows) for queries
+  // 16 s + fr (columns).
   const std::uint16_t *qh = ap.qkv + pos;
-  bf16x8 qa[4], kb[4];
+  bf16x8 kf[4], qf[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    qa[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + qcol + fc);
-    kb[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + kcol + fc);
+    kf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + kcol + g * 8);
+    qf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + qcol + g * 8);
   }
-  f32x4 s[4][4];
+  f32x4 s[4][4];  // [t][s]
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      s[i][j] = Mfma(qa[i], kb[j], f32x4{0.f, 0.f, 0.f, 0.f});
+    for (int q = 0; q < 4; ++q)
+      s[t][q] = Mfma(kf[t], qf[q], f32x4{0.f, 0.f, 0.f, 0.f});
   if constexpr (SPLIT) {
     const std::uint16_t *ql = ap.qkv_lo + pos;
-    bf16x8 qlo[4], klo[4];
+    bf16x8 kl[4], qlo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      qlo[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + qcol + fc);
-      klo[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + kcol + fc);
+      kl[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + kcol + g * 8);
+      qlo[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + qcol + g * 8);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        s[i][j] = Mfma(qlo[i], kb[j], Mfma(qa[i], klo[j], s[i][j]));
+      for (int q = 0; q < 4; ++q)
+        s[t][q] = Mfma(kl[t], qf[q], Mfma(kf[t], qlo[q], s[t][q]));
   }
 
-  // Scale, add the smolgen bias, softmax over keys.  Lane holds rows
-  // q = 16 i + 4 (lane / 16) + r, key = 16 j + lane % 16.
+  // Scale, bias, softmax over the 64 keys of each query 16 q + fr; the lane
+  // holds 16 of them, lanes fr, fr + 16, fr + 32, fr + 48 hold the rest.
   const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
   const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
+  bf16x8 pf[4][2], pl[4][2];  // [query tile][key-tile pair]: B operands of ctx^T
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int q = 0; q < 4; ++q) {
+    const int query = q * 16 + fr;
+    float v[4][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int q = i * 16 + (lane >> 4) * 4 + r;
-      float v[4];
+    for (int t = 0; t < 4; ++t) {
+      const int key0 = t * 16 + g * 4;
+      float bb[4] = {0.f, 0.f, 0.f, 0.f};
+      if (ap.bias) {
+        if constexpr (BIAS_F32) {
+          const f32x4 x = *reinterpret_cast<const f32x4 *>(
+              static_cast<const float *>(ap.bias) + bias_off + query * kSq + key0);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = s[i][j][r] * scale;
-        if (ap.bias) {
-          const int bi = q * kSq + j * 16 + fr;
-          if constexpr (BIAS_F32)
-            v[j] += static_cast<const float *>(ap.bias)[bias_off + bi];
-          else
-            v[j] += bf16_to_f32(static_cast<const std::uint16_t *>(ap.bias)[bias_off + bi]);
+          for (int r = 0; r < 4; ++r)
+            bb[r] = x[r];
+        } else {
+          const u32x2 x = *reinterpret_cast<const u32x2 *>(
+              static_cast<const std::uint16_t *>(ap.bias) + bias_off + query * kSq + key0);
+          bb[0] = __uint_as_float(x[0] << 16);
+          bb[1] = __uint_as_float(x[0] & 0xFFFF0000u);
+          bb[2] = __uint_as_float(x[1] << 16);
+          bb[3] = __uint_as_float(x[1] & 0xFFFF0000u);
         }
       }
-      float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1)
-        m = fmaxf(m, __shfl_xor(m, o, 64));
-      float sum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[j] = __expf(v[j] - m);
-        sum += v[j];
-      }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1)
-        sum += __shfl_xor(sum, o, 64);
-      const float inv = 1.f / sum;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p = v[j] * inv;
-        const std::uint16_t hi = f32_to_bf16(p);
-        p_lds[wave][0][Swz(q, j * 16 + fr)] = hi;
-        if constexpr (SPLIT)
-          p_lds[wave][PLANES - 1][Swz(q, j * 16 + fr)] = f32_to_bf16(p - bf16_to_f32(hi));
-      }
+      for (int r = 0; r < 4; ++r)
+        v[t][r] = s[t][q][r] * scale + bb[r];
     }
-  __syncthreads();
-
-  // O = P V: M = 64 queries, N = 32 depths, K = 64 keys.
-  f32x4 o[4][2];
+    float m = v[0][0];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      o[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < 4; ++r)
+        m = fmaxf(m, v[t][r]);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float sum = 0.f;
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    bf16x8 pa[4], vb[2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      pa[i] = *reinterpret_cast<const bf16x8 *>(&p_lds[wave][0][Swz(i * 16 + fr, kk * 32 + fc)]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      vb[j] = *reinterpret_cast<const bf16x8 *>(&vt_lds[wave][0][Swz(j * 16 + fr, kk * 32 + fc)]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        o[i][j] = Mfma(pa[i], vb[j], o[i][j]);
-    if constexpr (SPLIT) {
-      bf16x8 pl[4], vl[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pl[i] = *reinterpret_cast<const bf16x8 *>(&p_lds[wave][1][Swz(i * 16 + fr, kk * 32 + fc)]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        vl[j] = *reinterpret_cast<const bf16x8 *>(&vt_lds[wave][1][Swz(j * 16 + fr, kk * 32 + fc)]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          o[i][j] = Mfma(pl[i], vb[j], Mfma(pa[i], vl[j], o[i][j]));
-    }
-  }
-  const size_t out_off = static_cast<size_t>(b) * kSq * E + h * kDepth;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int q = i * 16 + (lane >> 4) * 4 + r;
-        const size_t idx = out_off + static_cast<size_t>(q) * E + j * 16 + fr;
-        const std::uint16_t hi = f32_to_bf16(o[i][j][r]);
-        ap.ctx[idx] = hi;
-        if constexpr (SPLIT)
-          ap.ctx_lo[idx] = f32_to_bf16(o[i][j][r] - bf16_to_f32(hi));
+        v[t][r] = __expf(v[t][r] - m);
+        sum += v[t][r];
       }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = 1.f / sum;
+    // K-slot j of pair u: key 32 u + 4 g + (j % 4) + 16 (j / 4), i.e. tile
+    // t = 2 u + j / 4, element r = j % 4.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      std::uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const float p0 = v[2 * u + j / 4][j % 4] * inv;
+        const float p1 = v[2 * u + j / 4][j % 4 + 1] * inv;
+        const std::uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
+        hw[j / 2] = h0 | (static_cast<std::uint32_t>(h1) << 16);
+        if constexpr (SPLIT)
+          lw[j / 2] = f32_to_bf16(p0 - bf16_to_f32(h0)) |
+                      (static_cast<std::uint32_t>(f32_to_bf16(p1 - bf16_to_f32(h1))) << 16);
+      }
+      pf[q][u] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+      if constexpr (SPLIT)
+        pl[q][u] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+    }
+  }
+  __syncthreads();
+
+  // ctx^T = V^T P^T: A = V^T fragment (depth 16 dt + fr, the lane's 8 keys),
+  // B = P fragment; tile (dt, q) holds depths 16 dt + 4 g + r for query
+  // 16 q + fr.
+  f32x4 o[2][4];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      o[dt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int row = (dt * 16 + fr) * kVtStride + 32 * u + 4 * g;
+      const std::uint16_t *vh = vt_lds[wave][0];
+      const bf16x8 va = Join(*reinterpret_cast<const u32x2 *>(vh + row),
+                             *reinterpret_cast<const u32x2 *>(vh + row + 16));
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[dt][q] = Mfma(va, pf[q][u], o[dt][q]);
+      if constexpr (SPLIT) {
+        const std::uint16_t *vl = vt_lds[wave][1];
+        const bf16x8 vb = Join(*reinterpret_cast<const u32x2 *>(vl + row),
+                               *reinterpret_cast<const u32x2 *>(vl + row + 16));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          o[dt][q] = Mfma(vb, pf[q][u], Mfma(va, pl[q][u], o[dt][q]));
+      }
+    }
+  const size_t out_off = static_cast<size_t>(b) * kSq * E + h * kDepth;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const size_t idx = out_off + static_cast<size_t>(q * 16 + fr) * E + dt * 16 + g * 4;
+      std::uint16_t hi[4];
+      std::uint32_t lw[2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        hi[r] = f32_to_bf16(o[dt][q][r]);
+      *reinterpret_cast<u32x2 *>(ap.ctx + idx) =
+          u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
+                hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int r = 0; r < 4; r += 2)
+          lw[r / 2] = f32_to_bf16(o[dt][q][r] - bf16_to_f32(hi[r])) |
+                      (static_cast<std::uint32_t>(
+                           f32_to_bf16(o[dt][q][r + 1] - bf16_to_f32(hi[r + 1])))
+                       << 16);
+        *reinterpret_cast<u32x2 *>(ap.ctx_lo + idx) = u32x2{lw[0], lw[1]};
+      }
+    }
 }
 
 template <bool SPLIT, bool BIAS_F32>
 hipError_t Launch(const AttentionParams &ap, int grid, hipStream_t stream) {
-  constexpr int PLANES = SPLIT ? 2 : 1;
-  constexpr int kLds = kHeadsPerBlock * PLANES * (kSq * kSq + kDepth * kSq) * 2;
-  auto kernel = AttentionKernel<SPLIT, BIAS_F32>;
-  static std::once_flag once;
-  static hipError_t attr = hipSuccess;
-  std::call_once(once, [&]() {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-  });
-  if (attr != hipSuccess)
-    return attr;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), kLds, stream, ap);
+  hipLaunchKernelGGL((AttentionKernel<SPLIT, BIAS_F32>), dim3(grid), dim3(256), 0, stream, ap);
   return hipGetLastError();
+}
+
+bool Misaligned(const void *p, std::uintptr_t bytes) {
+  return (reinterpret_cast<std::uintptr_t>(p) & (bytes - 1)) != 0;
 }
 
 }  // namespace
@@ -220,11 +260,12 @@ hipError_t Launch(const AttentionParams &ap, int grid, hipStream_t stream) {
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::string *err) {
   const bool split = ap.qkv_lo != nullptr;
   if (ap.batch <= 0 || ap.heads <= 0 || ap.heads % kHeadsPerBlock || !ap.qkv || !ap.ctx ||
-      (reinterpret_cast<std::uintptr_t>(ap.qkv) & 15u) ||
-      (split && (!ap.ctx_lo || (reinterpret_cast<std::uintptr_t>(ap.qkv_lo) & 15u)))) {
+      Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 8) ||
+      (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
+      (split && (!ap.ctx_lo || Misaligned(ap.qkv_lo, 16) || Misaligned(ap.ctx_lo, 8)))) {
     if (err)
-      *err = "attention: needs batch > 0, heads % 4 == 0, 16-byte aligned qkv, and "
-             "lo planes for both input and output in split mode";
+      *err = "attention: needs batch > 0, heads % 4 == 0, 16-byte aligned qkv, 8-byte "
+             "aligned ctx and bias, and lo planes for both input and output in split mode";
     return hipErrorInvalidValue;
   }
   const int grid = ap.batch * (ap.heads / kHeadsPerBlock);

@@ -6,14 +6,19 @@
 // C[M,N] = A[M,K] . W[N,K]^T.  Both operands are K-contiguous (activations
 // row-major, weights in the reference's [out][in] layout).  A workgroup of
 // WM x WN waves owns a BM x BN tile; each wave owns a (BM/WM) x (BN/WN)
-// sub-tile of v_mfma_f32_16x16x32_bf16 instructions.  K advances in 64-wide
-// steps through a two-stage LDS ring filled by global_load_lds_dwordx4
-// (direct global->LDS, no VGPR round trip): the next step's tiles are in
-// flight while the current one feeds the MFMAs.  LDS rows are 128 bytes with
-// their 16-byte chunks XOR-swizzled by (row & 7), which keeps the
-// ds_read_b128 fragment reads free of bank conflicts; the swizzle is applied
+// sub-tile of v_mfma_f32_16x16x32_bf16 instructions.  K advances in BK-wide
+// steps (BK = 32 or 64) through an ST-stage LDS ring filled by
+// global_load_lds_dwordx4 (direct global->LDS, no VGPR round trip): ST - 1
+// steps' tiles are in flight while the current one feeds the MFMAs, enough
+// bytes in flight to cover the L2/HBM latency.  LDS rows
+// are BK bf16 wide with their 16-byte chunks XOR-swizzled so that the 16 rows
+// a fragment read touches spread over all bank groups; the swizzle is applied
 // on the global side (each lane fetches the chunk that belongs in its LDS
 // slot).
+//
+// The MFMA computes the transposed tile, D = W_frag . A_frag^T, so each lane
+// ends up holding four consecutive output columns of one row: the epilogue
+// stores 8 bytes (bf16) or 16 bytes (fp32) per lane instead of 2 or 4.
 //
 // Split precision: when A_lo is set, the activation is carried as
 // hi + lo bf16 planes (lo = bf16(x - hi)) and every fragment pair issues two
@@ -26,11 +31,20 @@
 namespace mfh {
 namespace {
 
-constexpr int kBK = 64;
 #define MFH_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
 
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Element offset of 16-byte chunk `chunk` of LDS row `row` (rows of BK bf16).
+// BK = 64: 8 chunks per 128-byte row, XOR with row & 7.  BK = 32: two rows
+// per 128 bytes, XOR with (row >> 1) & 3, so rows r..r+7 cover all eight
+// 16-byte bank groups.
+template <int BK>
 __device__ __forceinline__ int Swz(int row, int chunk) {
-  return row * kBK + ((chunk ^ (row & 7)) << 3);
+  if constexpr (BK == 64)
+    return row * 64 + ((chunk ^ (row & 7)) << 3);
+  else
+    return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3);
 }
 
 // Activation with a compile-time kind; ACT_RUNTIME defers to p.act.
@@ -43,14 +57,17 @@ __device__ __forceinline__ float Act(float v, int runtime_act) {
     return activate(v, ACT);
 }
 
-template <int BM, int BN, int WM, int WN, bool SPLIT, int MODE, int ACT>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 16, TN = WTN / 16;
-  constexpr int A_ROWS = SPLIT ? 2 * BM : BM;     // hi rows then lo rows
-  constexpr int STAGE = (A_ROWS + BN) * kBK;      // bf16 elements per stage
-  constexpr int LOADS = (A_ROWS + BN) * kBK * 2 / 1024;  // 1 KiB wave-loads
+  constexpr int CPR = BK / 8;                      // 16-byte chunks per LDS row
+  constexpr int RPL = 64 / CPR;                    // rows per 1 KiB wave-load
+  constexpr int A_ROWS = SPLIT ? 2 * BM : BM;      // hi rows then lo rows
+  constexpr int STAGE = (A_ROWS + BN) * BK;        // bf16 elements per stage
+  constexpr int LOADS = (A_ROWS + BN) * BK * 2 / 1024;
+  static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
   static_assert(LOADS % NWAVES == 0, "stage loads must split evenly over waves");
   constexpr int LPW = LOADS / NWAVES;
   extern __shared__ __attribute__((aligned(1024))) std::uint16_t lds[];
@@ -81,17 +98,18 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   const int kslice = p.K / p.k_splits;
   const int k_begin = blockIdx.y * kslice;
 
-  // Each lane's source pointer for its LPW wave-loads.  A wave-load fills
-  // 1 KiB = 8 rows x 128 B of LDS; lane l lands in row l/8, physical chunk
-  // l%8, so it fetches logical chunk (l%8) ^ (row & 7).  Rows past M or N
-  // read a clamped valid row: they only feed outputs that are never stored.
+  // Each lane's source pointer for its LPW wave-loads.  Lane l lands in row
+  // l / CPR of its wave-load, physical chunk l % CPR, so it fetches the
+  // logical chunk that the swizzle puts there.  Rows past M or N read a
+  // clamped valid row: they only feed outputs that are never stored.
   const std::uint16_t *src[LPW];
   int dst[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int L = wave * LPW + j;
-    const int row = L * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ (row & 7);
+    const int row = L * RPL + lane / CPR;
+    const int phys = lane % CPR;
+    const int chunk = BK == 64 ? (phys ^ (row & 7)) : (phys ^ ((row >> 1) & 3));
     if (row < BM) {
       src[j] = p.A + static_cast<size_t>(min(m0 + row, p.M - 1)) * p.lda + k_begin + chunk * 8;
     } else if (SPLIT && row < 2 * BM) {
@@ -104,13 +122,18 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     dst[j] = L * 512;
   }
 
-  const int KT = kslice / kBK;
-  // Stage 0 in flight before the loop.
+  const int KT = kslice / BK;
+  // Stages 0 .. ST-2 in flight before the loop.
 #pragma unroll
-  for (int j = 0; j < LPW; ++j)
-    __builtin_amdgcn_global_load_lds(static_cast<const void *>(src[j]),
-                                     MFH_LDS_PTR(lds + dst[j]), 16, 0, 0);
+  for (int s = 0; s < ST - 1; ++s)
+    if (s < KT) {
+#pragma unroll
+      for (int j = 0; j < LPW; ++j)
+        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src[j] + s * BK),
+                                         MFH_LDS_PTR(lds + s * STAGE + dst[j]), 16, 0, 0);
+    }
 
+  // acc[i][j]: transposed 16x16 tile, rows = output columns n, cols = rows m.
   f32x4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -119,141 +142,180 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int fr = lane & 15, fc = lane >> 4;
+  int slot = 0;                       // kt % ST
+  int fill = (ST - 1) % ST;           // (kt + ST - 1) % ST
   for (int kt = 0; kt < KT; ++kt) {
-    // This wave's loads for step kt are done; the barrier makes every
-    // wave's loads visible and guarantees the other stage is no longer read.
-    __builtin_amdgcn_s_waitcnt(0);
+    // Wait until this wave's loads of step kt have landed (the ST - 2 later
+    // steps may stay in flight; loads complete in issue order), then the
+    // barrier makes every wave's loads visible and guarantees that slot
+    // `fill`, consumed in step kt - 1, is no longer read.
+    if (kt + ST - 2 < KT) {
+      constexpr int n = (ST - 2) * LPW;
+      static_assert(n < 64, "vmcnt holds at most 63");
+      __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
     asm volatile("s_barrier" ::: "memory");
-    if (kt + 1 < KT) {
-      std::uint16_t *next = lds + ((kt + 1) & 1) * STAGE;
+    if (kt + ST - 1 < KT) {
+      std::uint16_t *next = lds + fill * STAGE;
 #pragma unroll
       for (int j = 0; j < LPW; ++j)
-        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src[j] + (kt + 1) * kBK),
-                                         MFH_LDS_PTR(next + dst[j]), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void *>(src[j] + (kt + ST - 1) * BK), MFH_LDS_PTR(next + dst[j]),
+            16, 0, 0);
     }
-    const std::uint16_t *sa = lds + (kt & 1) * STAGE;
-    const std::uint16_t *sw = sa + A_ROWS * kBK;
+    const std::uint16_t *sa = lds + slot * STAGE;
+    slot = slot + 1 == ST ? 0 : slot + 1;
+    fill = fill + 1 == ST ? 0 : fill + 1;
+    const std::uint16_t *sw = sa + A_ROWS * BK;
 #pragma unroll
-    for (int kk = 0; kk < kBK / 32; ++kk) {
+    for (int kk = 0; kk < BK / 32; ++kk) {
       bf16x8 af[TM], bw[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8 *>(sa + Swz(wm * WTM + i * 16 + fr, kk * 4 + fc));
-#pragma unroll
       for (int j = 0; j < TN; ++j)
-        bw[j] = *reinterpret_cast<const bf16x8 *>(sw + Swz(wn * WTN + j * 16 + fr, kk * 4 + fc));
+        bw[j] = *reinterpret_cast<const bf16x8 *>(
+            sw + Swz<BK>(wn * WTN + j * 16 + fr, kk * 4 + fc));
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8 *>(
+            sa + Swz<BK>(wm * WTM + i * 16 + fr, kk * 4 + fc));
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
       if constexpr (SPLIT) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
           af[i] = *reinterpret_cast<const bf16x8 *>(
-              sa + Swz(BM + wm * WTM + i * 16 + fr, kk * 4 + fc));
+              sa + Swz<BK>(BM + wm * WTM + i * 16 + fr, kk * 4 + fc));
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bw[j], acc[i][j], 0, 0, 0);
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
       }
     }
   }
 
-  // Accumulator layout of the 16x16 MFMA: lane holds rows 4*(lane/16)+r,
-  // column lane%16 of its tile.
-  const int row_base = m0 + wm * WTM + (lane >> 4) * 4;
-  const int col_base = n0 + wn * WTN + (lane & 15);
+  // Transposed accumulator layout: lane holds output row m_base + lane % 16
+  // of its tile, columns n_base + 4 * (lane / 16) + r, r = 0..3.
+  const int row_base = m0 + wm * WTM + (lane & 15);
+  const int col_base = n0 + wn * WTN + (lane >> 4) * 4;
   if (p.k_splits > 1) {
     float *part = static_cast<float *>(p.C) + static_cast<size_t>(blockIdx.y) * p.M * p.ldc;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = col_base + j * 16;
-      if (col >= p.N)
+    for (int i = 0; i < TM; ++i) {
+      const int row = row_base + i * 16;
+      if (row >= p.M)
         continue;
+      float *c = part + static_cast<size_t>(row) * p.ldc;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) {
+        const int col = col_base + j * 16;
+        if (p.vec && col + 3 < p.N) {
+          *reinterpret_cast<f32x4 *>(c + col) = acc[i][j];
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row_base + i * 16 + r;
-          if (row < p.M)
-            part[static_cast<size_t>(row) * p.ldc + col] = acc[i][j][r];
+          for (int r = 0; r < 4; ++r)
+            if (col + r < p.N)
+              c[col + r] = acc[i][j][r];
         }
+      }
     }
     return;
   }
   // Epilogue, specialised at compile time on the output mode and activation;
-  // the split-column target and the residual plane are resolved per column.
+  // the split-column target is resolved per 4-column group (split_n is a
+  // multiple of 4).
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int col = col_base + j * 16;
     if (col >= p.N)
       continue;
-    const float b = p.bias ? p.bias[col] : 0.f;
-    if constexpr (MODE == GEMM_OUT_RESID_F32) {
-      float *c = static_cast<float *>(p.C) + col;
-      const float *res = p.resid + col;
+    const bool full = p.vec && col + 3 < p.N;
+    float b[4];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int r = 0; r < 4; ++r)
+      b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row_base + i * 16 + r;
-          if (row < p.M)
-            c[static_cast<size_t>(row) * p.ldc] =
-                res[static_cast<size_t>(row) * p.ldr] + p.alpha * (acc[i][j][r] + b);
-        }
-    } else {
-      const bool second = col >= p.split_n;
-      const int cc = second ? col - p.split_n : col;
-      const int ld = second ? p.ldc2 : p.ldc;
-      if constexpr (MODE == GEMM_OUT_F32) {
-        float *c = static_cast<float *>(second ? p.C2 : p.C) + cc;
+    for (int i = 0; i < TM; ++i) {
+      const int row = row_base + i * 16;
+      if (row >= p.M)
+        continue;
+      float v[4];
+      if constexpr (MODE == GEMM_OUT_RESID_F32) {
+        float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
+        const float *res = p.resid + static_cast<size_t>(row) * p.ldr + col;
+        if (full) {
+          const f32x4 rv = *reinterpret_cast<const f32x4 *>(res);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = row_base + i * 16 + r;
-            if (row < p.M)
-              c[static_cast<size_t>(row) * ld] = Act<ACT>(acc[i][j][r] + b, p.act);
-          }
-      } else {
-        std::uint16_t *c = static_cast<std::uint16_t *>(second ? p.C2 : p.C) + cc;
-        std::uint16_t *c_lo = static_cast<std::uint16_t *>(second ? p.C2_lo : p.C_lo);
-        if (c_lo) {
-          c_lo += cc;
-#pragma unroll
-          for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = row_base + i * 16 + r;
-              if (row < p.M) {
-                const float v = Act<ACT>(acc[i][j][r] + b, p.act);
-                const std::uint16_t hi = f32_to_bf16(v);
-                c[static_cast<size_t>(row) * ld] = hi;
-                c_lo[static_cast<size_t>(row) * ld] = f32_to_bf16(v - bf16_to_f32(hi));
-              }
-            }
+          for (int r = 0; r < 4; ++r)
+            v[r] = rv[r] + p.alpha * (acc[i][j][r] + b[r]);
+          *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
         } else {
 #pragma unroll
-          for (int i = 0; i < TM; ++i)
+          for (int r = 0; r < 4; ++r)
+            if (col + r < p.N)
+              c[r] = res[r] + p.alpha * (acc[i][j][r] + b[r]);
+        }
+      } else {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = row_base + i * 16 + r;
-              if (row < p.M)
-                c[static_cast<size_t>(row) * ld] = f32_to_bf16(Act<ACT>(acc[i][j][r] + b, p.act));
-            }
+        for (int r = 0; r < 4; ++r)
+          v[r] = Act<ACT>(acc[i][j][r] + b[r], p.act);
+        const bool second = col >= p.split_n;
+        const int cc = second ? col - p.split_n : col;
+        const size_t off = static_cast<size_t>(row) * (second ? p.ldc2 : p.ldc) + cc;
+        const int valid = p.N - col;
+        if constexpr (MODE == GEMM_OUT_F32) {
+          float *c = static_cast<float *>(second ? p.C2 : p.C) + off;
+          if (full) {
+            *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (r < valid)
+                c[r] = v[r];
+          }
+        } else {
+          std::uint16_t *c = static_cast<std::uint16_t *>(second ? p.C2 : p.C) + off;
+          std::uint16_t *c_lo = static_cast<std::uint16_t *>(second ? p.C2_lo : p.C_lo);
+          std::uint16_t hi[4], lo[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            hi[r] = f32_to_bf16(v[r]);
+            lo[r] = f32_to_bf16(v[r] - bf16_to_f32(hi[r]));
+          }
+          if (full) {
+            *reinterpret_cast<u32x2 *>(c) =
+                u32x2{hi[0] | (static_cast<unsigned>(hi[1]) << 16),
+                      hi[2] | (static_cast<unsigned>(hi[3]) << 16)};
+            if (c_lo)
+              *reinterpret_cast<u32x2 *>(c_lo + off) =
+                  u32x2{lo[0] | (static_cast<unsigned>(lo[1]) << 16),
+                        lo[2] | (static_cast<unsigned>(lo[3]) << 16)};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (r < valid) {
+                c[r] = hi[r];
+                if (c_lo)
+                  c_lo[off + r] = lo[r];
+              }
+          }
         }
       }
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN, bool SPLIT, int MODE, int ACT>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   constexpr int A_ROWS = SPLIT ? 2 * BM : BM;
-  constexpr size_t kLds = 2ull * (A_ROWS + BN) * kBK * 2;
-  auto kernel = GemmKernel<BM, BN, WM, WN, SPLIT, MODE, ACT>;
+  constexpr size_t kLds = static_cast<size_t>(ST) * (A_ROWS + BN) * BK * 2;
+  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&]() {
@@ -270,63 +332,80 @@ hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
 
 // Epilogue dispatch: the activations the network uses (none, mish) get
 // dedicated instances, anything else the runtime switch.
-template <int BM, int BN, int WM, int WN, bool SPLIT>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
 hipError_t Launch(const GemmParams &p, hipStream_t stream) {
   if (p.k_splits > 1 || (p.out_mode == GEMM_OUT_F32 && p.act == ACT_NONE))
-    return LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE>(p, stream);
   if (p.out_mode == GEMM_OUT_RESID_F32)
-    return LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE>(p, stream);
   if (p.out_mode == GEMM_OUT_F32)
     return p.act == ACT_MISH
-               ? LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH>(p, stream)
-               : LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME>(p, stream);
+               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH>(p, stream)
+               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME>(p, stream);
   if (p.act == ACT_NONE)
-    return LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE>(p, stream);
   if (p.act == ACT_MISH)
-    return LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH>(p, stream);
-  return LaunchVariant<BM, BN, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH>(p, stream);
+  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME>(p, stream);
 }
 
-bool Aligned16(const void *ptr) {
-  return (reinterpret_cast<std::uintptr_t>(ptr) & 15u) == 0;
+bool Aligned(const void *ptr, std::uintptr_t bytes) {
+  return (reinterpret_cast<std::uintptr_t>(ptr) & (bytes - 1)) == 0;
 }
 
 }  // namespace
 
-hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err) {
+hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *err) {
   auto fail = [&](const char *why) {
     if (err)
       *err = std::string("gemm: ") + why;
     return hipErrorInvalidValue;
   };
+  GemmParams p = p_in;
   if (p.M <= 0 || p.N <= 0 || p.K <= 0)
     return fail("non-positive shape");
-  if (p.K % kBK)
-    return fail("K must be a multiple of 64");
-  if (p.k_splits < 1 || p.K % (p.k_splits * kBK))
-    return fail("K must split into multiples of 64");
+  if (p.K % 32)
+    return fail("K must be a multiple of 32");
+  if (p.k_splits < 1 || p.K % (p.k_splits * 32))
+    return fail("K must split into multiples of 32");
   if (p.k_splits > 1 && (p.out_mode != GEMM_OUT_F32 || p.bias || p.act != ACT_NONE ||
                          p.split_n < p.N))
     return fail("split-K writes raw fp32 partials only (no bias, activation or split)");
   if (!p.A || !p.W || !p.C)
     return fail("null operand");
-  if (!Aligned16(p.A) || !Aligned16(p.W) || (p.A_lo && !Aligned16(p.A_lo)) || p.lda % 8 ||
-      p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
+  if (!Aligned(p.A, 16) || !Aligned(p.W, 16) || (p.A_lo && !Aligned(p.A_lo, 16)) ||
+      p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
     return fail("operands must be 16-byte aligned with ld >= K, ld % 8 == 0");
   if (p.out_mode == GEMM_OUT_RESID_F32 && (!p.resid || p.split_n < p.N))
     return fail("residual mode needs resid and no split");
-  if (p.split_n < p.N && (!p.C2 || p.ldc2 < p.N - p.split_n))
-    return fail("split output needs C2 wide enough");
+  if (p.split_n < p.N && (!p.C2 || p.ldc2 < p.N - p.split_n || p.split_n % 4))
+    return fail("split output needs C2 wide enough and split_n % 4 == 0");
   if (p.split_n < p.N && (p.C_lo != nullptr) != (p.C2_lo != nullptr))
     return fail("split output needs lo planes for both parts or neither");
   if (p.ldc < (p.split_n < p.N ? p.split_n : p.N))
     return fail("ldc too small");
+  // Vector (4-column) stores need every output row start aligned to 4
+  // elements' width; otherwise the epilogue stores element by element.
+  const bool f32 = p.out_mode != GEMM_OUT_BF16 || p.k_splits > 1;
+  const std::uintptr_t vb = f32 ? 16 : 8;
+  p.vec = Aligned(p.C, vb) && p.ldc % 4 == 0 && (!p.C_lo || Aligned(p.C_lo, vb)) &&
+          (p.split_n >= p.N ||
+           (Aligned(p.C2, vb) && p.ldc2 % 4 == 0 && (!p.C2_lo || Aligned(p.C2_lo, vb)))) &&
+          (p.out_mode != GEMM_OUT_RESID_F32 || (Aligned(p.resid, 16) && p.ldr % 4 == 0));
   const bool split = p.A_lo != nullptr;
   const bool large = p.M >= 2048 && p.N >= 128;
-  if (large)
-    return split ? Launch<128, 128, 2, 2, true>(p, stream)
-                 : Launch<128, 128, 2, 2, false>(p, stream);
-  return split ? Launch<64, 64, 2, 2, true>(p, stream) : Launch<64, 64, 2, 2, false>(p, stream);
+  const int kslice = p.K / p.k_splits;
+  // Tile choice measured on MI355X at the BT4 body shapes (M = 16384):
+  // split precision runs 64 x 128 tiles (A hi + lo + W = 64 KiB of LDS for
+  // two stages, two workgroups per CU), bf16 runs 128 x 128.
+  if (large && kslice % 64 == 0)
+    return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
+                 : Launch<128, 128, 64, 2, 2, 2, false>(p, stream);
+  if (kslice % 64 == 0)
+    return split ? Launch<64, 64, 64, 2, 2, 2, true>(p, stream)
+                 : Launch<64, 64, 64, 2, 2, 2, false>(p, stream);
+  return split ? Launch<64, 64, 32, 2, 2, 2, true>(p, stream)
+               : Launch<64, 64, 32, 2, 2, 2, false>(p, stream);
 }
 
 }  // namespace mfh

@@ -60,6 +60,8 @@ struct GemmParams {
   // K split over blockIdx.y; each slice writes fp32 partials to
   // C + slice * M * ldc (GEMM_OUT_F32, no bias/activation).
   int k_splits = 1;
+  // Set by LaunchGemm: every output row start allows 4-column vector stores.
+  bool vec = false;
 };
 
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
