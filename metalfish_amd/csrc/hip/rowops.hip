@@ -91,15 +91,17 @@ __global__ void ScatterPeKernel(const float *__restrict__ pe, int batch, int pe_
     emb_in_lo[off] = f32_to_bf16(pe[idx] - bf16_to_f32(hi));
 }
 
-// Row LayerNorm.  T threads per row (64: one wave, 256: one workgroup);
-// each thread keeps its <= kMaxPerThread values in registers.  The input is
-// the sum of `parts` partial rows plus bias, through the activation, as
-// produced by a split-K GEMM; statistics in fp32 with the reference formula
+// Row LayerNorm.  T threads per row (64: one wave, 256: one workgroup),
+// each holding NV float4 vectors of the row in registers: element
+// c = 4 (i T + t) + e for vector i of thread t.  The input is the sum of
+// `parts` partial rows plus bias, through the activation, as produced by a
+// split-K GEMM; statistics in fp32 with the reference formula
 // var = E[x^2] - mean^2 clamped at 0, inv_std = 1 / sqrt(var + eps)
-// (cpu_network.cpp:424-460).
-constexpr int kMaxPerThread = 32;
+// (cpu_network.cpp:424-460).  Loads are 16 bytes, stores 16 (fp32) or 8
+// (bf16) bytes per lane.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-template <int T>
+template <int T, int NV>
 __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
   constexpr int kRowsPerBlock = 256 / T;
   __shared__ float red[2][4];
@@ -108,22 +110,29 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
   const bool active = row < lp.rows;
   const int width = lp.width;
   const size_t plane = static_cast<size_t>(lp.rows) * width;
-  float v[kMaxPerThread];
+  const size_t row_off = static_cast<size_t>(row) * width;
+  f32x4 v[NV];
   float s = 0.f, ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int c = i * T + t;
-    float x = 0.f;
+  for (int i = 0; i < NV; ++i) {
+    const int c = 4 * (i * T + t);
+    f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
     if (active && c < width) {
-      const size_t off = static_cast<size_t>(row) * width + c;
-      x = lp.x[off];
+      x = *reinterpret_cast<const f32x4 *>(lp.x + row_off + c);
       for (int part = 1; part < lp.parts; ++part)
-        x += lp.x[part * plane + off];
+        x += *reinterpret_cast<const f32x4 *>(lp.x + part * plane + row_off + c);
       if (lp.bias)
-        x += lp.bias[c];
-      x = activate(x, lp.act);
-      s += x;
-      ss += x * x;
+        x += *reinterpret_cast<const f32x4 *>(lp.bias + c);
+      if (lp.act != ACT_NONE) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          x[e] = activate(x[e], lp.act);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s += x[e];
+        ss += x[e] * x[e];
+      }
     }
     v[i] = x;
   }
@@ -146,23 +155,37 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
   const float inv_std = 1.f / sqrtf(var + lp.eps);
   const int sq = row % kSquares;
 #pragma unroll
-  for (int i = 0; i < kMaxPerThread; ++i) {
-    const int c = i * T + t;
+  for (int i = 0; i < NV; ++i) {
+    const int c = 4 * (i * T + t);
     if (c >= width)
       break;
-    float y = (v[i] - mean) * inv_std * lp.gamma[c] + lp.beta[c];
-    if (lp.mult_gate)
-      y = y * lp.mult_gate[static_cast<size_t>(c) * kSquares + sq];
-    if (lp.add_gate)
-      y = y + lp.add_gate[static_cast<size_t>(c) * kSquares + sq];
-    const size_t off = static_cast<size_t>(row) * width + c;
+    const f32x4 gm = *reinterpret_cast<const f32x4 *>(lp.gamma + c);
+    const f32x4 bt = *reinterpret_cast<const f32x4 *>(lp.beta + c);
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y[e] = (v[i][e] - mean) * inv_std * gm[e] + bt[e];
+      if (lp.mult_gate)
+        y[e] = y[e] * lp.mult_gate[static_cast<size_t>(c + e) * kSquares + sq];
+      if (lp.add_gate)
+        y[e] = y[e] + lp.add_gate[static_cast<size_t>(c + e) * kSquares + sq];
+    }
     if (lp.y_f32)
-      lp.y_f32[off] = y;
+      *reinterpret_cast<f32x4 *>(lp.y_f32 + row_off + c) = y;
     if (lp.y_bf16) {
-      const std::uint16_t hi = f32_to_bf16(y);
-      lp.y_bf16[off] = hi;
+      std::uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[e] = f32_to_bf16(y[e]);
+        lo[e] = f32_to_bf16(y[e] - bf16_to_f32(hi[e]));
+      }
+      *reinterpret_cast<u32x2 *>(lp.y_bf16 + row_off + c) =
+          u32x2{hi[0] | (static_cast<unsigned>(hi[1]) << 16),
+                hi[2] | (static_cast<unsigned>(hi[3]) << 16)};
       if (lp.y_bf16_lo)
-        lp.y_bf16_lo[off] = f32_to_bf16(y - bf16_to_f32(hi));
+        *reinterpret_cast<u32x2 *>(lp.y_bf16_lo + row_off + c) =
+            u32x2{lo[0] | (static_cast<unsigned>(lo[1]) << 16),
+                  lo[2] | (static_cast<unsigned>(lo[3]) << 16)};
     }
   }
 }
@@ -268,13 +291,33 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
     Fail(err, "layernorm: gates need square rows");
     return hipErrorInvalidValue;
   }
+  auto aligned = [](const void *p, std::uintptr_t a) {
+    return (reinterpret_cast<std::uintptr_t>(p) & (a - 1)) == 0;
+  };
+  if (lp.width % 4 || !aligned(lp.x, 16) || (lp.bias && !aligned(lp.bias, 16)) ||
+      !aligned(lp.gamma, 16) || !aligned(lp.beta, 16) || (lp.y_f32 && !aligned(lp.y_f32, 16)) ||
+      (lp.y_bf16 && !aligned(lp.y_bf16, 8)) || (lp.y_bf16_lo && !aligned(lp.y_bf16_lo, 8))) {
+    Fail(err, "layernorm: width % 4 == 0 and 16-byte aligned rows required");
+    return hipErrorInvalidValue;
+  }
   // The thread count per row depends on the width only, so a row's
   // reduction order (and result bits) never depends on the batch size.
-  if (lp.width <= 64 * kMaxPerThread) {
-    hipLaunchKernelGGL(LayerNormKernel<64>, dim3((lp.rows + 3) / 4), dim3(256), 0, stream, lp);
-  } else if (lp.width <= 256 * kMaxPerThread) {
-    hipLaunchKernelGGL(LayerNormKernel<256>, dim3(lp.rows), dim3(256), 0, stream, lp);
-  } else {
+  const int nv64 = (lp.width + 255) / 256;      // float4s per lane, one wave per row
+  const int nv256 = (lp.width + 1023) / 1024;   // float4s per lane, 256 threads per row
+  const dim3 g64((lp.rows + 3) / 4), g256(lp.rows), blk(256);
+  if (nv64 <= 1)
+    hipLaunchKernelGGL((LayerNormKernel<64, 1>), g64, blk, 0, stream, lp);
+  else if (nv64 <= 2)
+    hipLaunchKernelGGL((LayerNormKernel<64, 2>), g64, blk, 0, stream, lp);
+  else if (nv64 <= 4)
+    hipLaunchKernelGGL((LayerNormKernel<64, 4>), g64, blk, 0, stream, lp);
+  else if (nv64 <= 8)
+    hipLaunchKernelGGL((LayerNormKernel<64, 8>), g64, blk, 0, stream, lp);
+  else if (nv256 <= 4)
+    hipLaunchKernelGGL((LayerNormKernel<256, 4>), g256, blk, 0, stream, lp);
+  else if (nv256 <= 8)
+    hipLaunchKernelGGL((LayerNormKernel<256, 8>), g256, blk, 0, stream, lp);
+  else {
     Fail(err, "layernorm: row wider than 8192");
     return hipErrorInvalidValue;
   }
