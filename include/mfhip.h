@@ -61,8 +61,10 @@ enum { MFH_WEIGHTS_BF16 = 0 };
  * BF16X2: activations are carried as a bf16 pair hi + lo (lo = bf16(x - hi))
  * and every product takes two (GEMMs) or three (attention, policy map)
  * bf16 MFMAs, giving ~16-bit activation precision against the exact bf16
- * weights at twice the MFMA work. */
-enum { MFH_PRECISION_BF16 = 0, MFH_PRECISION_BF16X2 = 1 };
+ * weights at twice the MFMA work.  BF16X2_GEMM: the pair only for the inputs
+ * of the dense layers and the policy map; attention Q/K/V, its
+ * probabilities, the smolgen activations and bias stay single bf16. */
+enum { MFH_PRECISION_BF16 = 0, MFH_PRECISION_BF16X2 = 1, MFH_PRECISION_BF16X2_GEMM = 2 };
 
 /* Network description: the format fields of the weights file plus the
  * attention head count (Weights.headcount) and run-time sizing. */
@@ -77,7 +79,7 @@ typedef struct {
   int smolgen_activation; /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
   int headcount;          /* body attention heads; head depth must be 32 */
   int weights_dtype;      /* MFH_WEIGHTS_BF16 */
-  int precision;          /* MFH_PRECISION_BF16 or MFH_PRECISION_BF16X2 */
+  int precision;          /* MFH_PRECISION_* */
   int max_batch;          /* largest batch one eval call accepts (>= 1) */
   int device;             /* HIP device ordinal, -1 = current device */
 } mfh_net_desc;

@@ -20,7 +20,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libmfhip.so")
 
 MFH_OK = 0
-PRECISION = {"bf16": 0, "bf16x2": 1}
+PRECISION = {"bf16": 0, "bf16x2": 1, "bf16x2_gemm": 2}
 ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid": 5,
               "selu": 6, "swish": 7, "relu_2": 8}
 

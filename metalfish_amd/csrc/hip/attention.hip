@@ -20,9 +20,10 @@
 // ctx^T leaves each lane with four consecutive depths of one query: one
 // 8-byte store.  Scores, softmax statistics and accumulation stay in fp32.
 //
-// Split precision: Q, K, V and the context arrive/leave as hi + lo bf16
-// planes, P is split the same way in registers, and each product takes three
-// MFMAs (hi.hi + hi.lo + lo.hi; the lo.lo term is below fp32 resolution).
+// Split precision: with SPLIT_IN, Q, K and V arrive as hi + lo bf16 planes,
+// P is split the same way in registers, and each product takes three MFMAs
+// (hi.hi + hi.lo + lo.hi; the lo.lo term is below fp32 resolution).  With
+// SPLIT_OUT the context leaves as hi + lo planes (it feeds a split GEMM).
 #include "mfh_device.h"
 #include "mfh_kernels.h"
 
@@ -47,7 +48,7 @@ __device__ __forceinline__ bf16x8 Join(u32x2 a, u32x2 b) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
-template <bool SPLIT, bool BIAS_F32>
+template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
 __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   constexpr int PLANES = SPLIT ? 2 : 1;
   __shared__ __attribute__((aligned(16))) std::uint16_t vt_lds[kHeadsPerBlock][PLANES]
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       *reinterpret_cast<u32x2 *>(ap.ctx + idx) =
           u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
                 hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
-      if constexpr (SPLIT) {
+      if constexpr (SPLIT_OUT) {
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
           lw[r / 2] = f32_to_bf16(o[dt][q][r] - bf16_to_f32(hi[r])) |
@@ -245,9 +246,10 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     }
 }
 
-template <bool SPLIT, bool BIAS_F32>
+template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
 hipError_t Launch(const AttentionParams &ap, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((AttentionKernel<SPLIT, BIAS_F32>), dim3(grid), dim3(256), 0, stream, ap);
+  hipLaunchKernelGGL((AttentionKernel<SPLIT, SPLIT_OUT, BIAS_F32>), dim3(grid), dim3(256), 0,
+                     stream, ap);
   return hipGetLastError();
 }
 
@@ -259,24 +261,26 @@ bool Misaligned(const void *p, std::uintptr_t bytes) {
 
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::string *err) {
   const bool split = ap.qkv_lo != nullptr;
+  const bool split_out = ap.ctx_lo != nullptr;
   if (ap.batch <= 0 || ap.heads <= 0 || ap.heads % kHeadsPerBlock || !ap.qkv || !ap.ctx ||
       Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 8) ||
       (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
-      (split && (!ap.ctx_lo || Misaligned(ap.qkv_lo, 16) || Misaligned(ap.ctx_lo, 8)))) {
+      (split && (!split_out || Misaligned(ap.qkv_lo, 16))) ||
+      (split_out && Misaligned(ap.ctx_lo, 8))) {
     if (err)
       *err = "attention: needs batch > 0, heads % 4 == 0, 16-byte aligned qkv, 8-byte "
-             "aligned ctx and bias, and lo planes for both input and output in split mode";
+             "aligned ctx and bias, and a lo output plane whenever the input has one";
     return hipErrorInvalidValue;
   }
   const int grid = ap.batch * (ap.heads / kHeadsPerBlock);
-  if (split) {
-    if (ap.bias_f32)
-      return Launch<true, true>(ap, grid, stream);
-    return Launch<true, false>(ap, grid, stream);
-  }
-  if (ap.bias_f32)
-    return Launch<false, true>(ap, grid, stream);
-  return Launch<false, false>(ap, grid, stream);
+  if (split)
+    return ap.bias_f32 ? Launch<true, true, true>(ap, grid, stream)
+                       : Launch<true, true, false>(ap, grid, stream);
+  if (split_out)
+    return ap.bias_f32 ? Launch<false, true, true>(ap, grid, stream)
+                       : Launch<false, true, false>(ap, grid, stream);
+  return ap.bias_f32 ? Launch<false, false, true>(ap, grid, stream)
+                     : Launch<false, false, false>(ap, grid, stream);
 }
 
 }  // namespace mfh

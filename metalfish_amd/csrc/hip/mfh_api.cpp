@@ -111,7 +111,8 @@ struct Dims {
   int C = 0, Hs = 0, HG = 0, G = 0;
   int Dp = 0, Vd = 0, Vh = 0, Vout = 0;
   bool gates = false, input_ffn = false, smolgen = false, wdl = true;
-  bool split = false;  // MFH_PRECISION_BF16X2
+  bool split = false;       // lo planes on dense-layer inputs (BF16X2, BF16X2_GEMM)
+  bool split_attn = false;  // lo planes on attention / smolgen operands (BF16X2)
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -249,9 +250,11 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
                     "HIP backend supports INPUT_EMBEDDING_PE_DENSE only (as the reference CPU backend)");
   if (desc.weights_dtype != MFH_WEIGHTS_BF16)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
-  if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2)
+  if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2 &&
+      desc.precision != MFH_PRECISION_BF16X2_GEMM)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported precision mode");
-  d.split = desc.precision == MFH_PRECISION_BF16X2;
+  d.split = desc.precision != MFH_PRECISION_BF16;
+  d.split_attn = desc.precision == MFH_PRECISION_BF16X2;
   d.wdl = desc.value == MFH_VALUE_WDL;
   d.act_default = desc.default_activation == MFH_DEFAULT_ACTIVATION_MISH ? mfh::ACT_MISH
                                                                          : mfh::ACT_RELU;
@@ -483,6 +486,12 @@ void PlanWorkspace(mfh_net *net) {
     if (d.split)
       add(name + "_lo", elems * 2);
   };
+  // Attention and smolgen operands carry the pair only in full BF16X2.
+  auto add16a = [&](const std::string &name, size_t elems) {
+    add(name, elems * 2);
+    if (d.split_attn)
+      add(name + "_lo", elems * 2);
+  };
   const int hid = d.F > d.Fi ? d.F : d.Fi;
   const int sk1 = d.smolgen ? SplitK(kSquares * d.C) : 1;
   const int skv = SplitK(kSquares * d.Vd);
@@ -494,13 +503,13 @@ void PlanWorkspace(mfh_net *net) {
   add("pre", M * d.E * 4);
   add("resid", M * d.E * 4);
   add16("act", M * d.E);
-  add16("qkv", M * 3 * d.E);
-  add16("comp", M * (d.C ? d.C : 1));
+  add16a("qkv", M * 3 * d.E);
+  add16a("comp", M * (d.C ? d.C : 1));
   add("sg1", sk1 * B * (d.Hs ? d.Hs : 1) * 4);
-  add16("sg1n", B * (d.Hs ? d.Hs : 1));
+  add16a("sg1n", B * (d.Hs ? d.Hs : 1));
   add("sg2", B * (d.HG ? d.HG : 1) * 4);
-  add16("sg2n", B * (d.HG ? d.HG : 1));
-  add("bias", d.smolgen ? B * d.H * kSquares * kSquares * (d.split ? 4 : 2) : 256);
+  add16a("sg2n", B * (d.HG ? d.HG : 1));
+  add("bias", d.smolgen ? B * d.H * kSquares * kSquares * (d.split_attn ? 4 : 2) : 256);
   add16("ctx", M * d.E);
   add16("hid", M * (hid ? hid : 1));
   add16("pol_emb", M * d.Dp);
@@ -734,16 +743,19 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       MFH_RUN(run_ln(l2));
       void *bias = net->S<void>("bias");
       MFH_RUN(run(gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares, d.G,
-                       nullptr, mfh::ACT_NONE, d.split ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
-                       bias, nullptr, kSquares * kSquares)));
+                       nullptr, mfh::ACT_NONE,
+                       d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16, bias, nullptr,
+                       kSquares * kSquares)));
       ap.bias = bias;
-      ap.bias_f32 = d.split ? 1 : 0;
+      ap.bias_f32 = d.split_attn ? 1 : 0;
     }
     {
       const double heads_total = static_cast<double>(B) * d.H;
       const double flops = heads_total * 2.0 * (2.0 * kSquares * kSquares * 32);
-      const double bytes = 2.0 * plane_mult * (3.0 * M * E + M * E) +
-                           (ap.bias ? heads_total * kSquares * kSquares * (d.split ? 4.0 : 2.0)
+      const double bytes = 2.0 * (d.split_attn ? 2.0 : 1.0) * 3.0 * M * E +
+                           2.0 * plane_mult * M * E +
+                           (ap.bias ? heads_total * kSquares * kSquares *
+                                          (d.split_attn ? 4.0 : 2.0)
                                     : 0.0);
       StageTimer t(net, st, "attention", flops, bytes);
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
@@ -1051,7 +1063,7 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
   o << ", policy attention Dp=" << d.Dp << ", value " << (d.wdl ? "wdl" : "scalar") << " "
     << d.Vd << "/" << d.Vh << ", activations " << ActName(d.act_default) << "/"
     << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", precision "
-    << (d.split ? "bf16x2" : "bf16") << ", weights bf16 "
+    << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : "bf16") << ", weights bf16 "
     << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
     << net->max_batch;
   const std::string s = o.str();

@@ -115,7 +115,8 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream,
 //   ctx = softmax(Q K^T / sqrt(32) + bias) V
 // qkv [B*64, 3E] bf16 (Q | K | V, head h at columns h*32..), bias [B,H,64,64]
 // (bf16, or fp32 when bias_f32) or null, ctx [B*64, E] bf16.  Split
-// precision when qkv_lo is set (then ctx_lo is required).
+// precision inputs when qkv_lo is set (then ctx_lo is required); ctx_lo
+// alone splits only the output.
 struct AttentionParams {
   const std::uint16_t *qkv = nullptr;
   const std::uint16_t *qkv_lo = nullptr;
