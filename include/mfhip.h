@@ -145,6 +145,14 @@ typedef struct {
 } mfh_capabilities;
 int mfh_net_capabilities(const mfh_net *net, mfh_capabilities *out);
 
+/* Graph execution (the counterpart of BackendConfig::cuda_graph_execution,
+ * reference src/nn/network.h:58 and cuda_network.cpp:312): when enabled (the
+ * default), the forward for a batch size and set of device buffers runs
+ * eagerly once and is then captured into a HIP graph that later calls
+ * replay with a single launch.  Profiling bypasses graphs.  Changing the
+ * setting drops the cached graphs. */
+int mfh_net_set_graphs(mfh_net *net, int enabled);
+
 /* Stage profiler (the counterpart of the reference's METALFISH_CUDA_PROFILE
  * stage timers, reference src/nn/cuda/cuda_stage_executor.cpp:421-482):
  * while enabled, every kernel launch of an eval call is bracketed by HIP

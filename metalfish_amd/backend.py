@@ -27,7 +27,8 @@ ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid
 # Every symbol include/mfhip.h declares.
 EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_planes",
            "mfh_net_eval_device", "mfh_net_info", "mfh_net_capabilities",
-           "mfh_net_set_profiling", "mfh_net_profile", "mfh_net_profile_reset",
+           "mfh_net_set_graphs", "mfh_net_set_profiling", "mfh_net_profile",
+           "mfh_net_profile_reset",
            "mfh_pack_planes", "mfh_device_count", "mfh_last_error", "mfh_debug_unpack_planes",
            "mfh_debug_gemm_bf16", "mfh_net_debug_tensor")
 
@@ -76,6 +77,7 @@ def lib():
             "mfh_net_eval_device": ([vp, i, vp, vp, vp, vp, vp], i),
             "mfh_net_info": ([vp, ctypes.c_char_p, ctypes.c_size_t], i),
             "mfh_net_capabilities": ([vp, ctypes.POINTER(MfhCapabilities)], i),
+            "mfh_net_set_graphs": ([vp, i], i),
             "mfh_net_set_profiling": ([vp, i], i),
             "mfh_net_profile": ([vp, ctypes.POINTER(MfhProfileEntry), i, ctypes.POINTER(i)], i),
             "mfh_net_profile_reset": ([vp], i),
@@ -212,6 +214,10 @@ class HipNetwork:
         """Device-resident forward (pointers are device addresses)."""
         _check(lib().mfh_net_eval_device(self._h, batch, d_masks, d_values, d_policy, d_wdl,
                                          stream), "mfh_net_eval_device")
+
+    def set_graphs(self, enabled: bool):
+        """Graph capture/replay of the forward (on by default)."""
+        _check(lib().mfh_net_set_graphs(self._h, 1 if enabled else 0), "mfh_net_set_graphs")
 
     def set_profiling(self, enabled: bool):
         _check(lib().mfh_net_set_profiling(self._h, 1 if enabled else 0), "mfh_net_set_profiling")

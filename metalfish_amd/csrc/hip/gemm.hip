@@ -57,6 +57,79 @@ __device__ __forceinline__ float Act(float v, int runtime_act) {
     return activate(v, ACT);
 }
 
+// Epilogue for four consecutive outputs (row, col .. col + 3) of C, given
+// the fp32 accumulators and bias: bias + activation to bf16 (with the lo
+// plane and the split column) or fp32, or resid + alpha * (acc + bias).
+// Columns at or past N are skipped; vector stores when the whole group is
+// inside and the rows allow it (p.vec).
+template <int MODE, int ACT>
+__device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col, f32x4 acc,
+                                          const float (&b)[4]) {
+  const bool full = p.vec && col + 3 < p.N;
+  float v[4];
+  if constexpr (MODE == GEMM_OUT_RESID_F32) {
+    float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
+    const float *res = p.resid + static_cast<size_t>(row) * p.ldr + col;
+    if (full) {
+      const f32x4 rv = *reinterpret_cast<const f32x4 *>(res);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        v[r] = rv[r] + p.alpha * (acc[r] + b[r]);
+      *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (col + r < p.N)
+          c[r] = res[r] + p.alpha * (acc[r] + b[r]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      v[r] = Act<ACT>(acc[r] + b[r], p.act);
+    // split_n is a multiple of 4, so a group never straddles it.
+    const bool second = col >= p.split_n;
+    const int cc = second ? col - p.split_n : col;
+    const size_t off = static_cast<size_t>(row) * (second ? p.ldc2 : p.ldc) + cc;
+    const int valid = p.N - col;
+    if constexpr (MODE == GEMM_OUT_F32) {
+      float *c = static_cast<float *>(second ? p.C2 : p.C) + off;
+      if (full) {
+        *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (r < valid)
+            c[r] = v[r];
+      }
+    } else {
+      std::uint16_t *c = static_cast<std::uint16_t *>(second ? p.C2 : p.C) + off;
+      std::uint16_t *c_lo = static_cast<std::uint16_t *>(second ? p.C2_lo : p.C_lo);
+      std::uint16_t hi[4], lo[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        hi[r] = f32_to_bf16(v[r]);
+        lo[r] = f32_to_bf16(v[r] - bf16_to_f32(hi[r]));
+      }
+      if (full) {
+        *reinterpret_cast<u32x2 *>(c) = u32x2{hi[0] | (static_cast<unsigned>(hi[1]) << 16),
+                                              hi[2] | (static_cast<unsigned>(hi[3]) << 16)};
+        if (c_lo)
+          *reinterpret_cast<u32x2 *>(c_lo + off) =
+              u32x2{lo[0] | (static_cast<unsigned>(lo[1]) << 16),
+                    lo[2] | (static_cast<unsigned>(lo[3]) << 16)};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (r < valid) {
+            c[r] = hi[r];
+            if (c_lo)
+              c_lo[off + r] = lo[r];
+          }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int NWAVES = WM * WN;
@@ -227,15 +300,12 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     }
     return;
   }
-  // Epilogue, specialised at compile time on the output mode and activation;
-  // the split-column target is resolved per 4-column group (split_n is a
-  // multiple of 4).
+  // Epilogue, specialised at compile time on the output mode and activation.
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int col = col_base + j * 16;
     if (col >= p.N)
       continue;
-    const bool full = p.vec && col + 3 < p.N;
     float b[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -243,72 +313,41 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = row_base + i * 16;
-      if (row >= p.M)
-        continue;
-      float v[4];
-      if constexpr (MODE == GEMM_OUT_RESID_F32) {
-        float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
-        const float *res = p.resid + static_cast<size_t>(row) * p.ldr + col;
-        if (full) {
-          const f32x4 rv = *reinterpret_cast<const f32x4 *>(res);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            v[r] = rv[r] + p.alpha * (acc[i][j][r] + b[r]);
-          *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (col + r < p.N)
-              c[r] = res[r] + p.alpha * (acc[i][j][r] + b[r]);
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          v[r] = Act<ACT>(acc[i][j][r] + b[r], p.act);
-        const bool second = col >= p.split_n;
-        const int cc = second ? col - p.split_n : col;
-        const size_t off = static_cast<size_t>(row) * (second ? p.ldc2 : p.ldc) + cc;
-        const int valid = p.N - col;
-        if constexpr (MODE == GEMM_OUT_F32) {
-          float *c = static_cast<float *>(second ? p.C2 : p.C) + off;
-          if (full) {
-            *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (r < valid)
-                c[r] = v[r];
-          }
-        } else {
-          std::uint16_t *c = static_cast<std::uint16_t *>(second ? p.C2 : p.C) + off;
-          std::uint16_t *c_lo = static_cast<std::uint16_t *>(second ? p.C2_lo : p.C_lo);
-          std::uint16_t hi[4], lo[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            hi[r] = f32_to_bf16(v[r]);
-            lo[r] = f32_to_bf16(v[r] - bf16_to_f32(hi[r]));
-          }
-          if (full) {
-            *reinterpret_cast<u32x2 *>(c) =
-                u32x2{hi[0] | (static_cast<unsigned>(hi[1]) << 16),
-                      hi[2] | (static_cast<unsigned>(hi[3]) << 16)};
-            if (c_lo)
-              *reinterpret_cast<u32x2 *>(c_lo + off) =
-                  u32x2{lo[0] | (static_cast<unsigned>(lo[1]) << 16),
-                        lo[2] | (static_cast<unsigned>(lo[3]) << 16)};
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (r < valid) {
-                c[r] = hi[r];
-                if (c_lo)
-                  c_lo[off + r] = lo[r];
-              }
-          }
-        }
-      }
+      if (row < p.M)
+        Epilogue4<MODE, ACT>(p, row, col, acc[i][j], b);
     }
   }
+}
+
+// Sums the k_splits fp32 partial tiles of a split-K launch in slice order
+// and applies the epilogue: one thread per four consecutive outputs.
+template <int MODE, int ACT>
+__global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const float *part,
+                                                            int splits) {
+  const int groups = (p.N + 3) / 4;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int row = idx / groups;
+  if (row >= p.M)
+    return;
+  const int col = (idx % groups) * 4;
+  const size_t plane = static_cast<size_t>(p.M) * p.N;
+  const float *src = part + static_cast<size_t>(row) * p.N + col;
+  f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (p.vec && col + 3 < p.N) {
+    for (int s = 0; s < splits; ++s)
+      a += *reinterpret_cast<const f32x4 *>(src + s * plane);
+  } else {
+    for (int s = 0; s < splits; ++s)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (col + r < p.N)
+          a[r] += src[s * plane + r];
+  }
+  float b[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
+  Epilogue4<MODE, ACT>(p, row, col, a, b);
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT>
@@ -328,6 +367,28 @@ hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   const int grid = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   hipLaunchKernelGGL(kernel, dim3(grid, p.k_splits), dim3(WM * WN * 64), kLds, stream, p);
   return hipGetLastError();
+}
+
+template <int MODE, int ACT>
+hipError_t LaunchReduce(const GemmParams &p, const float *part, int splits,
+                        hipStream_t stream) {
+  const long threads = static_cast<long>(p.M) * ((p.N + 3) / 4);
+  hipLaunchKernelGGL((ReduceEpilogueKernel<MODE, ACT>), dim3((threads + 255) / 256), dim3(256),
+                     0, stream, p, part, splits);
+  return hipGetLastError();
+}
+
+hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_t stream) {
+  if (p.out_mode == GEMM_OUT_RESID_F32)
+    return LaunchReduce<GEMM_OUT_RESID_F32, ACT_NONE>(p, part, splits, stream);
+  if (p.out_mode == GEMM_OUT_F32)
+    return p.act == ACT_NONE ? LaunchReduce<GEMM_OUT_F32, ACT_NONE>(p, part, splits, stream)
+                             : LaunchReduce<GEMM_OUT_F32, ACT_RUNTIME>(p, part, splits, stream);
+  if (p.act == ACT_NONE)
+    return LaunchReduce<GEMM_OUT_BF16, ACT_NONE>(p, part, splits, stream);
+  if (p.act == ACT_MISH)
+    return LaunchReduce<GEMM_OUT_BF16, ACT_MISH>(p, part, splits, stream);
+  return LaunchReduce<GEMM_OUT_BF16, ACT_RUNTIME>(p, part, splits, stream);
 }
 
 // Epilogue dispatch: the activations the network uses (none, mish) get
@@ -394,6 +455,40 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
           (p.out_mode != GEMM_OUT_RESID_F32 || (Aligned(p.resid, 16) && p.ldr % 4 == 0));
   const bool split = p.A_lo != nullptr;
   const bool large = p.M >= 2048 && p.N >= 128;
+  // Small problems (few positions): 64 x 64 tiles leave most CUs idle and
+  // walk K serially, so the launcher splits K over up to 512 workgroups,
+  // writes fp32 partials to p.partials and sums them in slice order in a
+  // second kernel that applies the epilogue.  The split depends on the shape
+  // only: a batch size always takes the same path and gives the same bits.
+  if (!large && p.k_splits == 1 && p.partials && Aligned(p.partials, 16) && p.vec &&
+      p.N % 4 == 0) {
+    const long tiles = static_cast<long>((p.M + 63) / 64) * ((p.N + 63) / 64);
+    const int steps = p.K / 64;
+    int splits = 1;
+    if (p.K % 64 == 0 && tiles < 256)
+      for (int s = 2; s <= steps; ++s)
+        if (steps % s == 0 && tiles * s <= 512 &&
+            static_cast<size_t>(s) * p.M * p.N <= p.partials_floats)
+          splits = s;
+    if (splits > 1) {
+      GemmParams q = p;
+      q.bias = nullptr;
+      q.act = ACT_NONE;
+      q.out_mode = GEMM_OUT_F32;
+      q.C = p.partials;
+      q.C_lo = q.C2 = q.C2_lo = nullptr;
+      q.ldc = p.N;
+      q.split_n = 1 << 30;
+      q.resid = nullptr;
+      q.k_splits = splits;
+      q.vec = true;
+      const hipError_t e = split ? Launch<64, 64, 64, 2, 2, 2, true>(q, stream)
+                                 : Launch<64, 64, 64, 2, 2, 2, false>(q, stream);
+      if (e != hipSuccess)
+        return e;
+      return Reduce(p, p.partials, splits, stream);
+    }
+  }
   const int kslice = p.K / p.k_splits;
   // Tile choice measured on MI355X at the BT4 body shapes (M = 16384):
   // split precision runs 64 x 128 tiles (A hi + lo + W = 64 KiB of LDS for

@@ -21,8 +21,10 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <set>
 #include <sstream>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../host/policy_tables.h"
@@ -156,6 +158,20 @@ struct mfh_net {
   };
   bool profiling = false;
   std::vector<Pending> pending;
+  // Forward graphs, keyed by batch size and the four device buffers; a key
+  // runs eagerly once before it is captured.
+  struct GraphKey {
+    int batch;
+    const void *masks, *values, *policy, *wdl;
+    bool operator<(const GraphKey &o) const {
+      return std::tie(batch, masks, values, policy, wdl) <
+             std::tie(o.batch, o.masks, o.values, o.policy, o.wdl);
+    }
+  };
+  bool graphs = true;
+  hipStream_t capture_stream = nullptr;
+  std::map<GraphKey, hipGraphExec_t> graph_execs;
+  std::set<GraphKey> graph_warm;
   std::vector<hipEvent_t> event_pool;
   std::map<std::string, Totals> totals;
 
@@ -462,6 +478,9 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
 // (smolgen dense1 -> LayerNorm, value dense1 -> value head).  It depends on K
 // only, so every position's result is bit-identical whatever the batch size
 // or the batch it shares a call with.
+// fp32 scratch for the split-K partials LaunchGemm may use on small batches.
+constexpr size_t kSplitKFloats = size_t(8) << 20;
+
 int SplitK(int k) {
   int s = 1;
   while (s < 8 && k % (2 * s * 64) == 0 && k / (2 * s) >= 256)
@@ -516,6 +535,8 @@ void PlanWorkspace(mfh_net *net) {
   add16("val_emb", M * d.Vd);
   add16("polqk", M * 2 * d.Dp);
   add("val1", skv * B * d.Vh * 4);
+  // Split-K partials of small-batch GEMMs.
+  add("splitk", kSplitKFloats * 4);
   add("policy", B * kPolicy * 4);
   add("wdl", B * 3 * 4);
   net->ws_bytes = AlignUp(off, 256);
@@ -609,6 +630,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     p.K = k;
     p.bias = bias;
     p.act = act;
+    p.partials = net->S<float>("splitk");
+    p.partials_floats = kSplitKFloats;
     p.out_mode = mode;
     p.C = C;
     p.C_lo = C_lo;
@@ -843,6 +866,55 @@ int CheckBatch(const mfh_net *net, int batch) {
 
 // Runs the staged batch in pin_in through the device and leaves outputs in
 // pin_out.  Caller holds net->mu.
+void DropGraphs(mfh_net *net) {
+  for (auto &kv : net->graph_execs)
+    (void)hipGraphExecDestroy(kv.second);
+  net->graph_execs.clear();
+  net->graph_warm.clear();
+}
+
+// Forward through a cached HIP graph (captured on the net's capture stream,
+// launched on `st`), or eagerly while profiling, for a key's first run, or
+// when graphs are off.  A graph bakes in the batch size and the buffers.
+int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
+               float *policy, float *wdl, hipStream_t st) {
+  if (!net->graphs || net->profiling)
+    return Forward(net, B, masks, values, policy, wdl, st);
+  const mfh_net::GraphKey key{B, masks, values, policy, wdl};
+  auto it = net->graph_execs.find(key);
+  if (it == net->graph_execs.end()) {
+    if (!net->graph_warm.count(key)) {
+      net->graph_warm.insert(key);
+      return Forward(net, B, masks, values, policy, wdl, st);
+    }
+    if (net->graph_execs.size() >= 64)
+      DropGraphs(net);
+    hipGraph_t graph = nullptr;
+    MFH_HIP_CHECK(hipStreamBeginCapture(net->capture_stream, hipStreamCaptureModeThreadLocal));
+    const int rc = Forward(net, B, masks, values, policy, wdl, net->capture_stream);
+    const hipError_t end = hipStreamEndCapture(net->capture_stream, &graph);
+    if (rc != MFH_OK || end != hipSuccess || !graph) {
+      if (graph)
+        (void)hipGraphDestroy(graph);
+      (void)hipGetLastError();
+      // Capture is not available here: stay eager from now on.
+      net->graphs = false;
+      return rc != MFH_OK ? rc : Forward(net, B, masks, values, policy, wdl, st);
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (inst != hipSuccess) {
+      (void)hipGetLastError();
+      net->graphs = false;
+      return Forward(net, B, masks, values, policy, wdl, st);
+    }
+    it = net->graph_execs.emplace(key, exec).first;
+  }
+  MFH_HIP_CHECK(hipGraphLaunch(it->second, st));
+  return MFH_OK;
+}
+
 int RunStaged(mfh_net *net, int batch) {
   const size_t n_in = static_cast<size_t>(batch) * kPlanes;
   auto *pin_masks = reinterpret_cast<std::uint64_t *>(net->pin_in);
@@ -855,7 +927,7 @@ int RunStaged(mfh_net *net, int batch) {
   MFH_HIP_CHECK(hipSetDevice(net->device));
   MFH_HIP_CHECK(hipMemcpyAsync(d_masks, pin_masks, n_in * 8, hipMemcpyHostToDevice, net->stream));
   MFH_HIP_CHECK(hipMemcpyAsync(d_values, pin_values, n_in * 4, hipMemcpyHostToDevice, net->stream));
-  const int rc = Forward(net, batch, d_masks, d_values, d_policy, d_wdl, net->stream);
+  const int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->stream);
   if (rc != MFH_OK) {
     (void)hipStreamSynchronize(net->stream);
     return rc;
@@ -953,8 +1025,9 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     if (raw->pin_in) (void)hipHostFree(raw->pin_in);
     if (raw->pin_out) (void)hipHostFree(raw->pin_out);
     if (raw->stream) (void)hipStreamDestroy(raw->stream);
+    if (raw->capture_stream) (void)hipStreamDestroy(raw->capture_stream);
     raw->weights = raw->ws = raw->pin_in = raw->pin_out = nullptr;
-    raw->stream = nullptr;
+    raw->stream = raw->capture_stream = nullptr;
   };
   if (hipMemcpy(net->weights, blob.bytes.data(), net->weight_bytes, hipMemcpyHostToDevice) !=
       hipSuccess) {
@@ -974,7 +1047,8 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     cleanup();
     return SetError(MFH_ERR_OUT_OF_MEMORY, "pinned staging allocation failed");
   }
-  if (hipStreamCreateWithFlags(&net->stream, hipStreamNonBlocking) != hipSuccess) {
+  if (hipStreamCreateWithFlags(&net->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&net->capture_stream, hipStreamNonBlocking) != hipSuccess) {
     cleanup();
     return SetError(MFH_ERR_HIP, "stream creation failed");
   }
@@ -986,10 +1060,12 @@ void mfh_net_destroy(mfh_net *net) {
   if (!net)
     return;
   (void)hipSetDevice(net->device);
-  if (net->stream) {
-    (void)hipStreamSynchronize(net->stream);
+  (void)hipDeviceSynchronize();
+  DropGraphs(net);
+  if (net->stream)
     (void)hipStreamDestroy(net->stream);
-  }
+  if (net->capture_stream)
+    (void)hipStreamDestroy(net->capture_stream);
   (void)CollectProfile(net);
   for (hipEvent_t e : net->event_pool)
     (void)hipEventDestroy(e);
@@ -1044,7 +1120,7 @@ int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
   std::lock_guard<std::mutex> lock(net->mu);
   MFH_HIP_CHECK(hipSetDevice(net->device));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = Forward(net, batch, d_masks, d_values, d_policy, d_wdl, st);
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, st);
   if (rc == MFH_OK)
     net->last_batch = batch;
   return rc;
@@ -1109,6 +1185,17 @@ int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t byt
   MFH_HIP_CHECK(hipSetDevice(net->device));
   MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
   MFH_HIP_CHECK(hipMemcpy(out, net->ws + net->ws_off.at(ws_name), size, hipMemcpyDeviceToHost));
+  return MFH_OK;
+}
+
+int mfh_net_set_graphs(mfh_net *net, int enabled) {
+  if (!net)
+    return SetError(MFH_ERR_INVALID, "null net");
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  MFH_HIP_CHECK(hipDeviceSynchronize());
+  DropGraphs(net);
+  net->graphs = enabled != 0;
   return MFH_OK;
 }
 

@@ -60,6 +60,10 @@ struct GemmParams {
   // K split over blockIdx.y; each slice writes fp32 partials to
   // C + slice * M * ldc (GEMM_OUT_F32, no bias/activation).
   int k_splits = 1;
+  // Optional fp32 scratch of partials_floats elements: lets LaunchGemm split
+  // K for small problems (partials summed by a second kernel).
+  float *partials = nullptr;
+  size_t partials_floats = 0;
   // Set by LaunchGemm: every output row start allows 4-column vector stores.
   bool vec = false;
 };
