@@ -9,14 +9,20 @@ outputs left in HBM (mfh_net_eval_device).  Weights are random-init (seeded,
 N(0, 1/fan_in)) stored as bf16; there is no network access for real nets.
 
 Prints one JSON line.  Besides the contract fields it carries:
-  roofline      -- the dominant kernel (the bf16 MFMA GEMM): algorithmic
-                   FLOPs of its launches / their summed duration, from HIP
-                   events recorded on the launch stream (mfh stage profiler);
-  cpu_baseline  -- the CPU oracle (a restatement of the reference CPU
-                   backend) timed on a bounded sample on this host's cores;
-  latency_batch1_ms -- p50 / p99 of single-position forwards;
-  mfma_util_pct -- executed MFMA work of the GEMMs against the dense bf16
-                   peak (twice the algorithmic work in bf16x2 precision).
+  roofline       -- the dominant kernel (the bf16 MFMA GEMM): algorithmic
+                    FLOPs of its launches / their summed duration, from HIP
+                    events recorded on the launch stream (mfh stage profiler);
+                    traffic from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+                    summarised in profiles/gemm_bf16_traffic.txt;
+  cpu_baseline   -- the CPU oracle (a restatement of the reference CPU
+                    backend) timed on a bounded sample on this host's cores;
+  small_batch    -- config 3: p50 / p99 latency, positions/s and weight-stream
+                    bandwidth at batches 1, 8, 32, 64;
+  encoder_layer  -- config 4: one encoder layer's time and MFMA utilisation at
+                    batches 256 and 1024 (bf16 activations);
+  precisions     -- batch-256 throughput of the other activation precisions;
+  mfma_util_pct  -- executed MFMA work of the GEMMs against the dense bf16
+                    peak (twice the algorithmic work in the split precisions).
 """
 
 from __future__ import annotations
@@ -32,7 +38,12 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 (no sparsity)
 PEAK_HBM_GBS = 8000.0
+GFLOP_PER_POSITION = 16.33  # BT4 shape, GEMM + attention + smolgen products
+LAYER_GFLOP_PER_POSITION = 1.033
 METRIC = "NN positions/sec at batch 256 (BT4-shape bf16, 1 GPU)"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_bf16_traffic.txt")
+BODY_ROLES = ("qkv", "out", "ffn1", "ffn2", "smolgen_dense1", "smolgen_dense2",
+              "smolgen_global")
 
 
 def parse_args():
@@ -41,13 +52,32 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=256)
-    ap.add_argument("--precision", choices=["bf16x2", "bf16"], default="bf16x2")
+    ap.add_argument("--precision", choices=["bf16x2", "bf16x2_gemm", "bf16"], default="bf16x2")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--latency-iters", type=int, default=100)
+    ap.add_argument("--latency-iters", type=int, default=200)
+    ap.add_argument("--small-batches", default="1,8,32,64")
+    ap.add_argument("--layer-batches", default="256,1024")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="only the headline, roofline and batch-1 latency")
     ap.add_argument("--cpu-positions", type=int, default=16,
                     help="positions in the CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy a 256 MiB buffer 5 times (the known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
+
+
+def copy_calibration():
+    import torch
+
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}))
 
 
 def cpu_baseline(spec, weights, planes, n, threads):
@@ -66,8 +96,111 @@ def cpu_baseline(spec, weights, planes, n, threads):
                       f"position per thread, {dt:.1f} s wall"}
 
 
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 counter summary
+    (key: value lines), or None when it is absent."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    vals = {}
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            if ":" in line and not line.lstrip().startswith("#"):
+                k, v = line.split(":", 1)
+                try:
+                    vals[k.strip()] = float(v.split()[0])
+                except (ValueError, IndexError):
+                    pass
+    return vals.get("hbm_bytes_per_launch")
+
+
+class Runner:
+    """One net plus device-resident inputs/outputs for up to max_batch."""
+
+    def __init__(self, backend, torch, np, spec, weights, masks, values, max_batch, precision,
+                 stream):
+        self.torch = torch
+        self.net = backend.create_network(spec, weights, max_batch=max_batch, device=0,
+                                          precision=precision)
+        reps = (max_batch + masks.shape[0] - 1) // masks.shape[0]
+        m = np.tile(masks, (reps, 1))[:max_batch]
+        v = np.tile(values, (reps, 1))[:max_batch]
+        self.d_masks = torch.from_numpy(np.ascontiguousarray(m).view(np.int64)).cuda()
+        self.d_values = torch.from_numpy(np.ascontiguousarray(v)).cuda()
+        self.d_policy = torch.empty((max_batch, 1858), dtype=torch.float32, device="cuda")
+        self.d_wdl = torch.empty((max_batch, 3), dtype=torch.float32, device="cuda")
+        self.stream = stream
+
+    def step(self, b):
+        self.net.eval_device(b, self.d_masks.data_ptr(), self.d_values.data_ptr(),
+                             self.d_policy.data_ptr(), self.d_wdl.data_ptr(),
+                             stream=self.stream.cuda_stream)
+
+    def time_steps(self, b, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            self.step(b)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(steps):
+            self.step(b)
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    def latencies(self, b, iters, warmup=5):
+        torch = self.torch
+        for _ in range(warmup):
+            self.step(b)
+        torch.cuda.synchronize()
+        lat = []
+        for _ in range(iters):
+            a = torch.cuda.Event(enable_timing=True)
+            z = torch.cuda.Event(enable_timing=True)
+            a.record(self.stream)
+            self.step(b)
+            z.record(self.stream)
+            z.synchronize()
+            lat.append(a.elapsed_time(z))
+        return lat
+
+    def profile(self, b, steps):
+        self.net.profile_reset()
+        self.net.set_profiling(True)
+        for _ in range(steps):
+            self.step(b)
+        self.torch.cuda.synchronize()
+        prof = self.net.profile()
+        self.net.set_profiling(False)
+        return prof
+
+    def close(self):
+        self.net.close()
+
+
+def gemm_totals(prof, roles=None, splitk=False):
+    """Summed ms / flops / launches of GEMM launches (by role if given)."""
+    ms = fl = by = 0.0
+    n = 0
+    for k, v in prof.items():
+        kind, _, role = k.partition(":")
+        if kind != ("gemm_bf16_splitk" if splitk else "gemm_bf16"):
+            continue
+        if roles is not None and role not in roles:
+            continue
+        ms += v["ms"]
+        fl += v["flops"]
+        by += v["bytes"]
+        n += v["launches"]
+    return {"ms": ms, "flops": fl, "bytes": by, "launches": n}
+
+
 def main():
     args = parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the "
               "transformer evaluation shards as independent positions per GPU with no "
@@ -84,33 +217,23 @@ def main():
     weights = synth.make_weights(spec, seed=args.seed)
     planes, _ = synth.playout_positions(B, seed=args.seed)
     masks, values = backend.pack_planes(planes)
-
-    net = backend.create_network(spec, weights, max_batch=B, device=0,
-                                 precision=args.precision)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
-    s = stream.cuda_stream
-    d_masks = torch.from_numpy(masks.view(np.int64)).cuda()
-    d_values = torch.from_numpy(values).cuda()
-    d_policy = torch.empty((B, 1858), dtype=torch.float32, device="cuda")
-    d_wdl = torch.empty((B, 3), dtype=torch.float32, device="cuda")
-    ptrs = (d_masks.data_ptr(), d_values.data_ptr(), d_policy.data_ptr(), d_wdl.data_ptr())
 
-    def step(b=B):
-        net.eval_device(b, *ptrs, stream=s)
+    run = Runner(backend, torch, np, spec, weights, masks, values, B, args.precision, stream)
+    weight_bytes = run.net.capabilities()["weight_bytes"]
 
+    # Timed region: exactly `steps` forwards after `warmup`, synchronised on
+    # both sides.
     for _ in range(args.warmup):
-        step()
+        run.step(B)
     torch.cuda.synchronize()
-
-    # Timed region: exactly `steps` forwards, synchronised on both sides.
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(args.steps):
-        step()
+        run.step(B)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -119,37 +242,83 @@ def main():
 
     # Per-kernel breakdown: the same steps again with the stage profiler's
     # HIP events on the launch stream.
-    net.profile_reset()
-    net.set_profiling(True)
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    prof = net.profile()
-    net.set_profiling(False)
-    gemm = prof.get("gemm_bf16", {"ms": 0.0, "flops": 0.0, "launches": 0, "bytes": 0.0})
-    gemm_ms = gemm["ms"]
-    achieved = gemm["flops"] / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
-    mfma_mult = 2.0 if args.precision == "bf16x2" else 1.0
+    prof = run.profile(B, args.steps)
+    gemm = gemm_totals(prof)
+    achieved = gemm["flops"] / (gemm["ms"] * 1e-3) / 1e12 if gemm["ms"] else 0.0
+    mfma_mult = 1.0 if args.precision == "bf16" else 2.0
     total_prof_ms = sum(v["ms"] for v in prof.values())
+    kinds = {}
+    for k, v in prof.items():
+        kind = k.split(":")[0]
+        agg = kinds.setdefault(kind, {"ms": 0.0, "launches": 0})
+        agg["ms"] += v["ms"]
+        agg["launches"] += v["launches"]
     breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 4),
                      "launches_per_step": v["launches"] // args.steps,
                      "share": round(v["ms"] / total_prof_ms, 4) if total_prof_ms else 0.0}
-                 for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+                 for k, v in sorted(kinds.items(), key=lambda kv: -kv[1]["ms"])}
+    gemm_roles = {}
+    for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+        if not k.startswith("gemm_bf16:") or not v["ms"]:
+            continue
+        gemm_roles[k.split(":", 1)[1]] = {
+            "ms_per_step": round(v["ms"] / args.steps, 4),
+            "alg_tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
+            "mfma_util_pct": round(100.0 * v["flops"] * mfma_mult / (v["ms"] * 1e-3) / 1e12 /
+                                   PEAK_BF16_TFLOPS, 1)}
 
-    # Batch-1 latency (MCTS single-leaf regime).
-    for _ in range(5):
-        step(1)
-    torch.cuda.synchronize()
-    lat = []
-    for _ in range(args.latency_iters):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        step(1)
-        b.record(stream)
-        b.synchronize()
-        lat.append(a.elapsed_time(b))
-    lat = np.array(lat)
+    # Batch-1 latency (MCTS single-leaf regime) and the other small batches
+    # (config 3); weights dominate the traffic, so bandwidth = weight bytes /
+    # latency.
+    lat1 = np.array(run.latencies(1, args.latency_iters)) if args.latency_iters > 0 else None
+    small = {}
+    if not args.no_extras:
+        for b in [int(x) for x in args.small_batches.split(",") if x]:
+            lat = np.array(lat1 if b == 1 and lat1 is not None else
+                           run.latencies(b, max(50, args.latency_iters // 2)))
+            p50 = float(np.percentile(lat, 50))
+            small[str(b)] = {
+                "p50_ms": round(p50, 4), "p99_ms": round(float(np.percentile(lat, 99)), 4),
+                "positions_per_s": round(b / (p50 * 1e-3), 1),
+                "weight_stream_gbs": round(weight_bytes / (p50 * 1e-3) / 1e9, 1),
+                "hbm_roofline_frac": round(weight_bytes / (p50 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "mfma_roofline_frac": round(GFLOP_PER_POSITION * 1e9 * b / (p50 * 1e-3) / 1e12 /
+                                            PEAK_BF16_TFLOPS, 4)}
+    run.close()
+
+    # Config 4: one encoder layer at the BT4 shape, bf16 activations.
+    layer = {}
+    if not args.no_extras:
+        lbs = [int(x) for x in args.layer_batches.split(",") if x]
+        lrun = Runner(backend, torch, np, spec, weights, masks, values, max(lbs), "bf16", stream)
+        for b in lbs:
+            lrun.time_steps(b, 2, 3)
+            p = lrun.profile(b, 3)
+            body = gemm_totals(p, BODY_ROLES)
+            attn = p.get("attention", {"ms": 0.0})["ms"]
+            per_layer_ms = (body["ms"] + attn) / 3 / spec.layers
+            enc = gemm_totals(p, ("qkv", "out", "ffn1", "ffn2"))
+            enc_tf = enc["flops"] / (enc["ms"] * 1e-3) / 1e12 if enc["ms"] else 0.0
+            layer[str(b)] = {
+                "layer_ms": round(per_layer_ms, 4),
+                "layer_gflop": round(LAYER_GFLOP_PER_POSITION * b, 1),
+                "layer_mfma_util_pct": round(100.0 * LAYER_GFLOP_PER_POSITION * b * 1e9 /
+                                             (per_layer_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 1),
+                "encoder_gemm_tflops": round(enc_tf, 1),
+                "encoder_gemm_mfma_util_pct": round(100.0 * enc_tf / PEAK_BF16_TFLOPS, 1)}
+        lrun.close()
+
+    # The other activation precisions at the headline batch.
+    precisions = {}
+    if not args.no_extras:
+        for prec in ("bf16x2", "bf16x2_gemm", "bf16"):
+            if prec == args.precision:
+                continue
+            r = Runner(backend, torch, np, spec, weights, masks, values, B, prec, stream)
+            ms = r.time_steps(B, max(5, args.steps // 2), 3)
+            precisions[prec] = {"positions_per_s": round(B / (ms * 1e-3), 1),
+                                "ms_per_step": round(ms, 4)}
+            r.close()
 
     cpu = None
     if args.cpu_positions > 0:
@@ -176,29 +345,33 @@ def main():
             "batch": B,
             "precision": args.precision,
             "weights": "bf16",
-            "algorithmic_gflop_per_position": 16.33,
+            "algorithmic_gflop_per_position": GFLOP_PER_POSITION,
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_bf16 (GemmKernel, all dense layers)",
+            "kernel": "gemm_bf16 (GemmKernel, all dense layers of the body and heads)",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": read_traffic(),
             "launches_per_step": gemm["launches"] // args.steps,
-            "avg_launch_us": round(gemm_ms * 1e3 / max(1, gemm["launches"]), 3),
+            "avg_launch_us": round(gemm["ms"] * 1e3 / max(1, gemm["launches"]), 3),
+            "algorithmic_bytes_per_launch": round(gemm["bytes"] / max(1, gemm["launches"])),
         },
         "mfma_util_pct": round(100.0 * achieved * mfma_mult / PEAK_BF16_TFLOPS, 2),
-        "whole_forward_tflops": round(16.33e9 * value / 1e12, 2),
-        "latency_batch1_ms": {"p50": round(float(np.percentile(lat, 50)), 4),
-                              "p99": round(float(np.percentile(lat, 99)), 4)},
+        "whole_forward_tflops": round(GFLOP_PER_POSITION * value / 1e3, 2),
+        "latency_batch1_ms": None if lat1 is None else {
+            "p50": round(float(np.percentile(lat1, 50)), 4),
+            "p99": round(float(np.percentile(lat1, 99)), 4)},
+        "small_batch": small,
+        "encoder_layer": layer,
+        "precisions": precisions,
         "kernel_breakdown": breakdown,
+        "gemm_roles": gemm_roles,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
-        "device": net.capabilities()["arch"],
     }
-    net.close()
     print(json.dumps(out))
 
 

@@ -560,7 +560,7 @@ struct StageTimer {
   hipStream_t st;
   mfh_net::Pending rec;
   bool on = false;
-  StageTimer(mfh_net *n, hipStream_t s, const char *name, double flops, double bytes)
+  StageTimer(mfh_net *n, hipStream_t s, const std::string &name, double flops, double bytes)
       : net(n), st(s) {
     if (!net->profiling)
       return;
@@ -594,10 +594,11 @@ int CollectProfile(mfh_net *net) {
   return MFH_OK;
 }
 
-const char *GemmKind(const mfh::GemmParams &p) {
-  if (p.k_splits > 1)
-    return "gemm_bf16_splitk";
-  return "gemm_bf16";
+// Profiler name of a GEMM launch: "gemm_bf16:<role>", or
+// "gemm_bf16_splitk:<role>" when the caller splits K (partials summed by the
+// consumer).
+std::string GemmKind(const mfh::GemmParams &p, const char *role) {
+  return std::string(p.k_splits > 1 ? "gemm_bf16_splitk:" : "gemm_bf16:") + role;
 }
 
 int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
@@ -639,13 +640,13 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     return p;
   };
   const double plane_mult = d.split ? 2.0 : 1.0;  // bytes of a bf16 activation
-  auto run = [&](const mfh::GemmParams &p) {
+  auto run = [&](const mfh::GemmParams &p, const char *role) {
     const double flops = 2.0 * p.M * p.N * p.K;
     const double out_bytes = p.out_mode == mfh::GEMM_OUT_BF16 ? 2.0 * plane_mult : 4.0;
     const double bytes = 2.0 * p.M * p.K * (p.A_lo ? 2.0 : 1.0) + 2.0 * p.N * p.K +
                          out_bytes * p.M * p.N * p.k_splits +
                          (p.out_mode == mfh::GEMM_OUT_RESID_F32 ? 4.0 * p.M * p.N : 0.0);
-    StageTimer t(net, st, GemmKind(p), flops, bytes);
+    StageTimer t(net, st, GemmKind(p, role), flops, bytes);
     return mfh::LaunchGemm(p, st, &err_);
   };
   auto run_ln = [&](const mfh::LayerNormParams &lp) {
@@ -690,7 +691,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     mfh::GemmParams p = gemm("pos_in", kSquares * 12, net->pre_w, kSquares * 12, B,
                              kSquares * d.P, kSquares * 12, net->W<float>(net->pre_b),
                              mfh::ACT_NONE, mfh::GEMM_OUT_F32, pe, nullptr, kSquares * d.P);
-    MFH_RUN(run(p));
+    MFH_RUN(run(p, "pe"));
   }
   {
     StageTimer tpe(net, st, "pe_scatter", 0.0, 4.0 * B * kSquares * d.P);
@@ -698,7 +699,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
                                  d.Kin, st, &err_));
   }
   MFH_RUN(run(gemm("emb_in", d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
-                   d.act_default, mfh::GEMM_OUT_F32, pre, nullptr, E)));
+                   d.act_default, mfh::GEMM_OUT_F32, pre, nullptr, E),
+                  "embedding"));
   {
     mfh::LayerNormParams lp = ln(pre, M, E, 1e-3f, net->W<float>(net->emb_ln_g),
                                  net->W<float>(net->emb_ln_b), resid, "act");
@@ -706,19 +708,22 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;
     MFH_RUN(run_ln(lp));
   }
-  auto residual_gemm = [&](const std::string &a, int k, size_t w_off, const float *bias) {
+  auto residual_gemm = [&](const std::string &a, int k, size_t w_off, const float *bias,
+                           const char *role) {
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
     p.resid = resid;
     p.ldr = E;
     p.alpha = d.alpha;
-    return run(p);
+    return run(p, role);
   };
   if (d.input_ffn) {
     MFH_RUN(run(gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
                      d.act_ffn, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"),
-                     net->Lo("hid"), d.Fi)));
-    MFH_RUN(residual_gemm("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b)));
+                     net->Lo("hid"), d.Fi),
+                "input_ffn1"));
+    MFH_RUN(residual_gemm("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
+                          "input_ffn2"));
     MFH_RUN(run_ln(ln(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
                       net->W<float>(net->in_ln_b), resid, "act")));
   }
@@ -734,7 +739,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       p.C2_lo = net->Lo("comp");
       p.ldc2 = d.C;
     }
-    MFH_RUN(run(p));
+    MFH_RUN(run(p, "qkv"));
     mfh::AttentionParams ap;
     ap.qkv = net->S<std::uint16_t>("qkv");
     ap.qkv_lo = net->Lo("qkv");
@@ -750,7 +755,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       mfh::GemmParams p1 = gemm("comp", flat, L.sg_d1_w, flat, B, d.Hs, flat, nullptr,
                                 mfh::ACT_NONE, mfh::GEMM_OUT_F32, sg1, nullptr, d.Hs);
       p1.k_splits = SplitK(flat);
-      MFH_RUN(run(p1));
+      MFH_RUN(run(p1, "smolgen_dense1"));
       mfh::LayerNormParams l1 = ln(sg1, B, d.Hs, 1e-3f, net->W<float>(L.sg_ln1_g),
                                    net->W<float>(L.sg_ln1_b), nullptr, "sg1n");
       l1.parts = p1.k_splits;
@@ -758,7 +763,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       l1.act = d.act_smolgen;
       MFH_RUN(run_ln(l1));
       MFH_RUN(run(gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr, mfh::ACT_NONE,
-                       mfh::GEMM_OUT_F32, sg2, nullptr, d.HG)));
+                       mfh::GEMM_OUT_F32, sg2, nullptr, d.HG),
+                  "smolgen_dense2"));
       mfh::LayerNormParams l2 = ln(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
                                    net->W<float>(L.sg_ln2_b), nullptr, "sg2n");
       l2.bias = net->W<float>(L.sg_d2_b);
@@ -768,7 +774,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       MFH_RUN(run(gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares, d.G,
                        nullptr, mfh::ACT_NONE,
                        d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16, bias, nullptr,
-                       kSquares * kSquares)));
+                       kSquares * kSquares),
+                  "smolgen_global"));
       ap.bias = bias;
       ap.bias_f32 = d.split_attn ? 1 : 0;
     }
@@ -783,12 +790,13 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       StageTimer t(net, st, "attention", flops, bytes);
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
     }
-    MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b)));
+    MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b), "out"));
     MFH_RUN(run_ln(ln(pre, M, E, d.eps_body, net->W<float>(L.ln1_g),
                       net->W<float>(L.ln1_b), resid, "act")));
     MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, d.F, E, net->W<float>(L.ffn1_b), d.act_ffn,
-                     mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), d.F)));
-    MFH_RUN(residual_gemm("hid", d.F, L.ffn2_w, net->W<float>(L.ffn2_b)));
+                     mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), d.F),
+                "ffn1"));
+    MFH_RUN(residual_gemm("hid", d.F, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2"));
     MFH_RUN(run_ln(ln(pre, M, E, d.eps_body, net->W<float>(L.ln2_g),
                       net->W<float>(L.ln2_b), resid, "act")));
   }
@@ -802,10 +810,11 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   ph.C2 = net->S<std::uint16_t>("val_emb");
   ph.C2_lo = net->Lo("val_emb");
   ph.ldc2 = d.Vd;
-  MFH_RUN(run(ph));
+  MFH_RUN(run(ph, "heads"));
   MFH_RUN(run(gemm("pol_emb", d.Dp, net->qk_w, d.Dp, M, 2 * d.Dp, d.Dp,
                    net->W<float>(net->qk_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
-                   net->S<std::uint16_t>("polqk"), net->Lo("polqk"), 2 * d.Dp)));
+                   net->S<std::uint16_t>("polqk"), net->Lo("polqk"), 2 * d.Dp),
+              "policy_qk"));
   {
     StageTimer t(net, st, "policy_map", 2.0 * B * kSquares * kSquares * d.Dp,
                  2.0 * plane_mult * M * 2.0 * d.Dp + 4.0 * B * kPolicy);
@@ -817,7 +826,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   mfh::GemmParams pv = gemm("val_emb", vflat, net->val1_w, vflat, B, d.Vh, vflat, nullptr,
                             mfh::ACT_NONE, mfh::GEMM_OUT_F32, val1, nullptr, d.Vh);
   pv.k_splits = SplitK(vflat);
-  MFH_RUN(run(pv));
+  MFH_RUN(run(pv, "value_dense1"));
   StageTimer tv(net, st, "value_head", 0.0, 4.0 * pv.k_splits * B * d.Vh);
   MFH_RUN(mfh::LaunchValueHead(val1, pv.k_splits, net->W<float>(net->val1_b), d.act_default, B,
                                d.Vh, net->W<float>(net->val2_w), net->W<float>(net->val2_b),
