@@ -2,10 +2,13 @@
 // promotion logits and the gather into the 1858-move policy
 // (reference src/nn/cpu/cpu_network.cpp:892-1025, gather table 91-103).
 //
-// One workgroup per position.  Wave w computes query rows 16w..16w+15 of
-// raw = Q K^T / sqrt(Dp) with v_mfma_f32_16x16x32_bf16 straight from global
-// memory (Q and K rows are K-contiguous); the 64x64 fp32 block goes to LDS.
-// The promotion logit for p in [0,192) is, as in the reference,
+// One workgroup of 16 waves per position.  Wave w computes query rows
+// 16 (w % 4) .. + 15 of Q K^T over the interleaved quarter of the Dp
+// dimension starting at 32 (w / 4), with v_mfma_f32_16x16x32_bf16 straight
+// from global memory (Q and K rows are K-contiguous); the four partial 64x64
+// blocks go to LDS and are summed in a fixed order, then scaled by
+// 1 / sqrt(Dp).  The promotion logit for p in [0,192) is, as in the
+// reference,
 //   raw[48 + (p%64)/8][56 + (p%64)%8] + K[56 + (p%24)/3] . (promo[p%3] + promo[3]).
 // The 24 promotion-offset dot products are formed once per position.
 // Split precision: Q and K arrive as hi + lo planes and each fragment product
@@ -20,14 +23,15 @@ constexpr int kSq = 64;
 constexpr int kOutputs = 1858;
 
 template <bool SPLIT>
-__global__ __launch_bounds__(256) void PolicyMapKernel(
+__global__ __launch_bounds__(1024) void PolicyMapKernel(
     const std::uint16_t *__restrict__ qk, const std::uint16_t *__restrict__ qk_lo, int dp,
     float scale, const float *__restrict__ promo, const std::int16_t *__restrict__ gather,
     float *__restrict__ policy) {
-  __shared__ float raw[kSq * kSq];
+  __shared__ float part[4][kSq * kSq];
   __shared__ float pk_term[24];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int qb = wave & 3, dc = wave >> 2;
   const int b = blockIdx.x;
   const size_t ld = static_cast<size_t>(2) * dp;
   const size_t pos = static_cast<size_t>(b) * kSq * ld;
@@ -38,21 +42,25 @@ __global__ __launch_bounds__(256) void PolicyMapKernel(
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const size_t qoff = (wave * 16 + fr) * ld + fc;
-  for (int k0 = 0; k0 < dp; k0 += 32) {
+  const size_t qoff = (qb * 16 + fr) * ld + fc;
+#pragma unroll 2
+  for (int k0 = dc * 32; k0 < dp; k0 += 128) {
     const bf16x8 a = *reinterpret_cast<const bf16x8 *>(base + qoff + k0);
-    bf16x8 a_lo;
-    if constexpr (SPLIT)
-      a_lo = *reinterpret_cast<const bf16x8 *>(qk_lo + pos + qoff + k0);
+    bf16x8 kb[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const size_t koff = (j * 16 + fr) * ld + dp + fc + k0;
-      const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(base + koff);
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kb, acc[j], 0, 0, 0);
-      if constexpr (SPLIT) {
-        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(qk_lo + pos + koff);
+    for (int j = 0; j < 4; ++j)
+      kb[j] = *reinterpret_cast<const bf16x8 *>(base + (j * 16 + fr) * ld + dp + fc + k0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kb[j], acc[j], 0, 0, 0);
+    if constexpr (SPLIT) {
+      const bf16x8 a_lo = *reinterpret_cast<const bf16x8 *>(qk_lo + pos + qoff + k0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(qk_lo + pos + (j * 16 + fr) * ld +
+                                                            dp + fc + k0);
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, kl, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, kb, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, kb[j], acc[j], 0, 0, 0);
       }
     }
   }
@@ -60,11 +68,10 @@ __global__ __launch_bounds__(256) void PolicyMapKernel(
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      raw[(wave * 16 + (lane >> 4) * 4 + r) * kSq + j * 16 + fr] = acc[j][r] * scale;
+      part[dc][(qb * 16 + (lane >> 4) * 4 + r) * kSq + j * 16 + fr] = acc[j][r];
 
-  // Promotion offsets: term[t][tf] = K[56+tf] . (promo[t] + promo[3]),
-  // six dot products per wave.
-  for (int d = wave; d < 24; d += 4) {
+  // Promotion offsets: term[t][tf] = K[56+tf] . (promo[t] + promo[3]).
+  for (int d = wave; d < 24; d += 16) {
     const int t = d / 8, tf = d % 8;
     const size_t koff = (56 + tf) * ld + dp;
     float s = 0.f;
@@ -81,15 +88,16 @@ __global__ __launch_bounds__(256) void PolicyMapKernel(
   __syncthreads();
 
   float *out = policy + static_cast<size_t>(b) * kOutputs;
-  for (int i = threadIdx.x; i < kOutputs; i += 256) {
+  auto raw = [&](int i) { return (((part[0][i] + part[1][i]) + part[2][i]) + part[3][i]) * scale; };
+  for (int i = threadIdx.x; i < kOutputs; i += 1024) {
     const int r = gather[i];
     float v = 0.f;
     if (r >= 0 && r < kSq * kSq) {
-      v = raw[r];
+      v = raw(r);
     } else if (r >= kSq * kSq) {
       const int p = r - kSq * kSq;
       const int pair = p % kSq;
-      v = raw[(48 + pair / 8) * kSq + 56 + pair % 8] + pk_term[(p % 3) * 8 + (p % 24) / 3];
+      v = raw((48 + pair / 8) * kSq + 56 + pair % 8) + pk_term[(p % 3) * 8 + (p % 24) / 3];
     }
     out[i] = v;
   }
@@ -109,10 +117,10 @@ hipError_t LaunchPolicyMap(const std::uint16_t *qk, const std::uint16_t *qk_lo, 
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(dp));
   if (qk_lo)
-    hipLaunchKernelGGL(PolicyMapKernel<true>, dim3(batch), dim3(256), 0, stream, qk, qk_lo, dp,
+    hipLaunchKernelGGL(PolicyMapKernel<true>, dim3(batch), dim3(1024), 0, stream, qk, qk_lo, dp,
                        scale, promo, gather, policy);
   else
-    hipLaunchKernelGGL(PolicyMapKernel<false>, dim3(batch), dim3(256), 0, stream, qk, qk_lo, dp,
+    hipLaunchKernelGGL(PolicyMapKernel<false>, dim3(batch), dim3(1024), 0, stream, qk, qk_lo, dp,
                        scale, promo, gather, policy);
   return hipGetLastError();
 }
