@@ -490,12 +490,18 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     }
   }
   const int kslice = p.K / p.k_splits;
-  // Tile choice measured on MI355X at the BT4 body shapes (M = 16384):
-  // split precision runs 64 x 128 tiles (A hi + lo + W = 64 KiB of LDS for
-  // two stages, two workgroups per CU), bf16 runs 128 x 128.
-  if (large && kslice % 64 == 0)
+  // Tile choice measured on MI355X at the BT4 body shapes (M = 16384): for
+  // K <= 1024, eight waves per workgroup on BK = 32 steps (split precision
+  // 128 x 128 tiles as 2 x 4 waves, bf16 256 x 128 tiles as 4 x 2 waves,
+  // 48 KiB of LDS for two stages); for longer K, four waves on BK = 64
+  // (split 64 x 128, bf16 128 x 128).
+  if (large && kslice % 64 == 0) {
+    if (kslice <= 1024)
+      return split ? Launch<128, 128, 32, 2, 2, 4, true>(p, stream)
+                   : Launch<256, 128, 32, 2, 4, 2, false>(p, stream);
     return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
                  : Launch<128, 128, 64, 2, 2, 2, false>(p, stream);
+  }
   if (kslice % 64 == 0)
     return split ? Launch<64, 64, 64, 2, 2, 2, true>(p, stream)
                  : Launch<64, 64, 64, 2, 2, 2, false>(p, stream);

@@ -137,6 +137,22 @@ def test_bt4_net_parity_16_positions(precision):
         assert top1 >= 0.995
 
 
+@pytest.mark.parametrize("precision", ["bf16x2", "bf16"])
+def test_bt4_large_batch_tiles(precision):
+    """40 positions = 2560 token rows: the dense layers take the large-M tile
+    configurations (the ones the batch-256 benchmark runs)."""
+    gpu, ref, legal = _compare("bt4", 40, check_packed=False, precision=precision)
+    perr = np.abs(gpu["policy"] - ref["policy"]).max()
+    werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
+    top1 = _top1_agreement(gpu["policy"], ref["policy"], legal)
+    print(f"bt4 x40 {precision}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}")
+    assert perr <= POLICY_TOL
+    assert werr <= WDL_TOL
+    if precision == "bf16x2":
+        assert perr <= 1e-3
+        assert top1 >= 0.995
+
+
 def test_batch_neighbours_and_chunking():
     """A position's outputs do not depend on its batch neighbours or on
     chunking (reference single-vs-batched parity, test_nn_comparison.cpp:
