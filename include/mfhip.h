@@ -55,8 +55,12 @@ enum {
 };
 /* NetworkFormat.DefaultActivation (net.proto:331-332). */
 enum { MFH_DEFAULT_ACTIVATION_RELU = 0, MFH_DEFAULT_ACTIVATION_MISH = 1 };
-/* Storage of the GEMM weights on the device. */
-enum { MFH_WEIGHTS_BF16 = 0 };
+/* Storage of the GEMM weights on the device.  BF16: each weight rounded to
+ * bf16.  FP8: each output row of a GEMM weight stored as OCP e4m3 codes
+ * (round to nearest even, saturating at 448) with one fp32 scale
+ * max|row| / 448; the kernels convert the codes exactly to bf16 and apply the
+ * scale to the accumulated row, halving weight bytes. */
+enum { MFH_WEIGHTS_BF16 = 0, MFH_WEIGHTS_FP8 = 1 };
 /* Activation precision.  BF16: every MFMA operand is one bf16 value (fastest).
  * BF16X2: activations are carried as a bf16 pair hi + lo (lo = bf16(x - hi))
  * and every product takes two (GEMMs) or three (attention, policy map)
@@ -78,7 +82,7 @@ typedef struct {
   int ffn_activation;     /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
   int smolgen_activation; /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
   int headcount;          /* body attention heads; head depth must be 32 */
-  int weights_dtype;      /* MFH_WEIGHTS_BF16 */
+  int weights_dtype;      /* MFH_WEIGHTS_BF16 or MFH_WEIGHTS_FP8 */
   int precision;          /* MFH_PRECISION_* */
   int max_batch;          /* largest batch one eval call accepts (>= 1) */
   int device;             /* HIP device ordinal, -1 = current device */
@@ -176,6 +180,12 @@ int mfh_net_profile_reset(mfh_net *net);
  * planes[batch*112*64] -> masks[batch*112], values[batch*112]. */
 int mfh_pack_planes(int batch, const float *planes, uint64_t *masks,
                     float *values);
+
+/* The FP8 weight quantisation of MFH_WEIGHTS_FP8 on the host (no device
+ * needed; no counterpart in the reference, which stores fp16/fp32 weights):
+ * w[rows*cols] row-major -> codes[rows*cols] e4m3 and scale[rows]. */
+int mfh_debug_quantize_fp8(int rows, int cols, const float *w, uint8_t *codes,
+                           float *scale);
 
 /* Number of visible devices (0 without a GPU). */
 int mfh_device_count(int *count);

@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(_PKG, "libmfhip.so")
 
 MFH_OK = 0
 PRECISION = {"bf16": 0, "bf16x2": 1, "bf16x2_gemm": 2}
+WEIGHTS = {"bf16": 0, "fp8": 1}
 ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid": 5,
               "selu": 6, "swish": 7, "relu_2": 8}
 
@@ -30,7 +31,7 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_net_set_graphs", "mfh_net_set_profiling", "mfh_net_profile",
            "mfh_net_profile_reset",
            "mfh_pack_planes", "mfh_device_count", "mfh_last_error", "mfh_debug_unpack_planes",
-           "mfh_debug_gemm_bf16", "mfh_net_debug_tensor")
+           "mfh_debug_gemm_bf16", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8")
 
 
 class MfhNetDesc(ctypes.Structure):
@@ -87,6 +88,7 @@ def lib():
             "mfh_debug_unpack_planes": ([i, vp, vp, vp], i),
             "mfh_debug_gemm_bf16": ([i, i, i, vp, vp, vp, i, vp], i),
             "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
+            "mfh_debug_quantize_fp8": ([i, i, vp, vp, vp], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -117,7 +119,7 @@ class HipNetwork:
 
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
-                 device=-1, precision="bf16x2"):
+                 device=-1, precision="bf16x2", weights_dtype="bf16"):
         self._weights = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
                          for k, v in weights.items()}
         names = list(self._weights)
@@ -131,7 +133,7 @@ class HipNetwork:
                           default_activation=1 if default_activation == "mish" else 0,
                           ffn_activation=ACTIVATION[ffn_activation],
                           smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
-                          weights_dtype=0, precision=PRECISION[precision],
+                          weights_dtype=WEIGHTS[weights_dtype], precision=PRECISION[precision],
                           max_batch=max_batch, device=device)
         handle = ctypes.c_void_p()
         self._h = None
@@ -141,6 +143,7 @@ class HipNetwork:
         self.wdl = wdl
         self.max_batch = max_batch
         self.precision = precision
+        self.weights_dtype = weights_dtype
         # Host weights are only needed for the upload.
         self._weights = None
 
@@ -262,6 +265,18 @@ def unpack_planes(masks, values):
     return out
 
 
+def quantize_fp8(w):
+    """The library's host e4m3 row quantisation: (codes uint8, scales fp32)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows = w.shape[0]
+    cols = w.size // rows
+    codes = np.zeros((rows, cols), np.uint8)
+    scale = np.zeros(rows, np.float32)
+    _check(lib().mfh_debug_quantize_fp8(rows, cols, _ptr(w), _ptr(codes), _ptr(scale)),
+           "mfh_debug_quantize_fp8")
+    return codes, scale
+
+
 def gemm_bf16(a_bits, w_bits, bias=None, act="none"):
     a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
     w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
@@ -274,12 +289,14 @@ def gemm_bf16(a_bits, w_bits, bias=None, act="none"):
     return out
 
 
-def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2"):
+def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
+                   weights_dtype="bf16"):
     """HipNetwork for a synth.NetSpec and its weights.  ``precision`` is
-    "bf16x2" (split activations, default: meets every parity gate) or "bf16"
-    (single-pass, twice the MFMA throughput)."""
+    "bf16x2" (split activations, default: meets every parity gate),
+    "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput);
+    ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales)."""
     return HipNetwork(weights, spec.heads, wdl=spec.wdl,
                       default_activation=spec.default_activation,
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,
-                      device=device, precision=precision)
+                      device=device, precision=precision, weights_dtype=weights_dtype)

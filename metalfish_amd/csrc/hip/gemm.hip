@@ -20,6 +20,12 @@
 // ends up holding four consecutive output columns of one row: the epilogue
 // stores 8 bytes (bf16) or 16 bytes (fp32) per lane instead of 2 or 4.
 //
+// FP8 weights (W8): the weight tile skips LDS.  Each wave loads its own
+// fragments (8 e4m3 codes = 8 bytes per lane) from global memory one K step
+// ahead, converts them exactly to bf16 with v_cvt_scalef32_pk_bf16_fp8, and
+// the row scale multiplies the accumulators in the epilogue (or the split-K
+// partials).
+//
 // Split precision: when A_lo is set, the activation is carried as
 // hi + lo bf16 planes (lo = bf16(x - hi)) and every fragment pair issues two
 // MFMAs, giving ~16-bit activation precision against exact bf16 weights.
@@ -47,6 +53,15 @@ __device__ __forceinline__ int Swz(int row, int chunk) {
     return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3);
 }
 
+// Eight e4m3 codes (bytes of q, lowest first) as eight bf16 values; exact.
+__device__ __forceinline__ bf16x8 Fp8x8ToBf16(u32x2 q) {
+  const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, false);
+  const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, true);
+  const auto c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, false);
+  const auto d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // Activation with a compile-time kind; ACT_RUNTIME defers to p.act.
 constexpr int ACT_RUNTIME = -2;
 template <int ACT>
@@ -66,6 +81,11 @@ template <int MODE, int ACT>
 __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col, f32x4 acc,
                                           const float (&b)[4]) {
   const bool full = p.vec && col + 3 < p.N;
+  if (p.wscale) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      acc[r] *= col + r < p.N ? p.wscale[col + r] : 0.f;
+  }
   float v[4];
   if constexpr (MODE == GEMM_OUT_RESID_F32) {
     float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
@@ -130,7 +150,8 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
   }
 }
 
-template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
+          bool W8>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -138,8 +159,10 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int CPR = BK / 8;                      // 16-byte chunks per LDS row
   constexpr int RPL = 64 / CPR;                    // rows per 1 KiB wave-load
   constexpr int A_ROWS = SPLIT ? 2 * BM : BM;      // hi rows then lo rows
-  constexpr int STAGE = (A_ROWS + BN) * BK;        // bf16 elements per stage
-  constexpr int LOADS = (A_ROWS + BN) * BK * 2 / 1024;
+  constexpr int W_ROWS = W8 ? 0 : BN;              // weight rows staged in LDS
+  constexpr int STAGE = (A_ROWS + W_ROWS) * BK;    // bf16 elements per stage
+  constexpr int LOADS = (A_ROWS + W_ROWS) * BK * 2 / 1024;
+  static_assert(!W8 || ST == 2, "fp8 weights use the two-stage loop");
   static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
   static_assert(LOADS % NWAVES == 0, "stage loads must split evenly over waves");
   constexpr int LPW = LOADS / NWAVES;
@@ -196,6 +219,22 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   }
 
   const int KT = kslice / BK;
+  constexpr int KK = BK / 32;
+  const int fr = lane & 15, fc = lane >> 4;
+  // FP8 weight fragments: lane reads 8 codes of row n at k offset 8 fc.
+  const std::uint8_t *wsrc[TN];
+  u32x2 wq[KK][TN];
+  if constexpr (W8) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      wsrc[j] = p.W8 + static_cast<size_t>(min(n0 + wn * WTN + j * 16 + fr, p.N - 1)) * p.ldw +
+                k_begin + fc * 8;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        wq[kk][j] = *reinterpret_cast<const u32x2 *>(wsrc[j] + kk * 32);
+  }
   // Stages 0 .. ST-2 in flight before the loop.
 #pragma unroll
   for (int s = 0; s < ST - 1; ++s)
@@ -214,7 +253,6 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     for (int j = 0; j < TN; ++j)
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int fr = lane & 15, fc = lane >> 4;
   int slot = 0;                       // kt % ST
   int fill = (ST - 1) % ST;           // (kt + ST - 1) % ST
   for (int kt = 0; kt < KT; ++kt) {
@@ -242,13 +280,28 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     slot = slot + 1 == ST ? 0 : slot + 1;
     fill = fill + 1 == ST ? 0 : fill + 1;
     const std::uint16_t *sw = sa + A_ROWS * BK;
+    u32x2 wn_next[KK][TN];
+    if constexpr (W8) {
+      if (kt + 1 < KT) {
 #pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            wn_next[kk][j] =
+                *reinterpret_cast<const u32x2 *>(wsrc[j] + (kt + 1) * BK + kk * 32);
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
       bf16x8 af[TM], bw[TN];
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bw[j] = *reinterpret_cast<const bf16x8 *>(
-            sw + Swz<BK>(wn * WTN + j * 16 + fr, kk * 4 + fc));
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (W8)
+          bw[j] = Fp8x8ToBf16(wq[kk][j]);
+        else
+          bw[j] = *reinterpret_cast<const bf16x8 *>(
+              sw + Swz<BK>(wn * WTN + j * 16 + fr, kk * 4 + fc));
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
         af[i] = *reinterpret_cast<const bf16x8 *>(
@@ -271,6 +324,13 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
                 __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
       }
     }
+    if constexpr (W8) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          wq[kk][j] = wn_next[kk][j];
+    }
   }
 
   // Transposed accumulator layout: lane holds output row m_base + lane % 16
@@ -288,13 +348,19 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int col = col_base + j * 16;
+        f32x4 v = acc[i][j];
+        if (p.wscale) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            v[r] *= col + r < p.N ? p.wscale[col + r] : 0.f;
+        }
         if (p.vec && col + 3 < p.N) {
-          *reinterpret_cast<f32x4 *>(c + col) = acc[i][j];
+          *reinterpret_cast<f32x4 *>(c + col) = v;
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             if (col + r < p.N)
-              c[col + r] = acc[i][j][r];
+              c[col + r] = v[r];
         }
       }
     }
@@ -350,11 +416,12 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
   Epilogue4<MODE, ACT>(p, row, col, a, b);
 }
 
-template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
+          bool W8 = false>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   constexpr int A_ROWS = SPLIT ? 2 * BM : BM;
-  constexpr size_t kLds = static_cast<size_t>(ST) * (A_ROWS + BN) * BK * 2;
-  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT>;
+  constexpr size_t kLds = static_cast<size_t>(ST) * (A_ROWS + (W8 ? 0 : BN)) * BK * 2;
+  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&]() {
@@ -393,21 +460,28 @@ hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_
 
 // Epilogue dispatch: the activations the network uses (none, mish) get
 // dedicated instances, anything else the runtime switch.
-template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
-hipError_t Launch(const GemmParams &p, hipStream_t stream) {
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8>
+hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
   if (p.k_splits > 1 || (p.out_mode == GEMM_OUT_F32 && p.act == ACT_NONE))
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8>(p, stream);
   if (p.out_mode == GEMM_OUT_RESID_F32)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8>(p, stream);
   if (p.out_mode == GEMM_OUT_F32)
     return p.act == ACT_MISH
-               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH>(p, stream)
-               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME>(p, stream);
+               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8>(p, stream)
+               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8>(p, stream);
   if (p.act == ACT_NONE)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8>(p, stream);
   if (p.act == ACT_MISH)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH>(p, stream);
-  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8>(p, stream);
+  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8>(p, stream);
+}
+
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
+hipError_t Launch(const GemmParams &p, hipStream_t stream) {
+  if (p.W8)
+    return LaunchW<BM, BN, BK, ST, WM, WN, SPLIT, true>(p, stream);
+  return LaunchW<BM, BN, BK, ST, WM, WN, SPLIT, false>(p, stream);
 }
 
 bool Aligned(const void *ptr, std::uintptr_t bytes) {
@@ -432,10 +506,13 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   if (p.k_splits > 1 && (p.out_mode != GEMM_OUT_F32 || p.bias || p.act != ACT_NONE ||
                          p.split_n < p.N))
     return fail("split-K writes raw fp32 partials only (no bias, activation or split)");
-  if (!p.A || !p.W || !p.C)
-    return fail("null operand");
-  if (!Aligned(p.A, 16) || !Aligned(p.W, 16) || (p.A_lo && !Aligned(p.A_lo, 16)) ||
-      p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
+  if (!p.A || (!p.W && !p.W8) || (p.W && p.W8) || !p.C)
+    return fail("null operand (or both W and W8)");
+  if (p.W8 && !p.wscale)
+    return fail("fp8 weights need row scales");
+  if (!Aligned(p.A, 16) || (p.W && !Aligned(p.W, 16)) || (p.W8 && !Aligned(p.W8, 8)) ||
+      (p.A_lo && !Aligned(p.A_lo, 16)) || p.lda % 8 || p.ldw % 8 || p.lda < p.K ||
+      p.ldw < p.K)
     return fail("operands must be 16-byte aligned with ld >= K, ld % 8 == 0");
   if (p.out_mode == GEMM_OUT_RESID_F32 && (!p.resid || p.split_n < p.N))
     return fail("residual mode needs resid and no split");
@@ -486,7 +563,10 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
                                  : Launch<64, 64, 64, 2, 2, 2, false>(q, stream);
       if (e != hipSuccess)
         return e;
-      return Reduce(p, p.partials, splits, stream);
+      // The partials already carry the fp8 row scale.
+      GemmParams r = p;
+      r.wscale = nullptr;
+      return Reduce(r, p.partials, splits, stream);
     }
   }
   const int kslice = p.K / p.k_splits;

@@ -58,6 +58,40 @@ std::uint16_t ToBf16(float f) {
   return static_cast<std::uint16_t>(u >> 16);
 }
 
+// OCP e4m3 (bias 7, no infinities, 0x7F = NaN, largest finite 448) of a
+// finite x, rounding to nearest even and saturating at +-448.
+std::uint8_t EncodeE4m3(float x) {
+  std::uint32_t u;
+  std::memcpy(&u, &x, 4);
+  const std::uint8_t sign = static_cast<std::uint8_t>((u >> 24) & 0x80u);
+  u &= 0x7FFFFFFFu;
+  float a;
+  std::memcpy(&a, &u, 4);
+  std::uint8_t code;
+  if (a < 0.015625f) {  // below 2^-6: subnormal codes m * 2^-9, m = 0..8
+    code = static_cast<std::uint8_t>(std::nearbyint(a * 512.0f));
+  } else {
+    // Keep 3 mantissa bits with round-to-nearest-even on the fp32 pattern.
+    const std::uint32_t r = u + 0x7FFFFu + ((u >> 20) & 1u);
+    const int e = static_cast<int>(r >> 23) - 127;
+    const int m = static_cast<int>((r >> 20) & 7u);
+    code = e > 8 || (e == 8 && m == 7) ? 0x7E : static_cast<std::uint8_t>(((e + 7) << 3) | m);
+  }
+  return static_cast<std::uint8_t>(sign | code);
+}
+
+// Row scale max|row| / 448 (1 for an all-zero row) and e4m3 codes of
+// row / scale.
+void QuantizeRowE4m3(const float *row, int n, std::uint8_t *codes, float *scale) {
+  float mx = 0.f;
+  for (int i = 0; i < n; ++i)
+    mx = std::fmax(mx, std::fabs(row[i]));
+  const float s = mx > 0.f ? mx / 448.0f : 1.0f;
+  for (int i = 0; i < n; ++i)
+    codes[i] = EncodeE4m3(row[i] / s);
+  *scale = s;
+}
+
 int ActFromProto(int proto_act, int default_act) {
   switch (proto_act) {
   case MFH_ACTIVATION_DEFAULT: return default_act;
@@ -102,10 +136,11 @@ struct Blob {
 };
 
 struct Layer {
-  size_t qkv_w, qkv_b, out_w, out_b, ln1_g, ln1_b, ffn1_w, ffn1_b, ffn2_w, ffn2_b,
-      ln2_g, ln2_b;
+  size_t qkv_b, out_b, ln1_g, ln1_b, ffn1_b, ffn2_b, ln2_g, ln2_b;
+  size_t qkv_w[2], out_w[2], ffn1_w[2], ffn2_w[2];  // {weights, fp8 row scales}
   bool smolgen = false;
-  size_t sg_d1_w, sg_d1_b, sg_ln1_g, sg_ln1_b, sg_d2_w, sg_d2_b, sg_ln2_g, sg_ln2_b;
+  size_t sg_d1_b, sg_ln1_g, sg_ln1_b, sg_d2_b, sg_ln2_g, sg_ln2_b;
+  size_t sg_d1_w[2], sg_d2_w[2];
 };
 
 struct Dims {
@@ -132,11 +167,14 @@ struct mfh_net {
   unsigned char *weights = nullptr;
   size_t weight_bytes = 0;
   // Offsets into `weights`.
-  size_t pre_w, pre_b, emb_w, emb_b, emb_ln_g, emb_ln_b, mult_gate, add_gate;
-  size_t in_ffn1_w, in_ffn1_b, in_ffn2_w, in_ffn2_b, in_ln_g, in_ln_b;
-  size_t global_w;
+  // GEMM weights are {offset, fp8 row-scale offset} pairs.
+  bool fp8 = false;
+  size_t pre_b, emb_b, emb_ln_g, emb_ln_b, mult_gate, add_gate;
+  size_t pre_w[2], emb_w[2], in_ffn1_w[2], in_ffn2_w[2], global_w[2];
+  size_t in_ffn1_b, in_ffn2_b, in_ln_g, in_ln_b;
   std::vector<Layer> layers;
-  size_t head_w, head_b, qk_w, qk_b, promo, val1_w, val1_b, val2_w, val2_b, gather;
+  size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
+  size_t head_w[2], qk_w[2], val1_w[2];
 
   unsigned char *ws = nullptr;
   size_t ws_bytes = 0;
@@ -242,6 +280,37 @@ size_t AddBf16(Blob &blob, const std::vector<const float *> &parts,
   return blob.Add(buf.data(), buf.size() * 2);
 }
 
+// A GEMM weight in the blob: bf16 [rows][ld], or e4m3 codes [rows][ld]
+// plus fp32 row scales at `s`.
+struct GemmW {
+  size_t w = 0, s = 0;
+};
+
+GemmW AddGemmW(Blob &blob, bool fp8, const std::vector<const float *> &parts,
+               const std::vector<int> &part_rows, int cols, int ld) {
+  if (!fp8)
+    return GemmW{AddBf16(blob, parts, part_rows, cols, ld), 0};
+  size_t rows = 0;
+  for (int r : part_rows)
+    rows += r;
+  std::vector<std::uint8_t> codes(rows * ld, 0);
+  std::vector<float> scales(rows, 1.0f);
+  std::vector<float> tmp(ld);
+  size_t row = 0;
+  for (size_t p = 0; p < parts.size(); ++p) {
+    for (int r = 0; r < part_rows[p]; ++r, ++row) {
+      std::fill(tmp.begin(), tmp.end(), 0.f);
+      if (parts[p])
+        std::memcpy(tmp.data(), parts[p] + static_cast<size_t>(r) * cols, cols * 4);
+      QuantizeRowE4m3(tmp.data(), ld, codes.data() + row * ld, &scales[row]);
+    }
+  }
+  GemmW g;
+  g.w = blob.Add(codes.data(), codes.size());
+  g.s = blob.Add(scales.data(), scales.size() * 4);
+  return g;
+}
+
 size_t AddF32(Blob &blob, const std::vector<const float *> &parts,
               const std::vector<int> &counts) {
   std::vector<float> buf;
@@ -264,7 +333,7 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   if (desc.input_embedding != MFH_INPUT_EMBEDDING_PE_DENSE)
     return SetError(MFH_ERR_UNSUPPORTED,
                     "HIP backend supports INPUT_EMBEDDING_PE_DENSE only (as the reference CPU backend)");
-  if (desc.weights_dtype != MFH_WEIGHTS_BF16)
+  if (desc.weights_dtype != MFH_WEIGHTS_BF16 && desc.weights_dtype != MFH_WEIGHTS_FP8)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
   if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2 &&
       desc.precision != MFH_PRECISION_BF16X2_GEMM)
@@ -340,6 +409,11 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   return MFH_OK;
 }
 
+void SetW(size_t (&dst)[2], const GemmW &g) {
+  dst[0] = g.w;
+  dst[1] = g.s;
+}
+
 int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   const Dims &d = net->d;
   const int E = d.E, S = kSquares;
@@ -352,9 +426,9 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   const float *ln_b = need("body.ip_emb_ln_betas", E);
   if (!ld.error.empty())
     return SetError(MFH_ERR_INVALID, ld.error);
-  net->pre_w = AddBf16(blob, {pre_w}, {S * d.P}, S * 12, S * 12);
+  SetW(net->pre_w, AddGemmW(blob, net->fp8, {pre_w}, {S * d.P}, S * 12, S * 12));
   net->pre_b = AddF32(blob, {pre_b}, {S * d.P});
-  net->emb_w = AddBf16(blob, {emb_w}, {E}, kPlanes + d.P, d.Kin);
+  SetW(net->emb_w, AddGemmW(blob, net->fp8, {emb_w}, {E}, kPlanes + d.P, d.Kin));
   net->emb_b = AddF32(blob, {emb_b}, {E});
   net->emb_ln_g = AddF32(blob, {ln_g}, {E});
   net->emb_ln_b = AddF32(blob, {ln_b}, {E});
@@ -378,9 +452,9 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     const float *b = need("body.ip_emb_ffn_ln_betas", E);
     if (!ld.error.empty())
       return SetError(MFH_ERR_INVALID, ld.error);
-    net->in_ffn1_w = AddBf16(blob, {w1}, {d.Fi}, E, E);
+    SetW(net->in_ffn1_w, AddGemmW(blob, net->fp8, {w1}, {d.Fi}, E, E));
     net->in_ffn1_b = AddF32(blob, {b1}, {d.Fi});
-    net->in_ffn2_w = AddBf16(blob, {w2}, {E}, d.Fi, d.Fi);
+    SetW(net->in_ffn2_w, AddGemmW(blob, net->fp8, {w2}, {E}, d.Fi, d.Fi));
     net->in_ffn2_b = AddF32(blob, {b2}, {E});
     net->in_ln_g = AddF32(blob, {g}, {E});
     net->in_ln_b = AddF32(blob, {b}, {E});
@@ -389,7 +463,7 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     const float *g = need("body.smolgen_w", static_cast<size_t>(S) * S * d.G);
     if (!g)
       return SetError(MFH_ERR_INVALID, ld.error);
-    net->global_w = AddBf16(blob, {g}, {S * S}, d.G, d.G);
+    SetW(net->global_w, AddGemmW(blob, net->fp8, {g}, {S * S}, d.G, d.G));
   }
   net->layers.resize(d.L);
   for (int i = 0; i < d.L; ++i) {
@@ -411,15 +485,15 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       cw = need(p + ".mha.smolgen.compress", static_cast<size_t>(d.C) * E);
     if (!ld.error.empty())
       return SetError(MFH_ERR_INVALID, ld.error);
-    L.qkv_w = AddBf16(blob, {qw, kw, vw, cw}, {E, E, E, d.smolgen ? d.C : 0}, E, E);
+    SetW(L.qkv_w, AddGemmW(blob, net->fp8, {qw, kw, vw, cw}, {E, E, E, d.smolgen ? d.C : 0}, E, E));
     L.qkv_b = AddF32(blob, {qb, kb, vb, nullptr}, {E, E, E, d.smolgen ? d.C : 0});
-    L.out_w = AddBf16(blob, {ow}, {E}, E, E);
+    SetW(L.out_w, AddGemmW(blob, net->fp8, {ow}, {E}, E, E));
     L.out_b = AddF32(blob, {ob}, {E});
     L.ln1_g = AddF32(blob, {l1g}, {E});
     L.ln1_b = AddF32(blob, {l1b}, {E});
-    L.ffn1_w = AddBf16(blob, {f1w}, {d.F}, E, E);
+    SetW(L.ffn1_w, AddGemmW(blob, net->fp8, {f1w}, {d.F}, E, E));
     L.ffn1_b = AddF32(blob, {f1b}, {d.F});
-    L.ffn2_w = AddBf16(blob, {f2w}, {E}, d.F, d.F);
+    SetW(L.ffn2_w, AddGemmW(blob, net->fp8, {f2w}, {E}, d.F, d.F));
     L.ffn2_b = AddF32(blob, {f2b}, {E});
     L.ln2_g = AddF32(blob, {l2g}, {E});
     L.ln2_b = AddF32(blob, {l2b}, {E});
@@ -434,11 +508,11 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       const float *g2 = need(s + ".ln2_gammas", d.HG), *b2 = need(s + ".ln2_betas", d.HG);
       if (!ld.error.empty())
         return SetError(MFH_ERR_INVALID, ld.error);
-      L.sg_d1_w = AddBf16(blob, {d1w}, {d.Hs}, S * d.C, S * d.C);
+      SetW(L.sg_d1_w, AddGemmW(blob, net->fp8, {d1w}, {d.Hs}, S * d.C, S * d.C));
       L.sg_d1_b = AddF32(blob, {d1b}, {d.Hs});
       L.sg_ln1_g = AddF32(blob, {g1}, {d.Hs});
       L.sg_ln1_b = AddF32(blob, {b1}, {d.Hs});
-      L.sg_d2_w = AddBf16(blob, {d2w}, {d.HG}, d.Hs, d.Hs);
+      SetW(L.sg_d2_w, AddGemmW(blob, net->fp8, {d2w}, {d.HG}, d.Hs, d.Hs));
       L.sg_d2_b = AddF32(blob, {d2b}, {d.HG});
       L.sg_ln2_g = AddF32(blob, {g2}, {d.HG});
       L.sg_ln2_b = AddF32(blob, {b2}, {d.HG});
@@ -460,12 +534,12 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   const float *v2b = need(vp + "ip2_val_b", d.Vout);
   if (!ld.error.empty())
     return SetError(MFH_ERR_INVALID, ld.error);
-  net->head_w = AddBf16(blob, {pw, vw}, {d.Dp, d.Vd}, E, E);
+  SetW(net->head_w, AddGemmW(blob, net->fp8, {pw, vw}, {d.Dp, d.Vd}, E, E));
   net->head_b = AddF32(blob, {pb, vb}, {d.Dp, d.Vd});
-  net->qk_w = AddBf16(blob, {q2w, k3w}, {d.Dp, d.Dp}, d.Dp, d.Dp);
+  SetW(net->qk_w, AddGemmW(blob, net->fp8, {q2w, k3w}, {d.Dp, d.Dp}, d.Dp, d.Dp));
   net->qk_b = AddF32(blob, {q2b, k3b}, {d.Dp, d.Dp});
   net->promo = AddF32(blob, {p4}, {4 * d.Dp});
-  net->val1_w = AddBf16(blob, {v1w}, {d.Vh}, S * d.Vd, S * d.Vd);
+  SetW(net->val1_w, AddGemmW(blob, net->fp8, {v1w}, {d.Vh}, S * d.Vd, S * d.Vd));
   net->val1_b = AddF32(blob, {v1b}, {d.Vh});
   net->val2_w = AddF32(blob, {v2w}, {d.Vout * d.Vh});
   net->val2_b = AddF32(blob, {v2b}, {d.Vout});
@@ -618,13 +692,18 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       return fail(e_);                                                         \
   } while (0)
   // GEMM with A from workspace tensor `a` (its residual plane when split).
-  auto gemm = [&](const std::string &a, int lda, size_t w_off, int ldw, int m, int n, int k,
-                  const float *bias, int act, int mode, void *C, void *C_lo, int ldc) {
+  auto gemm = [&](const std::string &a, int lda, const size_t (&w)[2], int ldw, int m, int n,
+                  int k, const float *bias, int act, int mode, void *C, void *C_lo, int ldc) {
     mfh::GemmParams p;
     p.A = net->S<std::uint16_t>(a);
     p.A_lo = net->Lo(a);
     p.lda = lda;
-    p.W = net->W<std::uint16_t>(w_off);
+    if (net->fp8) {
+      p.W8 = net->W<std::uint8_t>(w[0]);
+      p.wscale = net->W<float>(w[1]);
+    } else {
+      p.W = net->W<std::uint16_t>(w[0]);
+    }
     p.ldw = ldw;
     p.M = m;
     p.N = n;
@@ -643,7 +722,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   auto run = [&](const mfh::GemmParams &p, const char *role) {
     const double flops = 2.0 * p.M * p.N * p.K;
     const double out_bytes = p.out_mode == mfh::GEMM_OUT_BF16 ? 2.0 * plane_mult : 4.0;
-    const double bytes = 2.0 * p.M * p.K * (p.A_lo ? 2.0 : 1.0) + 2.0 * p.N * p.K +
+    const double bytes = 2.0 * p.M * p.K * (p.A_lo ? 2.0 : 1.0) + (p.W8 ? 1.0 : 2.0) * p.N * p.K +
                          out_bytes * p.M * p.N * p.k_splits +
                          (p.out_mode == mfh::GEMM_OUT_RESID_F32 ? 4.0 * p.M * p.N : 0.0);
     StageTimer t(net, st, GemmKind(p, role), flops, bytes);
@@ -708,8 +787,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;
     MFH_RUN(run_ln(lp));
   }
-  auto residual_gemm = [&](const std::string &a, int k, size_t w_off, const float *bias,
-                           const char *role) {
+  auto residual_gemm = [&](const std::string &a, int k, const size_t (&w_off)[2],
+                           const float *bias, const char *role) {
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
     p.resid = resid;
@@ -1018,6 +1097,7 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
   net->arch = arch;
   net->device_name = prop.name;
   Blob blob;
+  net->fp8 = desc->weights_dtype == MFH_WEIGHTS_FP8;
   rc = Pack(net.get(), ld, blob);
   if (rc != MFH_OK)
     return rc;
@@ -1285,6 +1365,15 @@ int mfh_debug_unpack_planes(int batch, const uint64_t *masks, const float *value
   (void)hipFree(dv);
   (void)hipFree(dp);
   return rc;
+}
+
+int mfh_debug_quantize_fp8(int rows, int cols, const float *w, uint8_t *codes, float *scale) {
+  if (rows <= 0 || cols <= 0 || !w || !codes || !scale)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_quantize_fp8: bad arguments");
+  for (int r = 0; r < rows; ++r)
+    QuantizeRowE4m3(w + static_cast<size_t>(r) * cols, cols, codes + static_cast<size_t>(r) * cols,
+                    scale + r);
+  return MFH_OK;
 }
 
 int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A, const uint16_t *W,

@@ -42,6 +42,10 @@ struct GemmParams {
   const std::uint16_t *A_lo = nullptr;
   int lda = 0;
   const std::uint16_t *W = nullptr;
+  // Alternatively e4m3 weight codes [N][ldw] with fp32 row scales (the
+  // accumulated row is multiplied by wscale[n]).
+  const std::uint8_t *W8 = nullptr;
+  const float *wscale = nullptr;
   int ldw = 0;
   int M = 0, N = 0, K = 0;
   const float *bias = nullptr;

@@ -151,15 +151,57 @@ def tensor_layout(spec: NetSpec):
     return out
 
 
-def make_weights(spec: NetSpec, seed: int = 0, quantize: bool = True):
+def e4m3_encode(x):
+    """OCP e4m3 codes of float32 ``x`` (round to nearest even, saturating at
+    +-448), the encoding the fp8 weight storage uses."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    sign = ((u >> 24) & 0x80).astype(np.uint8)
+    au = u & 0x7FFFFFFF
+    a = au.astype(np.uint32).view(np.float32)
+    sub = a < np.float32(0.015625)
+    code_sub = np.rint(a * np.float32(512.0)).astype(np.int64)
+    r = au + 0x7FFFF + ((au >> 20) & 1)
+    e = (r >> 23).astype(np.int64) - 127
+    m = ((r >> 20) & 7).astype(np.int64)
+    code_n = np.where((e > 8) | ((e == 8) & (m == 7)), 0x7E, ((e + 7) << 3) | m)
+    return (sign | np.where(sub, code_sub, code_n).astype(np.uint8)).astype(np.uint8)
+
+
+def e4m3_values():
+    """float32 value of each of the 256 e4m3 codes (NaN for 0x7F / 0xFF)."""
+    v = np.empty(256, np.float32)
+    for c in range(256):
+        e, m = (c >> 3) & 15, c & 7
+        mag = (1 + m / 8.0) * 2.0 ** (e - 7) if e else m * 2.0 ** -9
+        v[c] = np.nan if (c & 0x7F) == 0x7F else (-mag if c & 0x80 else mag)
+    return v
+
+
+def quantize_fp8_rows(w):
+    """Per-row e4m3 quantisation of a [rows, cols] matrix: (codes, scales,
+    dequantised fp32 values), scale = max|row| / 448."""
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(w.shape[0], -1)
+    mx = np.abs(w).max(axis=1)
+    scale = np.where(mx > 0, mx / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+    codes = e4m3_encode(w / scale[:, None])
+    deq = (e4m3_values()[codes] * scale[:, None]).astype(np.float32)
+    return codes, scale, deq
+
+
+def make_weights(spec: NetSpec, seed: int = 0, quantize: bool = True, fp8: bool = False):
     """Deterministic fp32 weights {name: ndarray}; GEMM matrices rounded to
-    bf16-representable values when ``quantize``."""
+    bf16-representable values when ``quantize``, or to their per-row e4m3
+    dequantised values when ``fp8`` (the values an fp8-weight net computes
+    with)."""
     L = lib()
     weights = {}
     for name, shape, kind, fan_in, bf16 in tensor_layout(spec):
         arr = np.empty(shape, dtype=np.float32)
         L.mfs_fill_tensor(seed, name.encode(), kind, float(fan_in), arr.ctypes.data, arr.size)
-        if bf16 and quantize:
+        if bf16 and fp8:
+            arr = quantize_fp8_rows(arr.reshape(shape[0], -1))[2].reshape(shape)
+        elif bf16 and quantize:
             L.mfs_round_bf16(arr.ctypes.data, arr.size)
         weights[name] = arr
     return weights
