@@ -21,6 +21,8 @@ Prints one JSON line.  Besides the contract fields it carries:
   encoder_layer  -- config 4: one encoder layer's time and MFMA utilisation at
                     batches 256 and 1024 (bf16 activations);
   precisions     -- batch-256 throughput of the other activation precisions;
+  fp8_weights    -- config 5: e4m3 weights with per-row scales at batch 1024,
+                    and batch-1 latency with the halved weight bytes;
   mfma_util_pct  -- executed MFMA work of the GEMMs against the dense bf16
                     peak (twice the algorithmic work in the split precisions).
 """
@@ -57,6 +59,7 @@ def parse_args():
     ap.add_argument("--latency-iters", type=int, default=200)
     ap.add_argument("--small-batches", default="1,8,32,64")
     ap.add_argument("--layer-batches", default="256,1024")
+    ap.add_argument("--fp8-batch", type=int, default=1024)
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline, roofline and batch-1 latency")
     ap.add_argument("--cpu-positions", type=int, default=16,
@@ -117,10 +120,10 @@ class Runner:
     """One net plus device-resident inputs/outputs for up to max_batch."""
 
     def __init__(self, backend, torch, np, spec, weights, masks, values, max_batch, precision,
-                 stream):
+                 stream, weights_dtype="bf16"):
         self.torch = torch
         self.net = backend.create_network(spec, weights, max_batch=max_batch, device=0,
-                                          precision=precision)
+                                          precision=precision, weights_dtype=weights_dtype)
         reps = (max_batch + masks.shape[0] - 1) // masks.shape[0]
         m = np.tile(masks, (reps, 1))[:max_batch]
         v = np.tile(values, (reps, 1))[:max_batch]
@@ -320,6 +323,28 @@ def main():
                                 "ms_per_step": round(ms, 4)}
             r.close()
 
+    # Config 5: fp8 e4m3 weights (per-row scales) at batch 1024, bf16x2
+    # activations; plus the weight-streaming batch-1 latency with the halved
+    # weight bytes.
+    fp8 = {}
+    if not args.no_extras:
+        fb = args.fp8_batch
+        fweights = synth.make_weights(spec, seed=args.seed, fp8=True)
+        backend_fp8 = Runner(backend, torch, np, spec, fweights, masks, values, fb, "bf16x2",
+                             stream, weights_dtype="fp8")
+        ms = backend_fp8.time_steps(fb, max(3, args.steps // 4), 2)
+        wb = backend_fp8.net.capabilities()["weight_bytes"]
+        lat = np.array(backend_fp8.latencies(1, max(50, args.latency_iters // 2)))
+        p50 = float(np.percentile(lat, 50))
+        fp8 = {"batch": fb, "positions_per_s": round(fb / (ms * 1e-3), 1),
+               "ms_per_step": round(ms, 4), "weight_bytes": int(wb),
+               "whole_forward_tflops": round(GFLOP_PER_POSITION * fb / ms, 1),
+               "mfma_frac_of_bf16_peak": round(GFLOP_PER_POSITION * fb / ms / PEAK_BF16_TFLOPS, 4),
+               "batch1_p50_ms": round(p50, 4),
+               "batch1_weight_stream_gbs": round(wb / (p50 * 1e-3) / 1e9, 1),
+               "mma": "bf16 MFMA on exactly converted e4m3 weights (bf16x2 activations)"}
+        backend_fp8.close()
+
     cpu = None
     if args.cpu_positions > 0:
         cpu = cpu_baseline(spec, weights, planes, args.cpu_positions, args.cpu_threads)
@@ -367,6 +392,7 @@ def main():
         "small_batch": small,
         "encoder_layer": layer,
         "precisions": precisions,
+        "fp8_weights": fp8,
         "kernel_breakdown": breakdown,
         "gemm_roles": gemm_roles,
         "cpu_baseline": cpu,
