@@ -65,37 +65,84 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   const int qcol = h * kDepth, kcol = E + h * kDepth, vcol = 2 * E + h * kDepth;
   const int fr = lane & 15, g = lane >> 4;
 
-  // V^T into LDS.  Lane l handles the key pair 2 (l % 32), 2 (l % 32) + 1
-  // and depths 16 (l / 32) .. + 16, writing one packed dword per depth.
-  {
-    const int kp = lane & 31, dh = (lane >> 5) * 16;
+  // All of the head's global loads go out before any is used, so their
+  // latencies overlap: V rows (for V^T), Q and K fragments, and the bias of
+  // the first query tile (the bias of tile q + 1 is fetched while tile q is
+  // processed).  Lane l's V rows: the key pair 2 (l % 32), 2 (l % 32) + 1,
+  // depths 16 (l / 32) .. + 16.
+  const int kp = lane & 31, dh = (lane >> 5) * 16;
+  u32x4 vrow[PLANES][4];
 #pragma unroll
-    for (int pl = 0; pl < PLANES; ++pl) {
-      const std::uint16_t *base = (pl ? ap.qkv_lo : ap.qkv) + pos + vcol + dh;
-      const u32x4 *r0 = reinterpret_cast<const u32x4 *>(base + (2 * kp) * ld);
-      const u32x4 *r1 = reinterpret_cast<const u32x4 *>(base + (2 * kp + 1) * ld);
-      const u32x4 a0 = r0[0], a1 = r0[1], c0 = r1[0], c1 = r1[1];
-      std::uint32_t *vt = reinterpret_cast<std::uint32_t *>(vt_lds[wave][pl]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const std::uint32_t x = (e < 8 ? a0 : a1)[(e & 7) >> 1];
-        const std::uint32_t y = (e < 8 ? c0 : c1)[(e & 7) >> 1];
-        const std::uint32_t lo = (e & 1) ? (x >> 16) : (x & 0xFFFFu);
-        const std::uint32_t hi = (e & 1) ? (y >> 16) : (y & 0xFFFFu);
-        vt[((dh + e) * kVtStride) / 2 + kp] = lo | (hi << 16);
-      }
-    }
+  for (int pl = 0; pl < PLANES; ++pl) {
+    const std::uint16_t *base = (pl ? ap.qkv_lo : ap.qkv) + pos + vcol + dh;
+    const u32x4 *r0 = reinterpret_cast<const u32x4 *>(base + (2 * kp) * ld);
+    const u32x4 *r1 = reinterpret_cast<const u32x4 *>(base + (2 * kp + 1) * ld);
+    vrow[pl][0] = r0[0];
+    vrow[pl][1] = r0[1];
+    vrow[pl][2] = r1[0];
+    vrow[pl][3] = r1[1];
   }
-
-  // S^T = K Q^T: tile (t, s) holds keys 16 t + 4 g + r (rows) for queries
-  // 16 s + fr (columns).
+  // S^T = K Q^T operands: tile (t, s) holds keys 16 t + 4 g + r (rows) for
+  // queries 16 s + fr (columns).
   const std::uint16_t *qh = ap.qkv + pos;
-  bf16x8 kf[4], qf[4];
+  bf16x8 kf[4], qf[4], kl[4], qlo[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     kf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + kcol + g * 8);
     qf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + qcol + g * 8);
   }
+  if constexpr (SPLIT) {
+    const std::uint16_t *ql = ap.qkv_lo + pos;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kl[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + kcol + g * 8);
+      qlo[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + qcol + g * 8);
+    }
+  }
+  const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
+  // Bias of query tile q for the lane's keys 16 t + 4 g .. + 3, t = 0..3.
+  auto load_bias = [&](int q, float (&bb)[4][4]) {
+    const int query = q * 16 + fr;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int key0 = t * 16 + g * 4;
+      if (!ap.bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bb[t][r] = 0.f;
+      } else if constexpr (BIAS_F32) {
+        const f32x4 x = *reinterpret_cast<const f32x4 *>(
+            static_cast<const float *>(ap.bias) + bias_off + query * kSq + key0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bb[t][r] = x[r];
+      } else {
+        const u32x2 x = *reinterpret_cast<const u32x2 *>(
+            static_cast<const std::uint16_t *>(ap.bias) + bias_off + query * kSq + key0);
+        bb[t][0] = __uint_as_float(x[0] << 16);
+        bb[t][1] = __uint_as_float(x[0] & 0xFFFF0000u);
+        bb[t][2] = __uint_as_float(x[1] << 16);
+        bb[t][3] = __uint_as_float(x[1] & 0xFFFF0000u);
+      }
+    }
+  };
+  float bcur[4][4], bnext[4][4];
+  load_bias(0, bcur);
+
+  // V^T into LDS, one packed dword (two keys) per depth.
+#pragma unroll
+  for (int pl = 0; pl < PLANES; ++pl) {
+    std::uint32_t *vt = reinterpret_cast<std::uint32_t *>(vt_lds[wave][pl]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const std::uint32_t x = vrow[pl][e < 8 ? 0 : 1][(e & 7) >> 1];
+      const std::uint32_t y = vrow[pl][e < 8 ? 2 : 3][(e & 7) >> 1];
+      const std::uint32_t lo = (e & 1) ? (x >> 16) : (x & 0xFFFFu);
+      const std::uint32_t hi = (e & 1) ? (y >> 16) : (y & 0xFFFFu);
+      vt[((dh + e) * kVtStride) / 2 + kp] = lo | (hi << 16);
+    }
+  }
+
   f32x4 s[4][4];  // [t][s]
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -103,13 +150,6 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     for (int q = 0; q < 4; ++q)
       s[t][q] = Mfma(kf[t], qf[q], f32x4{0.f, 0.f, 0.f, 0.f});
   if constexpr (SPLIT) {
-    const std::uint16_t *ql = ap.qkv_lo + pos;
-    bf16x8 kl[4], qlo[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kl[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + kcol + g * 8);
-      qlo[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + qcol + g * 8);
-    }
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -120,36 +160,22 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   // Scale, bias, softmax over the 64 keys of each query 16 q + fr; the lane
   // holds 16 of them, lanes fr, fr + 16, fr + 32, fr + 48 hold the rest.
   const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
-  const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
   bf16x8 pf[4][2], pl[4][2];  // [query tile][key-tile pair]: B operands of ctx^T
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int query = q * 16 + fr;
+    if (q + 1 < 4)
+      load_bias(q + 1, bnext);
     float v[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int key0 = t * 16 + g * 4;
-      float bb[4] = {0.f, 0.f, 0.f, 0.f};
-      if (ap.bias) {
-        if constexpr (BIAS_F32) {
-          const f32x4 x = *reinterpret_cast<const f32x4 *>(
-              static_cast<const float *>(ap.bias) + bias_off + query * kSq + key0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            bb[r] = x[r];
-        } else {
-          const u32x2 x = *reinterpret_cast<const u32x2 *>(
-              static_cast<const std::uint16_t *>(ap.bias) + bias_off + query * kSq + key0);
-          bb[0] = __uint_as_float(x[0] << 16);
-          bb[1] = __uint_as_float(x[0] & 0xFFFF0000u);
-          bb[2] = __uint_as_float(x[1] << 16);
-          bb[3] = __uint_as_float(x[1] & 0xFFFF0000u);
-        }
-      }
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        v[t][r] = s[t][q][r] * scale + bb[r];
-    }
+        v[t][r] = s[t][q][r] * scale + bcur[t][r];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        bcur[t][r] = bnext[t][r];
     float m = v[0][0];
 #pragma unroll
     for (int t = 0; t < 4; ++t)

@@ -136,6 +136,17 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
     }
     v[i] = x;
   }
+  // gamma / beta are independent of the statistics: fetch them before the
+  // reductions so their latency overlaps.
+  f32x4 gm[NV], bt[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = 4 * (i * T + t);
+    if (c < width) {
+      gm[i] = *reinterpret_cast<const f32x4 *>(lp.gamma + c);
+      bt[i] = *reinterpret_cast<const f32x4 *>(lp.beta + c);
+    }
+  }
   s = wave_sum(s);
   ss = wave_sum(ss);
   if (T == 256) {
@@ -159,12 +170,10 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
     const int c = 4 * (i * T + t);
     if (c >= width)
       break;
-    const f32x4 gm = *reinterpret_cast<const f32x4 *>(lp.gamma + c);
-    const f32x4 bt = *reinterpret_cast<const f32x4 *>(lp.beta + c);
     f32x4 y;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      y[e] = (v[i][e] - mean) * inv_std * gm[e] + bt[e];
+      y[e] = (v[i][e] - mean) * inv_std * gm[i][e] + bt[i][e];
       if (lp.mult_gate)
         y[e] = y[e] * lp.mult_gate[static_cast<size_t>(c + e) * kSquares + sq];
       if (lp.add_gate)
