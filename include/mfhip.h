@@ -187,6 +187,70 @@ int mfh_pack_planes(int batch, const float *planes, uint64_t *masks,
 int mfh_debug_quantize_fp8(int rows, int cols, const float *w, uint8_t *codes,
                            float *scale);
 
+/* ---- Network files (no device needed) ----------------------------------
+ *
+ * A reader for the reference's `.pb` / `.pb.gz` network files
+ * (reference src/nn/proto/net.proto) that needs no libprotobuf.  Loading
+ * applies the reference's legacy format fix-ups and layer decoding
+ * (LINEAR16 / FLOAT16 / BFLOAT16 / FLOAT32), folds convolution batch norms,
+ * resolves the selected policy and value heads ("vanilla", "winner") and
+ * yields the weight inventory: the tensors mfh_net_create takes, under the
+ * same names. */
+typedef struct mfh_weights mfh_weights;
+
+/* NetworkFormat fields after the fix-ups (values as in net.proto:253-343;
+ * input_embedding is PE_MAP when the file leaves it unset, as
+ * DescribeNetworkFormat reads it, reference src/nn/network_format.cpp:97-100)
+ * and the head counts. */
+typedef struct {
+  int input;
+  int output;
+  int network;
+  int policy;
+  int value;
+  int moves_left;
+  int default_activation;
+  int smolgen_activation;
+  int ffn_activation;
+  int input_embedding;
+  int headcount;     /* Weights.headcount */
+  int pol_headcount; /* pol_headcount of the selected policy head */
+} mfh_weights_format;
+
+/* LoadWeights (reference src/nn/loader.cpp:162-189: names ending in ".gz"
+ * are gzip-decompressed, the magic must be 0x1c0, FixOlderWeightsFile
+ * 86-135 is applied) followed by MultiHeadWeights (src/nn/weights.cpp:
+ * 216-291) and CreateNetworkWeightInventory for the selected heads
+ * (src/nn/network_weight_inventory.cpp:332-352).  Errors (MFH_ERR_INVALID)
+ * carry the reference's messages, e.g. "Invalid weight file: bad magic
+ * number", "RPE weights file not supported.". */
+int mfh_weights_load(const char *path, mfh_weights **out);
+
+/* The same on an in-memory serialised Net message (ParseWeightsProto,
+ * reference src/nn/loader.cpp:137-158; not gzip). */
+int mfh_weights_parse(const void *data, uint64_t bytes, mfh_weights **out);
+
+/* Format fields and head counts.  With desc non-NULL, also fills the format
+ * fields and headcount of a net description, as DescribeNetworkFormat reads
+ * them (reference src/nn/network_format.cpp:72-127), leaving weights_dtype,
+ * precision, max_batch and device as the caller set them.  Either pointer
+ * may be NULL. */
+int mfh_weights_describe(const mfh_weights *w, mfh_weights_format *format,
+                         mfh_net_desc *desc);
+
+/* The inventory (NetworkWeightInventory::tensors, reference
+ * src/nn/network_weight_inventory.h:33-56): names, fp32 data and element
+ * counts, in inventory order.  Valid until mfh_weights_free. */
+int mfh_weights_tensors(const mfh_weights *w, const mfh_tensor **tensors,
+                        int *count);
+
+/* Dims of tensor `index` (the layer's dims, or its flat size when the file
+ * gives none; NetworkWeightTensorView::dims). */
+int mfh_weights_tensor_dims(const mfh_weights *w, int index,
+                            const uint32_t **dims, int *ndims);
+
+void mfh_weights_free(mfh_weights *w);
+
 /* Number of visible devices (0 without a GPU). */
 int mfh_device_count(int *count);
 

@@ -1,6 +1,7 @@
 """Builds the native libraries of metalfish_amd in-tree.
 
-* ``libmfhip.so``  -- gfx950 kernels + the C ABI of include/mfhip.h (hipcc).
+* ``libmfhip.so``  -- gfx950 kernels + the C ABI of include/mfhip.h (hipcc),
+  with the host-only network-file reader (g++, zlib).
 * ``libmfhost.so`` -- seeded nets and chess positions, include/mfh_synth.h (g++).
 * ``libmfadapter.so`` / ``hip_network_test`` -- the C++ ``HipNetwork``
   adapter (NN::Network over the C ABI) and its self-test driver.
@@ -22,6 +23,8 @@ CSRC = os.path.join(PKG, "csrc")
 
 HIP_SOURCES = ["hip/gemm.hip", "hip/attention.hip", "hip/rowops.hip", "hip/policy.hip",
                "hip/mfh_api.cpp", "host/policy_tables.cpp"]
+# Host-only parts of libmfhip.so (no device code), compiled with g++.
+HIP_HOST_SOURCES = ["host/weights_file.cpp"]
 HOST_SOURCES = ["host/chess.cpp", "host/policy_tables.cpp", "host/synth_api.cpp"]
 
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -64,9 +67,17 @@ def build_hip(jobs=8):
         if len(procs) >= jobs:
             _wait(procs)
             procs = []
+    for src in HIP_HOST_SOURCES:
+        obj = os.path.join(objdir, src.replace("/", "_") + ".o")
+        objs.append(obj)
+        cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", "-Wextra", "-c",
+               os.path.join(CSRC, src), "-o", obj]
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                            stderr=subprocess.STDOUT, text=True)))
     _wait(procs)
     out = os.path.join(PKG, "libmfhip.so")
-    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", out + ".tmp"])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-lz", "-o",
+          out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 

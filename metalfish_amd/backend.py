@@ -31,7 +31,11 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_net_set_graphs", "mfh_net_set_profiling", "mfh_net_profile",
            "mfh_net_profile_reset",
            "mfh_pack_planes", "mfh_device_count", "mfh_last_error", "mfh_debug_unpack_planes",
-           "mfh_debug_gemm_bf16", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8")
+           "mfh_debug_gemm_bf16", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8",
+           "mfh_weights_load", "mfh_weights_parse", "mfh_weights_describe",
+           "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free")
+FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
+                 "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
 
 class MfhNetDesc(ctypes.Structure):
@@ -43,6 +47,10 @@ class MfhNetDesc(ctypes.Structure):
 
 class MfhTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("count", ctypes.c_uint64)]
+
+
+class MfhWeightsFormat(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in FORMAT_FIELDS + ("headcount", "pol_headcount")]
 
 
 class MfhProfileEntry(ctypes.Structure):
@@ -89,6 +97,15 @@ def lib():
             "mfh_debug_gemm_bf16": ([i, i, i, vp, vp, vp, i, vp], i),
             "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
             "mfh_debug_quantize_fp8": ([i, i, vp, vp, vp], i),
+            "mfh_weights_load": ([ctypes.c_char_p, ctypes.POINTER(vp)], i),
+            "mfh_weights_parse": ([vp, u64, ctypes.POINTER(vp)], i),
+            "mfh_weights_describe": ([vp, ctypes.POINTER(MfhWeightsFormat),
+                                      ctypes.POINTER(MfhNetDesc)], i),
+            "mfh_weights_tensors": ([vp, ctypes.POINTER(ctypes.POINTER(MfhTensor)),
+                                     ctypes.POINTER(i)], i),
+            "mfh_weights_tensor_dims": ([vp, i, ctypes.POINTER(ctypes.POINTER(ctypes.c_uint32)),
+                                         ctypes.POINTER(i)], i),
+            "mfh_weights_free": ([vp], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -119,7 +136,10 @@ class HipNetwork:
 
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
-                 device=-1, precision="bf16x2", weights_dtype="bf16"):
+                 device=-1, precision="bf16x2", weights_dtype="bf16", net_format=None):
+        """``net_format``: NetworkFormat fields of a loaded file
+        (``WeightsFile.format``); they replace the description the keyword
+        arguments give."""
         self._weights = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
                          for k, v in weights.items()}
         names = list(self._weights)
@@ -135,6 +155,11 @@ class HipNetwork:
                           smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
                           weights_dtype=WEIGHTS[weights_dtype], precision=PRECISION[precision],
                           max_batch=max_batch, device=device)
+        if net_format is not None:
+            for k in ("network", "policy", "value", "moves_left", "input_embedding",
+                      "default_activation", "ffn_activation", "smolgen_activation"):
+                setattr(desc, k, int(net_format[k]))
+            wdl = net_format["value"] == 2
         handle = ctypes.c_void_p()
         self._h = None
         _check(lib().mfh_net_create(ctypes.byref(desc), tensors, len(names),
@@ -300,3 +325,62 @@ def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,
                       device=device, precision=precision, weights_dtype=weights_dtype)
+
+
+class WeightsFile:
+    """A decoded network file: the NetworkFormat after the reference's legacy
+    fix-ups (``format``), head counts and the weight inventory of the
+    selected heads (``tensors`` {name: fp32 array}, ``dims``) -- LoadWeights,
+    MultiHeadWeights and CreateNetworkWeightInventory of the reference
+    (src/nn/loader.cpp:162-189, src/nn/weights.cpp:216-291,
+    src/nn/network_weight_inventory.cpp:332-352)."""
+
+    def __init__(self, handle):
+        L = lib()
+        try:
+            fmt = MfhWeightsFormat()
+            _check(L.mfh_weights_describe(handle, ctypes.byref(fmt), None),
+                   "mfh_weights_describe")
+            self.format = {k: getattr(fmt, k) for k in FORMAT_FIELDS}
+            self.headcount = fmt.headcount
+            self.pol_headcount = fmt.pol_headcount
+            views = ctypes.POINTER(MfhTensor)()
+            n = ctypes.c_int(0)
+            _check(L.mfh_weights_tensors(handle, ctypes.byref(views), ctypes.byref(n)),
+                   "mfh_weights_tensors")
+            self.tensors, self.dims = {}, {}
+            for j in range(n.value):
+                t = views[j]
+                name = t.name.decode()
+                buf = (ctypes.c_float * t.count).from_address(t.data)
+                self.tensors[name] = np.frombuffer(buf, dtype=np.float32).copy()
+                d = ctypes.POINTER(ctypes.c_uint32)()
+                nd = ctypes.c_int(0)
+                _check(L.mfh_weights_tensor_dims(handle, j, ctypes.byref(d), ctypes.byref(nd)),
+                       "mfh_weights_tensor_dims")
+                self.dims[name] = [d[k] for k in range(nd.value)]
+        finally:
+            L.mfh_weights_free(handle)
+
+    def create_network(self, max_batch=256, device=-1, precision="bf16x2",
+                       weights_dtype="bf16"):
+        """HipNetwork for this file (CreateNetwork(const WeightsFile&, ...),
+        reference src/nn/network.cpp:137-208)."""
+        return HipNetwork(self.tensors, self.headcount, max_batch=max_batch, device=device,
+                          precision=precision, weights_dtype=weights_dtype,
+                          net_format=self.format)
+
+
+def load_weights(path) -> WeightsFile:
+    """Reads a ``.pb`` / ``.pb.gz`` network file (no device needed)."""
+    h = ctypes.c_void_p()
+    _check(lib().mfh_weights_load(os.fsencode(path), ctypes.byref(h)), "mfh_weights_load")
+    return WeightsFile(h)
+
+
+def parse_weights(data: bytes) -> WeightsFile:
+    """Decodes a serialised Net message held in memory."""
+    h = ctypes.c_void_p()
+    buf = ctypes.create_string_buffer(bytes(data), len(data))
+    _check(lib().mfh_weights_parse(buf, len(data), ctypes.byref(h)), "mfh_weights_parse")
+    return WeightsFile(h)

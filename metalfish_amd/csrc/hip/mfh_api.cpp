@@ -21,6 +21,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <new>
 #include <set>
 #include <sstream>
 #include <string>
@@ -28,6 +29,7 @@
 #include <vector>
 
 #include "../host/policy_tables.h"
+#include "../host/weights_file.h"
 #include "mfh_kernels.h"
 
 namespace {
@@ -155,6 +157,12 @@ struct Dims {
 };
 
 }  // namespace
+
+// A decoded network file and the C views of its tensors.
+struct mfh_weights {
+  mfh::wf::Weights w;
+  std::vector<mfh_tensor> views;
+};
 
 struct mfh_net {
   std::mutex mu;
@@ -1375,6 +1383,98 @@ int mfh_debug_quantize_fp8(int rows, int cols, const float *w, uint8_t *codes, f
                     scale + r);
   return MFH_OK;
 }
+
+// ---- Network files ----------------------------------------------------------
+
+static int WrapWeights(mfh::wf::Weights &&w, mfh_weights **out) {
+  auto *h = new (std::nothrow) mfh_weights;
+  if (!h)
+    return SetError(MFH_ERR_OUT_OF_MEMORY, "out of host memory");
+  h->w = std::move(w);
+  h->views.reserve(h->w.tensors.size());
+  for (const auto &t : h->w.tensors)
+    h->views.push_back(mfh_tensor{t.name.c_str(), t.data.data(), t.data.size()});
+  *out = h;
+  return MFH_OK;
+}
+
+int mfh_weights_load(const char *path, mfh_weights **out) {
+  if (!path || !out)
+    return SetError(MFH_ERR_INVALID, "mfh_weights_load: bad arguments");
+  *out = nullptr;
+  try {
+    return WrapWeights(mfh::wf::LoadFile(path), out);
+  } catch (const std::bad_alloc &) {
+    return SetError(MFH_ERR_OUT_OF_MEMORY, "out of host memory reading " + std::string(path));
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_INVALID, e.what());
+  }
+}
+
+int mfh_weights_parse(const void *data, uint64_t bytes, mfh_weights **out) {
+  if ((!data && bytes) || !out)
+    return SetError(MFH_ERR_INVALID, "mfh_weights_parse: bad arguments");
+  *out = nullptr;
+  try {
+    if (bytes < 2)
+      throw std::runtime_error("Invalid weight file: too small");
+    return WrapWeights(mfh::wf::Parse(static_cast<const uint8_t *>(data), bytes), out);
+  } catch (const std::bad_alloc &) {
+    return SetError(MFH_ERR_OUT_OF_MEMORY, "out of host memory");
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_INVALID, e.what());
+  }
+}
+
+int mfh_weights_describe(const mfh_weights *w, mfh_weights_format *format, mfh_net_desc *desc) {
+  if (!w)
+    return SetError(MFH_ERR_INVALID, "mfh_weights_describe: null weights");
+  const auto &f = w->w.format;
+  if (format) {
+    format->input = f.input;
+    format->output = f.output;
+    format->network = f.network;
+    format->policy = f.policy;
+    format->value = f.value;
+    format->moves_left = f.moves_left;
+    format->default_activation = f.default_activation;
+    format->smolgen_activation = f.smolgen_activation;
+    format->ffn_activation = f.ffn_activation;
+    format->input_embedding = f.input_embedding;
+    format->headcount = static_cast<int>(w->w.headcount);
+    format->pol_headcount = static_cast<int>(w->w.pol_headcount);
+  }
+  if (desc) {
+    desc->network = f.network;
+    desc->policy = f.policy;
+    desc->value = f.value;
+    desc->moves_left = f.moves_left;
+    desc->input_embedding = f.input_embedding;
+    desc->default_activation = f.default_activation;
+    desc->ffn_activation = f.ffn_activation;
+    desc->smolgen_activation = f.smolgen_activation;
+    desc->headcount = static_cast<int>(w->w.headcount);
+  }
+  return MFH_OK;
+}
+
+int mfh_weights_tensors(const mfh_weights *w, const mfh_tensor **tensors, int *count) {
+  if (!w || !tensors || !count)
+    return SetError(MFH_ERR_INVALID, "mfh_weights_tensors: bad arguments");
+  *tensors = w->views.data();
+  *count = static_cast<int>(w->views.size());
+  return MFH_OK;
+}
+
+int mfh_weights_tensor_dims(const mfh_weights *w, int index, const uint32_t **dims, int *ndims) {
+  if (!w || !dims || !ndims || index < 0 || index >= static_cast<int>(w->w.tensors.size()))
+    return SetError(MFH_ERR_INVALID, "mfh_weights_tensor_dims: bad arguments");
+  *dims = w->w.tensors[index].dims.data();
+  *ndims = static_cast<int>(w->w.tensors[index].dims.size());
+  return MFH_OK;
+}
+
+void mfh_weights_free(mfh_weights *w) { delete w; }
 
 int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A, const uint16_t *W,
                         const float *bias, int act, float *C) {

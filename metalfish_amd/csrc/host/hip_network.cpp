@@ -33,14 +33,7 @@ bool OutputsValid(const float *policy, const float *value, int count, bool wdl) 
   return true;
 }
 
-}  // namespace
-
-HipNetwork::HipNetwork(const std::vector<WeightTensor> &weights,
-                       const HipNetworkConfig &config) {
-  std::vector<mfh_tensor> tensors;
-  tensors.reserve(weights.size());
-  for (const auto &w : weights)
-    tensors.push_back(mfh_tensor{w.name.c_str(), w.data, static_cast<std::uint64_t>(w.elements)});
+mfh_net_desc DescFromConfig(const HipNetworkConfig &config) {
   mfh_net_desc desc{};
   desc.network = config.network;
   desc.policy = config.policy;
@@ -55,11 +48,52 @@ HipNetwork::HipNetwork(const std::vector<WeightTensor> &weights,
   desc.precision = config.precision;
   desc.max_batch = config.max_batch;
   desc.device = config.device;
-  const int rc = mfh_net_create(&desc, tensors.data(), static_cast<int>(tensors.size()), &net_);
+  return desc;
+}
+
+}  // namespace
+
+HipNetwork::HipNetwork(const std::vector<WeightTensor> &weights,
+                       const HipNetworkConfig &config) {
+  std::vector<mfh_tensor> tensors;
+  tensors.reserve(weights.size());
+  for (const auto &w : weights)
+    tensors.push_back(mfh_tensor{w.name.c_str(), w.data, static_cast<std::uint64_t>(w.elements)});
+  Create(DescFromConfig(config), tensors.data(), static_cast<int>(tensors.size()));
+}
+
+HipNetwork::HipNetwork(const std::string &weights_path, const HipNetworkConfig &config) {
+  mfh_weights *file = nullptr;
+  int rc = mfh_weights_load(weights_path.c_str(), &file);
+  if (rc != MFH_OK)
+    throw std::runtime_error(LastError("weights load", rc));
+  mfh_net_desc desc = DescFromConfig(config);
+  const mfh_tensor *tensors = nullptr;
+  int count = 0;
+  rc = mfh_weights_describe(file, nullptr, &desc);
+  if (rc == MFH_OK)
+    rc = mfh_weights_tensors(file, &tensors, &count);
+  if (rc != MFH_OK) {
+    const std::string msg = LastError("weights load", rc);
+    mfh_weights_free(file);
+    throw std::runtime_error(msg);
+  }
+  try {
+    Create(desc, tensors, count);
+  } catch (...) {
+    mfh_weights_free(file);
+    throw;
+  }
+  // The device holds its own copy of the weights now.
+  mfh_weights_free(file);
+}
+
+void HipNetwork::Create(mfh_net_desc desc, const mfh_tensor *tensors, int count) {
+  const int rc = mfh_net_create(&desc, tensors, count, &net_);
   if (rc != MFH_OK)
     throw std::runtime_error(LastError("initialisation", rc));
-  wdl_ = config.value == MFH_VALUE_WDL;
-  max_batch_ = config.max_batch;
+  wdl_ = desc.value == MFH_VALUE_WDL;
+  max_batch_ = desc.max_batch;
   policy_.resize(static_cast<std::size_t>(max_batch_) * kPolicyOutputs);
   value_.resize(static_cast<std::size_t>(max_batch_) * 3);
 }

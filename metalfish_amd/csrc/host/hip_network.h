@@ -47,6 +47,11 @@ struct HipNetworkConfig {
 class HipNetwork : public Network {
 public:
   HipNetwork(const std::vector<WeightTensor> &weights, const HipNetworkConfig &config);
+  // From a `.pb` / `.pb.gz` network file, as CreateNetwork(weights_path, ...)
+  // loads one first (reference src/nn/network.cpp:226-258): the file's
+  // format fields and head count replace those of `config`; precision,
+  // max_batch and device are taken from `config`.
+  HipNetwork(const std::string &weights_path, const HipNetworkConfig &config);
   ~HipNetwork() override;
   HipNetwork(const HipNetwork &) = delete;
   HipNetwork &operator=(const HipNetwork &) = delete;
@@ -59,6 +64,7 @@ public:
   BackendCapabilities GetBackendCapabilities() const override;
 
 private:
+  void Create(mfh_net_desc desc, const mfh_tensor *tensors, int count);
   void RunChunk(const InputPlanes *inputs, int count, NetworkOutput *outputs);
 
   mfh_net *net_ = nullptr;

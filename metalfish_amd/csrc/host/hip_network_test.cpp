@@ -3,7 +3,8 @@
 // Evaluate, and writes the NetworkOutput fields for comparison.
 //
 // Usage: hip_network_test NET PLANES OUT HEADS PRECISION MAX_BATCH
-//   NET    : u32 count, then per tensor u32 name_len, name, u64 n, n floats
+//   NET    : u32 count, then per tensor u32 name_len, name, u64 n, n floats;
+//            or a network file ending in ".pb" / ".pb.gz" (HEADS unused)
 //   PLANES : u32 batch, then batch*112*64 floats
 //   OUT    : batch*(1858+3+1) floats from EvaluateBatch, then the same for
 //            Evaluate of each position
@@ -13,6 +14,7 @@
 #include <cstring>
 #include <cstdlib>
 #include <exception>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -48,15 +50,23 @@ int main(int argc, char **argv) {
     std::fprintf(stderr, "usage: %s NET PLANES OUT HEADS PRECISION MAX_BATCH\n", argv[0]);
     return 2;
   }
+  const std::string net_path = argv[1];
+  auto ends_with = [&](const char *suffix) {
+    const std::size_t n = std::strlen(suffix);
+    return net_path.size() >= n && net_path.compare(net_path.size() - n, n, suffix) == 0;
+  };
+  const bool net_file = ends_with(".pb") || ends_with(".pb.gz");
   std::vector<char> net_bytes, plane_bytes;
-  if (!ReadAll(argv[1], net_bytes) || !ReadAll(argv[2], plane_bytes))
+  if ((!net_file && !ReadAll(argv[1], net_bytes)) || !ReadAll(argv[2], plane_bytes))
     return 2;
   std::vector<Hip::WeightTensor> weights;
   std::vector<std::string> names;
   std::size_t off = 0;
   std::uint32_t count = 0;
-  std::memcpy(&count, net_bytes.data(), 4);
-  off = 4;
+  if (!net_file) {
+    std::memcpy(&count, net_bytes.data(), 4);
+    off = 4;
+  }
   names.reserve(count);
   for (std::uint32_t i = 0; i < count; ++i) {
     std::uint32_t len = 0;
@@ -82,7 +92,10 @@ int main(int argc, char **argv) {
     config.headcount = std::atoi(argv[4]);
     config.precision = std::string(argv[5]) == "bf16" ? MFH_PRECISION_BF16 : MFH_PRECISION_BF16X2;
     config.max_batch = std::atoi(argv[6]);
-    Hip::HipNetwork net(weights, config);
+    std::unique_ptr<Hip::HipNetwork> owner =
+        net_file ? std::make_unique<Hip::HipNetwork>(net_path, config)
+                 : std::make_unique<Hip::HipNetwork>(weights, config);
+    Hip::HipNetwork &net = *owner;
     std::fprintf(stderr, "%s\n", net.GetNetworkInfo().c_str());
     const BackendCapabilities caps = net.GetBackendCapabilities();
     if (caps.actual_backend != "hip" || !caps.has_wdl || caps.max_batch_size != config.max_batch)

@@ -15,6 +15,7 @@ is reported rather than gated.
 import numpy as np
 import pytest
 
+import netfile
 import oracle
 from metalfish_amd import backend, synth
 
@@ -216,6 +217,29 @@ def test_graph_replay_matches_eager():
         other = net.evaluate_batch(planes[:3])  # a different batch size in between
         assert other["policy"].shape == (3, 1858)
     net.close()
+
+
+def test_bt4_net_from_network_file(tmp_path):
+    """A BT4-shape net written as a .pb network file and read back through
+    mfh_weights_load gives the same device results, bit for bit, as the net
+    built from the tensors."""
+    spec = synth.SPECS["bt4"]
+    weights = synth.make_weights(spec, seed=0)
+    path = tmp_path / "bt4.pb"
+    netfile.write(path, netfile.spec_net_bytes(spec, weights, synth.tensor_layout(spec)))
+    wf = backend.load_weights(str(path))
+    assert wf.headcount == spec.heads and wf.format["network"] == 7
+    assert sorted(wf.tensors) == sorted(weights)
+    planes, _ = synth.playout_positions(16, seed=2)
+    from_file = wf.create_network(max_batch=16)
+    del wf
+    got = from_file.eval_planes(planes)
+    from_file.close()
+    ref_net = backend.create_network(spec, weights, max_batch=16)
+    want = ref_net.eval_planes(planes)
+    ref_net.close()
+    for g, w in zip(got, want):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
 
 
 def test_bad_batch_rejected():
