@@ -218,7 +218,7 @@ def main():
     spec = synth.SPECS["bt4"]
     B = args.batch
     weights = synth.make_weights(spec, seed=args.seed)
-    planes, _ = synth.playout_positions(B, seed=args.seed)
+    planes, legal = synth.playout_positions(B, seed=args.seed)
     masks, values = backend.pack_planes(planes)
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -287,6 +287,59 @@ def main():
                 "hbm_roofline_frac": round(weight_bytes / (p50 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                 "mfma_roofline_frac": round(GFLOP_PER_POSITION * 1e9 * b / (p50 * 1e-3) / 1e12 /
                                             PEAK_BF16_TFLOPS, 4)}
+    # Legal-move priors on the device (mfh_net_eval_priors) against the
+    # 1858-logit round trip (mfh_net_eval) at the headline batch: host wall
+    # clock per call (PCIe included), bytes per position back to the host,
+    # and the priors kernel's own time (device-resident forward with and
+    # without it).
+    mcts = {}
+    if not args.no_extras:
+        moves = [l[l >= 0].astype(np.int16) for l in legal]
+        avg_moves = float(np.mean([m.size for m in moves]))
+
+        def wall_ms(fn, iters=10):
+            fn()
+            fn()
+            t = time.perf_counter()
+            for _ in range(iters):
+                fn()
+            return (time.perf_counter() - t) * 1e3 / iters
+
+        logits_ms = wall_ms(lambda: run.net.eval_packed(masks, values))
+        priors_ms = wall_ms(lambda: run.net.eval_priors(masks, values, moves, 1.0))
+        offsets = np.zeros(B + 1, np.int32)
+        offsets[1:] = np.cumsum([m.size for m in moves])
+        d_off = torch.from_numpy(offsets).cuda()
+        d_idx = torch.from_numpy(np.concatenate(moves)).cuda()
+        d_priors = torch.empty(int(offsets[-1]), dtype=torch.float32, device="cuda")
+
+        def dev_priors():
+            run.net.eval_priors_device(B, run.d_masks.data_ptr(), run.d_values.data_ptr(),
+                                       d_off.data_ptr(), d_idx.data_ptr(), 1.0,
+                                       run.d_policy.data_ptr(), d_priors.data_ptr(),
+                                       run.d_wdl.data_ptr(), stream.cuda_stream)
+
+        def dev_time(fn, iters=20):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            z = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(iters):
+                fn()
+            z.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(z) / iters
+
+        fwd_ms = dev_time(lambda: run.step(B))
+        fwd_priors_ms = dev_time(dev_priors)
+        mcts = {"batch": B, "moves_per_position": round(avg_moves, 2),
+                "d2h_bytes_per_position": {"logits": 1858 * 4 + 12,
+                                           "priors": round(avg_moves * 4 + 12, 1)},
+                "host_call_ms": {"logits": round(logits_ms, 4), "priors": round(priors_ms, 4)},
+                "device_forward_ms": round(fwd_ms, 4),
+                "device_forward_plus_priors_ms": round(fwd_priors_ms, 4)}
     run.close()
 
     # Config 4: one encoder layer at the BT4 shape, bf16 activations.
@@ -390,6 +443,7 @@ def main():
             "p50": round(float(np.percentile(lat1, 50)), 4),
             "p99": round(float(np.percentile(lat1, 99)), 4)},
         "small_batch": small,
+        "mcts_priors": mcts,
         "encoder_layer": layer,
         "precisions": precisions,
         "fp8_weights": fp8,

@@ -133,6 +133,40 @@ int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
                         const float *d_values, float *d_policy, float *d_wdl,
                         void *stream);
 
+/* Forward pass plus the MCTS priors of each position's legal moves, so that
+ * only the priors and the value head output cross PCIe (about 35 floats per
+ * position instead of 1858).  Replaces the host-side gather of
+ * NNMCTSEvaluator::BuildResult (reference src/mcts/evaluator.cpp:181-224)
+ * and the softmax of ApplyNNPolicyToNode (reference src/mcts/search.cpp:
+ * 127-199), which keep working unchanged on mfh_net_eval's logits.
+ *
+ * The moves of position b are move_indices[move_offsets[b] ..
+ * move_offsets[b + 1]) in the caller's edge order: policy indices as
+ * MoveToNNIndex gives them (side-to-move mirroring and transform applied by
+ * the caller); an index outside 0..1857 reads logit 0, as BuildResult does.
+ * move_offsets[0] must be 0 and each position has 0..256 moves (kMaxEdges,
+ * search.cpp:49).  priors[move_offsets[batch]] receives, per position,
+ * exp((logit - max) / softmax_temp) with the reference's Schraudolph
+ * exponential (src/mcts/core.h:38-44), divided by their sequential sum (1/n
+ * each when the sum is not positive): the same float operations in the same
+ * order as the reference, so the priors equal the CPU computation on the
+ * same logits bit for bit.  wdl as in mfh_net_eval; moves_left must be
+ * NULL. */
+int mfh_net_eval_priors(mfh_net *net, int batch, const uint64_t *masks,
+                        const float *values, const int32_t *move_offsets,
+                        const int16_t *move_indices, float softmax_temp,
+                        float *priors, float *wdl, float *moves_left);
+
+/* Same on device-resident buffers, enqueued on `stream` like
+ * mfh_net_eval_device; d_policy receives the raw logits on the way.  The
+ * offsets are read on the device and are not checked: the caller keeps them
+ * within the rules above. */
+int mfh_net_eval_priors_device(mfh_net *net, int batch, const uint64_t *d_masks,
+                               const float *d_values, const int32_t *d_move_offsets,
+                               const int16_t *d_move_indices, float softmax_temp,
+                               float *d_policy, float *d_priors, float *d_wdl,
+                               void *stream);
+
 /* Human-readable description (GetNetworkInfo, reference network.h:47). */
 int mfh_net_info(const mfh_net *net, char *buf, size_t len);
 

@@ -33,7 +33,8 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_pack_planes", "mfh_device_count", "mfh_last_error", "mfh_debug_unpack_planes",
            "mfh_debug_gemm_bf16", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8",
            "mfh_weights_load", "mfh_weights_parse", "mfh_weights_describe",
-           "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free")
+           "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
+           "mfh_net_eval_priors", "mfh_net_eval_priors_device")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -106,6 +107,9 @@ def lib():
             "mfh_weights_tensor_dims": ([vp, i, ctypes.POINTER(ctypes.POINTER(ctypes.c_uint32)),
                                          ctypes.POINTER(i)], i),
             "mfh_weights_free": ([vp], None),
+            "mfh_net_eval_priors": ([vp, i, vp, vp, vp, vp, ctypes.c_float, vp, vp, vp], i),
+            "mfh_net_eval_priors_device": ([vp, i, vp, vp, vp, vp, ctypes.c_float, vp, vp, vp,
+                                            vp], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -225,6 +229,41 @@ class HipNetwork:
                                              _ptr(policy[s:e]), _ptr(value[s:e]), None),
                    "mfh_net_eval_planes")
         return policy, value
+
+    def eval_priors(self, masks, values, moves, softmax_temp=1.0):
+        """MCTS priors of each position's legal moves, computed on the device
+        (mfh_net_eval_priors).  ``moves``: one sequence of policy indices per
+        position (at most 256).  Returns (list of float32 prior arrays, raw
+        value head output [B, 3] or [B, 1])."""
+        masks = np.ascontiguousarray(masks, dtype=np.uint64).reshape(-1, 112)
+        values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1, 112)
+        b = masks.shape[0]
+        if len(moves) != b:
+            raise ValueError("one move list per position")
+        priors_out, value_out = [], []
+        for s in range(0, b, self.max_batch):
+            e = min(b, s + self.max_batch)
+            chunk = [np.asarray(m, dtype=np.int16).reshape(-1) for m in moves[s:e]]
+            offsets = np.zeros(e - s + 1, np.int32)
+            offsets[1:] = np.cumsum([c.size for c in chunk])
+            idx = np.concatenate(chunk) if offsets[-1] else np.zeros(1, np.int16)
+            priors = np.zeros(max(1, int(offsets[-1])), np.float32)
+            value = np.zeros((e - s, 3 if self.wdl else 1), np.float32)
+            _check(lib().mfh_net_eval_priors(self._h, e - s, _ptr(masks[s:e]), _ptr(values[s:e]),
+                                             _ptr(offsets), _ptr(idx), float(softmax_temp),
+                                             _ptr(priors), _ptr(value), None),
+                   "mfh_net_eval_priors")
+            priors_out += [priors[offsets[j]:offsets[j + 1]] for j in range(e - s)]
+            value_out.append(value)
+        return priors_out, np.concatenate(value_out)
+
+    def eval_priors_device(self, batch, d_masks, d_values, d_offsets, d_indices, softmax_temp,
+                           d_policy, d_priors, d_wdl, stream=None):
+        """Device-resident form of eval_priors (pointers are device addresses)."""
+        _check(lib().mfh_net_eval_priors_device(self._h, batch, d_masks, d_values, d_offsets,
+                                                d_indices, float(softmax_temp), d_policy,
+                                                d_priors, d_wdl, stream),
+               "mfh_net_eval_priors_device")
 
     def evaluate_batch(self, planes):
         """NetworkOutput fields for planes [B,112,64] (EvaluateBatch)."""

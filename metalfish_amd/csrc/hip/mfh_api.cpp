@@ -50,6 +50,7 @@ int SetError(int code, const std::string &msg) {
   } while (0)
 
 constexpr int kSquares = 64;
+constexpr int kMaxMoves = 256;  // edges per node (reference src/mcts/search.cpp:49)
 constexpr int kPlanes = 112;
 constexpr int kPolicy = 1858;
 
@@ -188,7 +189,7 @@ struct mfh_net {
   size_t ws_bytes = 0;
   std::map<std::string, size_t> ws_off;
 
-  unsigned char *pin_in = nullptr;   // masks | values
+  unsigned char *pin_in = nullptr;   // masks | values | move offsets | move indices
   unsigned char *pin_out = nullptr;  // policy | value
   int last_batch = 0;
 
@@ -621,6 +622,10 @@ void PlanWorkspace(mfh_net *net) {
   add("splitk", kSplitKFloats * 4);
   add("policy", B * kPolicy * 4);
   add("wdl", B * 3 * 4);
+  // Legal-move priors (mfh_net_eval_priors): offsets, policy indices, priors.
+  add("move_offsets", (B + 1) * 4);
+  add("move_indices", B * kMaxMoves * 2);
+  add("priors", B * kMaxMoves * 4);
   net->ws_bytes = AlignUp(off, 256);
 }
 
@@ -1039,6 +1044,81 @@ int RunStaged(mfh_net *net, int batch) {
   return MFH_OK;
 }
 
+// Pinned input layout: masks, values, then the move offsets and indices of
+// mfh_net_eval_priors (16-byte aligned).
+size_t PinOffsetsOffset(int max_batch) {
+  return AlignUp(static_cast<size_t>(max_batch) * kPlanes * 12, 16);
+}
+size_t PinMovesOffset(int max_batch) {
+  return AlignUp(PinOffsetsOffset(max_batch) + (static_cast<size_t>(max_batch) + 1) * 4, 16);
+}
+
+// Forward plus the legal-move priors for a batch staged in pin_in (inputs,
+// offsets and indices); priors land in the policy area of pin_out, the value
+// head output after the max_batch policy rows as for RunStaged.
+int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
+  const size_t n_in = static_cast<size_t>(batch) * kPlanes;
+  auto *d_masks = net->S<std::uint64_t>("masks");
+  auto *d_values = net->S<float>("values");
+  auto *d_policy = net->S<float>("policy");
+  auto *d_wdl = net->S<float>("wdl");
+  auto *d_offsets = net->S<std::int32_t>("move_offsets");
+  auto *d_indices = net->S<std::int16_t>("move_indices");
+  auto *d_priors = net->S<float>("priors");
+  const unsigned char *pin = net->pin_in;
+  const size_t mb = static_cast<size_t>(net->max_batch);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  MFH_HIP_CHECK(hipMemcpyAsync(d_masks, pin, n_in * 8, hipMemcpyHostToDevice, net->stream));
+  MFH_HIP_CHECK(hipMemcpyAsync(d_values, pin + mb * kPlanes * 8, n_in * 4,
+                               hipMemcpyHostToDevice, net->stream));
+  MFH_HIP_CHECK(hipMemcpyAsync(d_offsets, pin + PinOffsetsOffset(net->max_batch),
+                               (static_cast<size_t>(batch) + 1) * 4, hipMemcpyHostToDevice,
+                               net->stream));
+  if (total_moves > 0)
+    MFH_HIP_CHECK(hipMemcpyAsync(d_indices, pin + PinMovesOffset(net->max_batch),
+                                 static_cast<size_t>(total_moves) * 2, hipMemcpyHostToDevice,
+                                 net->stream));
+  int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->stream);
+  if (rc == MFH_OK) {
+    std::string err;
+    if (mfh::LaunchPolicyPriors(d_policy, d_offsets, d_indices, batch, inv_temp, d_priors,
+                           net->stream, &err) != hipSuccess)
+      rc = SetError(MFH_ERR_HIP, "policy priors launch failed: " + err);
+  }
+  if (rc != MFH_OK) {
+    (void)hipStreamSynchronize(net->stream);
+    return rc;
+  }
+  auto *pin_priors = reinterpret_cast<float *>(net->pin_out);
+  auto *pin_value = pin_priors + mb * kPolicy;
+  if (total_moves > 0)
+    MFH_HIP_CHECK(hipMemcpyAsync(pin_priors, d_priors, static_cast<size_t>(total_moves) * 4,
+                                 hipMemcpyDeviceToHost, net->stream));
+  MFH_HIP_CHECK(hipMemcpyAsync(pin_value, d_wdl, static_cast<size_t>(batch) * net->d.Vout * 4,
+                               hipMemcpyDeviceToHost, net->stream));
+  MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
+  net->last_batch = batch;
+  return MFH_OK;
+}
+
+// Move offsets must start at 0 and give each position 0..256 moves.
+int CheckMoves(int batch, const std::int32_t *offsets, int *total) {
+  if (!offsets)
+    return SetError(MFH_ERR_INVALID, "null move offsets");
+  if (offsets[0] != 0)
+    return SetError(MFH_ERR_INVALID, "move offsets must start at 0");
+  for (int b = 0; b < batch; ++b) {
+    const std::int64_t n = static_cast<std::int64_t>(offsets[b + 1]) - offsets[b];
+    if (n < 0 || n > kMaxMoves) {
+      std::ostringstream o;
+      o << "position " << b << " has " << n << " moves (allowed 0.." << kMaxMoves << ")";
+      return SetError(MFH_ERR_INVALID, o.str());
+    }
+  }
+  *total = offsets[batch];
+  return MFH_OK;
+}
+
 int CopyOut(mfh_net *net, int batch, float *policy, float *wdl) {
   const auto *pin_policy = reinterpret_cast<const float *>(net->pin_out);
   const auto *pin_value = pin_policy + static_cast<size_t>(net->max_batch) * kPolicy;
@@ -1135,7 +1215,8 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     cleanup();
     return SetError(MFH_ERR_OUT_OF_MEMORY, "workspace allocation failed");
   }
-  const size_t in_bytes = static_cast<size_t>(net->max_batch) * kPlanes * 12;
+  const size_t in_bytes = PinMovesOffset(net->max_batch) +
+                          static_cast<size_t>(net->max_batch) * kMaxMoves * 2;
   const size_t out_bytes = static_cast<size_t>(net->max_batch) * (kPolicy + 3) * 4;
   if (hipHostMalloc(reinterpret_cast<void **>(&net->pin_in), in_bytes, hipHostMallocDefault) !=
           hipSuccess ||
@@ -1221,6 +1302,65 @@ int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
   if (rc == MFH_OK)
     net->last_batch = batch;
   return rc;
+}
+
+int mfh_net_eval_priors(mfh_net *net, int batch, const uint64_t *masks, const float *values,
+                        const int32_t *move_offsets, const int16_t *move_indices,
+                        float softmax_temp, float *priors, float *wdl, float *moves_left) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (!masks || !values || !wdl || moves_left)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_priors: bad output/input pointers");
+  int total = 0;
+  rc = CheckMoves(batch, move_offsets, &total);
+  if (rc != MFH_OK)
+    return rc;
+  if (total > 0 && (!move_indices || !priors))
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_priors: null move indices or priors");
+  std::lock_guard<std::mutex> lock(net->mu);
+  const size_t n_in = static_cast<size_t>(batch) * kPlanes;
+  const size_t mb = static_cast<size_t>(net->max_batch);
+  std::memcpy(net->pin_in, masks, n_in * 8);
+  std::memcpy(net->pin_in + mb * kPlanes * 8, values, n_in * 4);
+  std::memcpy(net->pin_in + PinOffsetsOffset(net->max_batch), move_offsets,
+              (static_cast<size_t>(batch) + 1) * 4);
+  if (total > 0)
+    std::memcpy(net->pin_in + PinMovesOffset(net->max_batch), move_indices,
+                static_cast<size_t>(total) * 2);
+  // ApplyNNPolicyToNode (search.cpp:133) multiplies by 1 / temperature.
+  rc = RunStagedPriors(net, batch, total, 1.0f / softmax_temp);
+  if (rc != MFH_OK)
+    return rc;
+  const auto *pin_priors = reinterpret_cast<const float *>(net->pin_out);
+  if (total > 0)
+    std::memcpy(priors, pin_priors, static_cast<size_t>(total) * 4);
+  std::memcpy(wdl, pin_priors + mb * kPolicy, static_cast<size_t>(batch) * net->d.Vout * 4);
+  return MFH_OK;
+}
+
+int mfh_net_eval_priors_device(mfh_net *net, int batch, const uint64_t *d_masks,
+                               const float *d_values, const int32_t *d_move_offsets,
+                               const int16_t *d_move_indices, float softmax_temp,
+                               float *d_policy, float *d_priors, float *d_wdl, void *stream) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (!d_masks || !d_values || !d_move_offsets || !d_move_indices || !d_policy || !d_priors ||
+      !d_wdl)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_priors_device: null pointer");
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, st);
+  if (rc != MFH_OK)
+    return rc;
+  std::string err;
+  if (mfh::LaunchPolicyPriors(d_policy, d_move_offsets, d_move_indices, batch, 1.0f / softmax_temp,
+                         d_priors, st, &err) != hipSuccess)
+    return SetError(MFH_ERR_HIP, "policy priors launch failed: " + err);
+  net->last_batch = batch;
+  return MFH_OK;
 }
 
 int mfh_net_info(const mfh_net *net, char *buf, size_t len) {

@@ -146,6 +146,14 @@ hipError_t LaunchPolicyMap(const std::uint16_t *qk, const std::uint16_t *qk_lo,
                            const std::int16_t *gather, float *policy,
                            hipStream_t stream, std::string *err);
 
+// MCTS priors over each position's legal moves (reference
+// src/mcts/search.cpp:127-199): policy [B, 1858] raw logits, offsets [B + 1]
+// into indices (policy indices, at most 256 per position; an index outside
+// [0, 1858) reads logit 0), priors written at the same offsets.
+hipError_t LaunchPolicyPriors(const float *policy, const std::int32_t *offsets,
+                              const std::int16_t *indices, int batch, float inv_temp,
+                              float *priors, hipStream_t stream, std::string *err);
+
 // Value head output: hidden = act(sum of `parts` partials [parts][B][vh] + b1)
 // then dense2 + softmax (WDL, 3 outputs) or tanh (scalar, 1 output).
 hipError_t LaunchValueHead(const float *hidden, int parts, const float *b1,

@@ -21,6 +21,7 @@ namespace {
 
 constexpr int kSq = 64;
 constexpr int kOutputs = 1858;
+constexpr int kMaxMoves = 256;
 
 template <bool SPLIT>
 __global__ __launch_bounds__(1024) void PolicyMapKernel(
@@ -103,7 +104,95 @@ __global__ __launch_bounds__(1024) void PolicyMapKernel(
   }
 }
 
+// Schraudolph's exponential (N. N. Schraudolph, "A fast, compact
+// approximation of the exponential function", Neural Computation 11(4),
+// 1999): the binary32 pattern int(x * 2^23 / ln 2) + 127 * 2^23, with x
+// clamped to [-88, 88] as the reference's MCTS does (src/mcts/core.h:38-44).
+// The clamp keeps the comparisons of std::min / std::max (a NaN becomes 88).
+__device__ __forceinline__ float SchraudolphExp(float x) {
+  x = x < 88.0f ? x : 88.0f;
+  x = -88.0f < x ? x : -88.0f;
+  const int bits = static_cast<int>(x * 12102203.0f) + 1065353216;
+  return __int_as_float(bits);
+}
+
+// MCTS priors of the legal moves (reference ApplyNNPolicyToNode,
+// src/mcts/search.cpp:127-199, fed as NNMCTSEvaluator::BuildResult feeds it,
+// src/mcts/evaluator.cpp:181-224): logit = policy[idx] for an index inside
+// [0, 1858) and 0 otherwise; max over the moves; p = exp((logit - max) /
+// temperature) with Schraudolph's exponential; a sequential sum in move order;
+// p / sum, or 1 / n when the sum is not positive.  Every step is the same IEEE
+// operation in the same order as on the CPU, so the priors match the CPU
+// computation bit for bit.  One wave per position, at most 256 moves
+// (search.cpp:49 kMaxEdges); the moves of position b are
+// indices[offsets[b] .. offsets[b + 1]).
+__global__ __launch_bounds__(64) void PolicyPriorsKernel(
+    const float *__restrict__ policy, const std::int32_t *__restrict__ offsets,
+    const std::int16_t *__restrict__ indices, float inv_temp, float *__restrict__ priors) {
+  __shared__ float e[kMaxMoves];
+  __shared__ float total;
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int start = offsets[b];
+  int n = offsets[b + 1] - start;
+  n = n < 0 ? 0 : (n > kMaxMoves ? kMaxMoves : n);
+  const float *logits = policy + static_cast<size_t>(b) * kOutputs;
+  float l[kMaxMoves / 64];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int r = 0; r < kMaxMoves / 64; ++r) {
+    const int i = r * 64 + lane;
+    l[r] = 0.0f;
+    if (i < n) {
+      const int k = indices[start + i];
+      l[r] = k >= 0 && k < kOutputs ? logits[k] : 0.0f;
+      m = l[r] > m ? l[r] : m;  // a NaN never replaces the running maximum
+    }
+  }
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    const float o = __shfl_xor(m, s);
+    m = o > m ? o : m;
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxMoves / 64; ++r) {
+    const int i = r * 64 + lane;
+    if (i < n)
+      e[i] = SchraudolphExp((l[r] - m) * inv_temp);
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float sum = 0.0f;
+    for (int i = 0; i < n; ++i)
+      sum += e[i];
+    total = sum;
+  }
+  __syncthreads();
+  const float sum = total;
+  const bool uniform = sum <= 0.0f;
+  const float scale = uniform ? 1.0f / static_cast<float>(n > 0 ? n : 1) : 1.0f / sum;
+#pragma unroll
+  for (int r = 0; r < kMaxMoves / 64; ++r) {
+    const int i = r * 64 + lane;
+    if (i < n)
+      priors[start + i] = uniform ? scale : e[i] * scale;
+  }
+}
+
 }  // namespace
+
+hipError_t LaunchPolicyPriors(const float *policy, const std::int32_t *offsets,
+                              const std::int16_t *indices, int batch, float inv_temp,
+                              float *priors, hipStream_t stream, std::string *err) {
+  if (batch <= 0 || !policy || !offsets || !indices || !priors) {
+    if (err)
+      *err = "policy_priors: needs batch > 0 and non-null buffers";
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(PolicyPriorsKernel, dim3(batch), dim3(64), 0, stream, policy, offsets,
+                     indices, inv_temp, priors);
+  return hipGetLastError();
+}
 
 hipError_t LaunchPolicyMap(const std::uint16_t *qk, const std::uint16_t *qk_lo, int batch,
                            int dp, const float *promo, const std::int16_t *gather,

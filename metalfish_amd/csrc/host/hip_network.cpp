@@ -157,6 +157,49 @@ std::vector<NetworkOutput> HipNetwork::EvaluateBatch(const std::vector<InputPlan
   return outputs;
 }
 
+std::vector<PriorsOutput> HipNetwork::EvaluateBatchPriors(
+    const std::vector<InputPlanes> &inputs,
+    const std::vector<std::vector<std::int16_t>> &move_indices, float softmax_temp) {
+  if (move_indices.size() != inputs.size())
+    throw std::runtime_error("HIP backend: one move list per position is required");
+  std::vector<PriorsOutput> outputs(inputs.size());
+  std::vector<std::int32_t> offsets;
+  std::vector<std::int16_t> flat;
+  std::vector<float> priors;
+  for (std::size_t start = 0; start < inputs.size(); start += max_batch_) {
+    const int count = static_cast<int>(std::min<std::size_t>(max_batch_, inputs.size() - start));
+    masks_.resize(static_cast<std::size_t>(count) * kTotalPlanes);
+    values_.resize(masks_.size());
+    int rc = mfh_pack_planes(count, inputs[start][0].data(), masks_.data(), values_.data());
+    offsets.assign(1, 0);
+    flat.clear();
+    for (int b = 0; b < count; ++b) {
+      const auto &m = move_indices[start + b];
+      flat.insert(flat.end(), m.begin(), m.end());
+      offsets.push_back(static_cast<std::int32_t>(flat.size()));
+    }
+    priors.resize(flat.size());
+    if (rc == MFH_OK)
+      rc = mfh_net_eval_priors(net_, count, masks_.data(), values_.data(), offsets.data(),
+                               flat.data(), softmax_temp, priors.data(), value_.data(), nullptr);
+    if (rc != MFH_OK)
+      throw std::runtime_error(LastError("priors evaluation", rc));
+    for (int b = 0; b < count; ++b) {
+      PriorsOutput &out = outputs[start + b];
+      out.priors.assign(priors.begin() + offsets[b], priors.begin() + offsets[b + 1]);
+      if (wdl_) {
+        out.has_wdl = true;
+        for (int k = 0; k < 3; ++k)
+          out.wdl[k] = value_[3 * b + k];
+        out.value = out.wdl[0] - out.wdl[2];
+      } else {
+        out.value = value_[b];
+      }
+    }
+  }
+  return outputs;
+}
+
 std::string HipNetwork::GetNetworkInfo() const {
   char buf[1024];
   if (mfh_net_info(net_, buf, sizeof(buf)) != MFH_OK)

@@ -44,6 +44,16 @@ struct HipNetworkConfig {
   int device = -1;
 };
 
+// Result of EvaluateBatchPriors for one position: the MCTS priors of its
+// legal moves in the caller's order, and the value head output decoded as
+// NetworkOutput decodes it (value = W - L for WDL nets).
+struct PriorsOutput {
+  std::vector<float> priors;
+  float value = 0.0f;
+  float wdl[3] = {};
+  bool has_wdl = false;
+};
+
 class HipNetwork : public Network {
 public:
   HipNetwork(const std::vector<WeightTensor> &weights, const HipNetworkConfig &config);
@@ -58,6 +68,13 @@ public:
 
   NetworkOutput Evaluate(const InputPlanes &input) override;
   std::vector<NetworkOutput> EvaluateBatch(const std::vector<InputPlanes> &inputs) override;
+  // The legal-move gather and prior softmax of the MCTS evaluator
+  // (reference src/mcts/evaluator.cpp:181-224, src/mcts/search.cpp:127-199)
+  // done on the device: move_indices[i] holds position i's policy indices
+  // (MoveToNNIndex order, at most 256), and only the priors come back.
+  std::vector<PriorsOutput> EvaluateBatchPriors(
+      const std::vector<InputPlanes> &inputs,
+      const std::vector<std::vector<std::int16_t>> &move_indices, float softmax_temp);
   std::string GetNetworkInfo() const override;
   bool HasWDL() const override { return wdl_; }
   bool HasMovesLeft() const override { return false; }
@@ -72,6 +89,8 @@ private:
   int max_batch_ = 0;
   std::vector<float> policy_;
   std::vector<float> value_;
+  std::vector<std::uint64_t> masks_;
+  std::vector<float> values_;
 };
 
 }  // namespace Hip

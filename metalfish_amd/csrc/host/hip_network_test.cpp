@@ -2,12 +2,15 @@
 // net file and a planes file, builds HipNetwork, runs EvaluateBatch and
 // Evaluate, and writes the NetworkOutput fields for comparison.
 //
-// Usage: hip_network_test NET PLANES OUT HEADS PRECISION MAX_BATCH
+// Usage: hip_network_test NET PLANES OUT HEADS PRECISION MAX_BATCH [MOVES TEMP]
 //   NET    : u32 count, then per tensor u32 name_len, name, u64 n, n floats;
 //            or a network file ending in ".pb" / ".pb.gz" (HEADS unused)
 //   PLANES : u32 batch, then batch*112*64 floats
 //   OUT    : batch*(1858+3+1) floats from EvaluateBatch, then the same for
-//            Evaluate of each position
+//            Evaluate of each position; with MOVES, then the priors of
+//            EvaluateBatchPriors (offsets[batch] floats) and its batch*4
+//            value fields (wdl[3], value)
+//   MOVES  : i32 offsets[batch+1], then i16 policy indices[offsets[batch]]
 // Exit codes: 0 ok, 2 usage or file error, 3 std::exception (message on stderr).
 #include <cstdint>
 #include <cstdio>
@@ -46,8 +49,9 @@ void Append(std::vector<float> &out, const NetworkOutput &o) {
 }  // namespace
 
 int main(int argc, char **argv) {
-  if (argc != 7) {
-    std::fprintf(stderr, "usage: %s NET PLANES OUT HEADS PRECISION MAX_BATCH\n", argv[0]);
+  if (argc != 7 && argc != 9) {
+    std::fprintf(stderr, "usage: %s NET PLANES OUT HEADS PRECISION MAX_BATCH [MOVES TEMP]\n",
+                 argv[0]);
     return 2;
   }
   const std::string net_path = argv[1];
@@ -107,6 +111,25 @@ int main(int argc, char **argv) {
       Append(out, o);
     for (const auto &in : inputs)
       Append(out, net.Evaluate(in));
+    if (argc == 9) {
+      std::vector<char> move_bytes;
+      if (!ReadAll(argv[7], move_bytes))
+        return 2;
+      std::vector<std::int32_t> offsets(batch + 1);
+      std::memcpy(offsets.data(), move_bytes.data(), offsets.size() * 4);
+      const auto *idx = reinterpret_cast<const std::int16_t *>(move_bytes.data() +
+                                                              offsets.size() * 4);
+      std::vector<std::vector<std::int16_t>> moves(batch);
+      for (std::uint32_t b = 0; b < batch; ++b)
+        moves[b].assign(idx + offsets[b], idx + offsets[b + 1]);
+      const auto priors = net.EvaluateBatchPriors(inputs, moves, std::strtof(argv[8], nullptr));
+      for (const auto &p : priors)
+        out.insert(out.end(), p.priors.begin(), p.priors.end());
+      for (const auto &p : priors) {
+        out.insert(out.end(), p.wdl, p.wdl + 3);
+        out.push_back(p.value);
+      }
+    }
     std::FILE *f = std::fopen(argv[3], "wb");
     if (!f || std::fwrite(out.data(), 4, out.size(), f) != out.size())
       return 2;

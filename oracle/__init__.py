@@ -95,3 +95,43 @@ class OracleNet:
 def ctypes_addr(arr):
     import ctypes
     return ctypes.addressof(arr)
+
+
+def fast_exp(x):
+    """FastMath::FastExp (reference src/mcts/core.h:38-44), elementwise on
+    float32: clamp to [-88, 88] with std::min/std::max comparisons (NaN ->
+    88), then the binary32 pattern int(x * 12102203) + 1065353216
+    (Schraudolph's method)."""
+    x = np.asarray(x, dtype=np.float32)
+    x = np.where(x < np.float32(88.0), x, np.float32(88.0)).astype(np.float32)
+    x = np.where(np.float32(-88.0) < x, x, np.float32(-88.0)).astype(np.float32)
+    prod = (x * np.float32(12102203.0)).astype(np.float32)
+    bits = np.trunc(prod).astype(np.int64) + 1065353216
+    return bits.astype(np.int32).view(np.float32)
+
+
+def mcts_priors(logits, indices, softmax_temp):
+    """Priors of one position's legal moves as the reference's MCTS forms
+    them: BuildResult's gather (src/mcts/evaluator.cpp:193-204: logit 0 for an
+    index outside the policy) and ApplyNNPolicyToNode
+    (src/mcts/search.cpp:127-199: max, FastExp((l - max) * (1 / temp)),
+    sequential float32 sum, multiply by 1 / sum, or 1 / n when the sum is not
+    positive).  ``logits`` [1858] float32, ``indices`` the move list."""
+    logits = np.asarray(logits, dtype=np.float32)
+    idx = np.asarray(indices, dtype=np.int64)
+    n = idx.size
+    if n == 0:
+        return np.zeros(0, np.float32)
+    ok = (idx >= 0) & (idx < logits.size)
+    l = np.where(ok, logits[np.where(ok, idx, 0)], np.float32(0.0)).astype(np.float32)
+    m = np.float32(-np.inf)
+    for v in l:  # the reference's sequential "if (l > max) max = l"
+        if v > m:
+            m = v
+    inv_temp = np.float32(1.0) / np.float32(softmax_temp)
+    p = fast_exp(((l - m).astype(np.float32) * inv_temp).astype(np.float32))
+    total = np.add.accumulate(p, dtype=np.float32)[-1]
+    if not total > np.float32(0.0) and not np.isnan(total):
+        return np.full(n, np.float32(1.0) / np.float32(n), dtype=np.float32)
+    inv = np.float32(1.0) / total
+    return (p * inv).astype(np.float32)

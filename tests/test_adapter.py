@@ -125,3 +125,33 @@ def test_adapter_from_network_file_matches_tensors(tmp_path, plumbing):
                           text=True, timeout=300)
     assert proc.returncode == 0, proc.stderr
     assert np.array_equal(np.fromfile(out2, dtype=np.float32).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_adapter_priors_match_cpu_computation(tmp_path, plumbing):
+    """HipNetwork::EvaluateBatchPriors: per position, the priors of its legal
+    moves equal the reference's CPU computation on the logits EvaluateBatch
+    returns, bit for bit, across max_batch chunks."""
+    spec, weights = plumbing
+    n = 20
+    planes, legal = synth.playout_positions(n, seed=21)
+    moves = [l[l >= 0].astype(np.int16) for l in legal]
+    offsets = np.zeros(n + 1, np.int32)
+    offsets[1:] = np.cumsum([m.size for m in moves])
+    mv = tmp_path / "moves.bin"
+    mv.write_bytes(offsets.tobytes() + np.concatenate(moves).tobytes())
+    net, pl, out = (str(tmp_path / x) for x in ("net.bin", "planes.bin", "out.bin"))
+    _write_net(net, weights)
+    _write_planes(pl, planes)
+    proc = subprocess.run([DRIVER, net, pl, out, str(spec.heads), "bf16x2", "8", str(mv), "0.7"],
+                          capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr
+    got = np.fromfile(out, dtype=np.float32)
+    base = got[:2 * n * (1858 + 4)].reshape(2, n, 1858 + 4)
+    priors = got[2 * n * (1858 + 4):2 * n * (1858 + 4) + offsets[-1]]
+    tail = got[2 * n * (1858 + 4) + offsets[-1]:].reshape(n, 4)
+    for b in range(n):
+        want = oracle.mcts_priors(base[0, b, :1858], moves[b], 0.7)
+        assert np.array_equal(priors[offsets[b]:offsets[b + 1]].view(np.uint32),
+                              want.view(np.uint32)), b
+    assert np.array_equal(tail.view(np.uint32), base[0, :, 1858:].view(np.uint32))

@@ -12,6 +12,8 @@ random-init nets the legal-move logits of many positions are within a few
 is reported rather than gated.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -240,6 +242,110 @@ def test_bt4_net_from_network_file(tmp_path):
     ref_net.close()
     for g, w in zip(got, want):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+
+
+def _move_lists(legal, rng):
+    """Real legal-move lists plus the edge cases: no moves, 256 moves with
+    out-of-range and repeated indices, a single move."""
+    moves = [l[l >= 0].astype(np.int16) for l in legal]
+    moves[1] = np.zeros(0, np.int16)
+    wild = rng.integers(0, 1858, 256).astype(np.int16)
+    wild[:6] = [-1, 1858, 2000, -300, 5, 5]
+    moves[2] = wild
+    moves[3] = moves[3][:1]
+    return moves
+
+
+@pytest.mark.parametrize("temp", [1.0, 0.45, 2.2])
+def test_mcts_priors_on_device(temp):
+    """mfh_net_eval_priors equals the reference's CPU prior computation
+    (oracle.mcts_priors, a restatement of search.cpp:127-199 and
+    evaluator.cpp:181-224) applied to the same logits, bit for bit, across
+    max_batch chunks; the value head output equals mfh_net_eval's."""
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=1)
+    net = backend.create_network(spec, weights, max_batch=16)
+    planes, legal = synth.playout_positions(24, seed=11)
+    masks, values = backend.pack_planes(planes)
+    moves = _move_lists(legal, np.random.default_rng(7))
+    logits, wdl = net.eval_packed(masks, values)
+    priors, wdl2 = net.eval_priors(masks, values, moves, temp)
+    assert np.array_equal(wdl.view(np.uint32), wdl2.view(np.uint32))
+    for b in range(len(moves)):
+        want = oracle.mcts_priors(logits[b], moves[b], temp)
+        assert priors[b].shape == want.shape
+        assert np.array_equal(priors[b].view(np.uint32), want.view(np.uint32)), b
+    net.close()
+
+
+class _DeviceBuffers:
+    """Device copies of numpy arrays through the HIP runtime libmfhip.so
+    itself uses (hipMalloc / hipMemcpy / hipFree via ctypes)."""
+
+    def __init__(self):
+        backend.lib()  # loads libamdhip64 as a dependency
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        self.hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_int]
+        self.hip.hipFree.argtypes = [ctypes.c_void_p]
+        self.ptrs = []
+
+    def put(self, arr):
+        arr = np.ascontiguousarray(arr)
+        p = ctypes.c_void_p()
+        assert self.hip.hipMalloc(ctypes.byref(p), max(arr.nbytes, 4)) == 0
+        self.ptrs.append(p.value)
+        if arr.nbytes:
+            assert self.hip.hipMemcpy(p.value, arr.ctypes.data, arr.nbytes, 1) == 0
+        return p.value
+
+    def get(self, ptr, like):
+        out = np.empty_like(like)
+        assert self.hip.hipMemcpy(out.ctypes.data, ptr, out.nbytes, 2) == 0
+        return out
+
+    def free(self):
+        for p in self.ptrs:
+            self.hip.hipFree(p)
+        self.ptrs = []
+
+
+def test_mcts_priors_device_entry_and_errors():
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=1)
+    net = backend.create_network(spec, weights, max_batch=8)
+    planes, legal = synth.playout_positions(8, seed=12)
+    masks, values = backend.pack_planes(planes)
+    moves = [l[l >= 0].astype(np.int16) for l in legal]
+    host_priors, host_wdl = net.eval_priors(masks, values, moves, 1.0)
+    offsets = np.zeros(9, np.int32)
+    offsets[1:] = np.cumsum([m.size for m in moves])
+    dev = _DeviceBuffers()
+    policy = np.zeros((8, 1858), np.float32)
+    priors = np.zeros(int(offsets[-1]), np.float32)
+    wdl_out = np.zeros((8, 3), np.float32)
+    d_policy, d_priors, d_wdl = dev.put(policy), dev.put(priors), dev.put(wdl_out)
+    # NULL stream: the default stream; hipMemcpy below waits for it.
+    net.eval_priors_device(8, dev.put(masks), dev.put(values), dev.put(offsets),
+                           dev.put(np.concatenate(moves)), 1.0, d_policy, d_priors, d_wdl, None)
+    got = dev.get(d_priors, priors)
+    assert np.array_equal(got.view(np.uint32), np.concatenate(host_priors).view(np.uint32))
+    assert np.array_equal(dev.get(d_wdl, wdl_out).view(np.uint32), host_wdl.view(np.uint32))
+    dev.free()
+    # Host-side checks of the move lists.
+    lib = backend.lib()
+    out = np.zeros(4096, np.float32)
+    wdl = np.zeros((8, 3), np.float32)
+    for bad in (np.array([1, 2, 3, 4, 5, 6, 7, 8, 9], np.int32),           # offsets[0] != 0
+                np.array([0, 257, 257, 257, 257, 257, 257, 257, 257], np.int32),  # > 256 moves
+                np.array([0, 5, 3, 9, 9, 9, 9, 9, 9], np.int32)):              # negative count
+        idx = np.zeros(512, np.int16)
+        rc = lib.mfh_net_eval_priors(net._h, 8, masks.ctypes.data, values.ctypes.data,
+                                     bad.ctypes.data, idx.ctypes.data, 1.0, out.ctypes.data,
+                                     wdl.ctypes.data, None)
+        assert rc == backend.MFH_OK - 1, bad
+    net.close()
 
 
 def test_bad_batch_rejected():
