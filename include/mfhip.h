@@ -53,6 +53,8 @@ enum {
   MFH_ACTIVATION_SWISH = 7,
   MFH_ACTIVATION_RELU_2 = 8
 };
+/* NetworkFormat.MovesLeftFormat (net.proto:310-313). */
+enum { MFH_MOVES_LEFT_NONE = 0, MFH_MOVES_LEFT_V1 = 1 };
 /* NetworkFormat.DefaultActivation (net.proto:331-332). */
 enum { MFH_DEFAULT_ACTIVATION_RELU = 0, MFH_DEFAULT_ACTIVATION_MISH = 1 };
 /* Storage of the GEMM weights on the device.  BF16: each weight rounded to
@@ -76,7 +78,7 @@ typedef struct {
   int network;            /* MFH_NETWORK_ATTENTIONBODY_* */
   int policy;             /* MFH_POLICY_ATTENTION */
   int value;              /* MFH_VALUE_WDL or MFH_VALUE_CLASSICAL */
-  int moves_left;         /* must be 0: no moves-left head yet */
+  int moves_left;         /* 0, or 1 (MOVES_LEFT_V1) for a moves-left head */
   int input_embedding;    /* MFH_INPUT_EMBEDDING_PE_DENSE */
   int default_activation; /* MFH_DEFAULT_ACTIVATION_* */
   int ffn_activation;     /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
@@ -112,7 +114,8 @@ void mfh_net_destroy(mfh_net *net);
  * (reference src/nn/input_plane_packing.h:61-83): masks[batch*112] and
  * values[batch*112].  Outputs: policy[batch*1858] raw logits in the 1858
  * order, wdl[batch*3] (WDL nets) or value[batch] (classical value head),
- * moves_left must be NULL.  Inputs are staged through pinned buffers with
+ * moves_left[batch] (nets with a moves-left head; NULL to skip; must be NULL
+ * otherwise).  Inputs are staged through pinned buffers with
  * asynchronous copies on the net's stream; the call returns when outputs are
  * in place.  Calls on one net are serialised (reference
  * src/nn/cuda/cuda_network.cpp:442).  batch must be 1..max_batch. */
@@ -150,8 +153,7 @@ int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
  * exponential (src/mcts/core.h:38-44), divided by their sequential sum (1/n
  * each when the sum is not positive): the same float operations in the same
  * order as the reference, so the priors equal the CPU computation on the
- * same logits bit for bit.  wdl as in mfh_net_eval; moves_left must be
- * NULL. */
+ * same logits bit for bit.  wdl and moves_left as in mfh_net_eval. */
 int mfh_net_eval_priors(mfh_net *net, int batch, const uint64_t *masks,
                         const float *values, const int32_t *move_offsets,
                         const int16_t *move_indices, float softmax_temp,
@@ -166,6 +168,15 @@ int mfh_net_eval_priors_device(mfh_net *net, int batch, const uint64_t *d_masks,
                                const int16_t *d_move_indices, float softmax_temp,
                                float *d_policy, float *d_priors, float *d_wdl,
                                void *stream);
+
+/* mfh_net_eval_device for a net with a moves-left head, which also writes
+ * d_moves_left[batch] (the reference's NetworkOutput::moves_left,
+ * network_output_decoder.cpp:68-71).  mfh_net_eval_device leaves the
+ * moves-left output in the net's workspace. */
+int mfh_net_eval_device_moves_left(mfh_net *net, int batch,
+                                   const uint64_t *d_masks, const float *d_values,
+                                   float *d_policy, float *d_wdl,
+                                   float *d_moves_left, void *stream);
 
 /* Human-readable description (GetNetworkInfo, reference network.h:47). */
 int mfh_net_info(const mfh_net *net, char *buf, size_t len);

@@ -34,7 +34,8 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_debug_gemm_bf16", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8",
            "mfh_weights_load", "mfh_weights_parse", "mfh_weights_describe",
            "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
-           "mfh_net_eval_priors", "mfh_net_eval_priors_device")
+           "mfh_net_eval_priors", "mfh_net_eval_priors_device",
+           "mfh_net_eval_device_moves_left")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -110,6 +111,7 @@ def lib():
             "mfh_net_eval_priors": ([vp, i, vp, vp, vp, vp, ctypes.c_float, vp, vp, vp], i),
             "mfh_net_eval_priors_device": ([vp, i, vp, vp, vp, vp, ctypes.c_float, vp, vp, vp,
                                             vp], i),
+            "mfh_net_eval_device_moves_left": ([vp, i, vp, vp, vp, vp, vp, vp], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -140,7 +142,8 @@ class HipNetwork:
 
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
-                 device=-1, precision="bf16x2", weights_dtype="bf16", net_format=None):
+                 device=-1, precision="bf16x2", weights_dtype="bf16", net_format=None,
+                 moves_left=False):
         """``net_format``: NetworkFormat fields of a loaded file
         (``WeightsFile.format``); they replace the description the keyword
         arguments give."""
@@ -152,7 +155,8 @@ class HipNetwork:
         for j, n in enumerate(names):
             a = self._weights[n]
             tensors[j] = MfhTensor(self._names[j], a.ctypes.data, a.size)
-        desc = MfhNetDesc(network=6, policy=3, value=2 if wdl else 1, moves_left=0,
+        desc = MfhNetDesc(network=6, policy=3, value=2 if wdl else 1,
+                          moves_left=1 if moves_left else 0,
                           input_embedding=2,
                           default_activation=1 if default_activation == "mish" else 0,
                           ffn_activation=ACTIVATION[ffn_activation],
@@ -164,12 +168,14 @@ class HipNetwork:
                       "default_activation", "ffn_activation", "smolgen_activation"):
                 setattr(desc, k, int(net_format[k]))
             wdl = net_format["value"] == 2
+            moves_left = net_format["moves_left"] == 1
         handle = ctypes.c_void_p()
         self._h = None
         _check(lib().mfh_net_create(ctypes.byref(desc), tensors, len(names),
                                     ctypes.byref(handle)), "mfh_net_create")
         self._h = handle
         self.wdl = wdl
+        self.moves_left = bool(moves_left)
         self.max_batch = max_batch
         self.precision = precision
         self.weights_dtype = weights_dtype
@@ -205,30 +211,35 @@ class HipNetwork:
         return (np.zeros((b, 1858), np.float32),
                 np.zeros((b, 3 if self.wdl else 1), np.float32))
 
-    def eval_packed(self, masks, values):
-        """Raw outputs (policy [B,1858], wdl [B,3] or value [B,1]) for packed
-        inputs, chunked by max_batch."""
+    def eval_packed(self, masks, values, with_moves_left=False):
+        """Raw outputs (policy [B,1858], wdl [B,3] or value [B,1], and with
+        ``with_moves_left`` the moves-left output [B]) for packed inputs,
+        chunked by max_batch."""
         masks = np.ascontiguousarray(masks, dtype=np.uint64).reshape(-1, 112)
         values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1, 112)
         b = masks.shape[0]
         policy, value = self._outputs(b)
+        ml = np.zeros(b, np.float32) if with_moves_left else None
         for s in range(0, b, self.max_batch):
             e = min(b, s + self.max_batch)
             _check(lib().mfh_net_eval(self._h, e - s, _ptr(masks[s:e]), _ptr(values[s:e]),
-                                      _ptr(policy[s:e]), _ptr(value[s:e]), None),
+                                      _ptr(policy[s:e]), _ptr(value[s:e]),
+                                      None if ml is None else _ptr(ml[s:e])),
                    "mfh_net_eval")
-        return policy, value
+        return (policy, value, ml) if with_moves_left else (policy, value)
 
-    def eval_planes(self, planes):
+    def eval_planes(self, planes, with_moves_left=False):
         planes = np.ascontiguousarray(planes, dtype=np.float32).reshape(-1, 112, 64)
         b = planes.shape[0]
         policy, value = self._outputs(b)
+        ml = np.zeros(b, np.float32) if with_moves_left else None
         for s in range(0, b, self.max_batch):
             e = min(b, s + self.max_batch)
             _check(lib().mfh_net_eval_planes(self._h, e - s, _ptr(planes[s:e]),
-                                             _ptr(policy[s:e]), _ptr(value[s:e]), None),
+                                             _ptr(policy[s:e]), _ptr(value[s:e]),
+                                             None if ml is None else _ptr(ml[s:e])),
                    "mfh_net_eval_planes")
-        return policy, value
+        return (policy, value, ml) if with_moves_left else (policy, value)
 
     def eval_priors(self, masks, values, moves, softmax_temp=1.0):
         """MCTS priors of each position's legal moves, computed on the device
@@ -267,11 +278,16 @@ class HipNetwork:
 
     def evaluate_batch(self, planes):
         """NetworkOutput fields for planes [B,112,64] (EvaluateBatch)."""
-        policy, raw = self.eval_planes(planes)
+        res = self.eval_planes(planes, with_moves_left=self.moves_left)
+        policy, raw = res[0], res[1]
         if self.wdl:
-            return {"policy": policy, "wdl": raw, "value": raw[:, 0] - raw[:, 2]}
-        return {"policy": policy, "wdl": np.zeros((raw.shape[0], 3), np.float32),
-                "value": raw[:, 0]}
+            out = {"policy": policy, "wdl": raw, "value": raw[:, 0] - raw[:, 2]}
+        else:
+            out = {"policy": policy, "wdl": np.zeros((raw.shape[0], 3), np.float32),
+                   "value": raw[:, 0]}
+        if self.moves_left:
+            out["moves_left"] = res[2]
+        return out
 
     def evaluate(self, planes):
         out = self.evaluate_batch(np.asarray(planes).reshape(1, 112, 64))
@@ -359,7 +375,7 @@ def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
     "bf16x2" (split activations, default: meets every parity gate),
     "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput);
     ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales)."""
-    return HipNetwork(weights, spec.heads, wdl=spec.wdl,
+    return HipNetwork(weights, spec.heads, wdl=spec.wdl, moves_left=spec.moves_left_dim > 0,
                       default_activation=spec.default_activation,
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,

@@ -150,7 +150,8 @@ struct Dims {
   int E = 0, H = 0, L = 0, F = 0, P = 0, Kin = 0, Fi = 0;
   int C = 0, Hs = 0, HG = 0, G = 0;
   int Dp = 0, Vd = 0, Vh = 0, Vout = 0;
-  bool gates = false, input_ffn = false, smolgen = false, wdl = true;
+  int Md = 0, Mh = 0;  // moves-left head: square embedding, hidden width
+  bool gates = false, input_ffn = false, smolgen = false, wdl = true, mlh = false;
   bool split = false;       // lo planes on dense-layer inputs (BF16X2, BF16X2_GEMM)
   bool split_attn = false;  // lo planes on attention / smolgen operands (BF16X2)
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
@@ -184,6 +185,8 @@ struct mfh_net {
   std::vector<Layer> layers;
   size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
   size_t head_w[2], qk_w[2], val1_w[2];
+  size_t mov_b = 0, mov1_b = 0, mov2_w = 0, mov2_b = 0;  // moves-left head
+  size_t mov_w[2] = {0, 0}, mov1_w[2] = {0, 0};
 
   unsigned char *ws = nullptr;
   size_t ws_bytes = 0;
@@ -209,10 +212,10 @@ struct mfh_net {
   // runs eagerly once before it is captured.
   struct GraphKey {
     int batch;
-    const void *masks, *values, *policy, *wdl;
+    const void *masks, *values, *policy, *wdl, *moves_left;
     bool operator<(const GraphKey &o) const {
-      return std::tie(batch, masks, values, policy, wdl) <
-             std::tie(o.batch, o.masks, o.values, o.policy, o.wdl);
+      return std::tie(batch, masks, values, policy, wdl, moves_left) <
+             std::tie(o.batch, o.masks, o.values, o.policy, o.wdl, o.moves_left);
     }
   };
   bool graphs = true;
@@ -337,8 +340,8 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
     return SetError(MFH_ERR_UNSUPPORTED, "HIP backend supports the attention policy head only");
   if (desc.value != MFH_VALUE_WDL && desc.value != MFH_VALUE_CLASSICAL)
     return SetError(MFH_ERR_UNSUPPORTED, "HIP backend supports WDL or classical value heads");
-  if (desc.moves_left)
-    return SetError(MFH_ERR_UNSUPPORTED, "HIP backend has no moves-left head yet");
+  if (desc.moves_left != 0 && desc.moves_left != 1)
+    return SetError(MFH_ERR_UNSUPPORTED, "unknown moves-left format (MOVES_LEFT_V1 or none)");
   if (desc.input_embedding != MFH_INPUT_EMBEDDING_PE_DENSE)
     return SetError(MFH_ERR_UNSUPPORTED,
                     "HIP backend supports INPUT_EMBEDDING_PE_DENSE only (as the reference CPU backend)");
@@ -350,6 +353,7 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   d.split = desc.precision != MFH_PRECISION_BF16;
   d.split_attn = desc.precision == MFH_PRECISION_BF16X2;
   d.wdl = desc.value == MFH_VALUE_WDL;
+  d.mlh = desc.moves_left == 1;
   d.act_default = desc.default_activation == MFH_DEFAULT_ACTIVATION_MISH ? mfh::ACT_MISH
                                                                          : mfh::ACT_RELU;
   d.act_ffn = ActFromProto(desc.ffn_activation, d.act_default);
@@ -379,6 +383,12 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   d.Vd = static_cast<int>(ld.Count("value.winner.ip_val_b"));
   d.Vh = static_cast<int>(ld.Count("value.winner.ip1_val_b"));
   d.Vout = static_cast<int>(ld.Count("value.winner.ip2_val_b"));
+  int mout = 0;
+  if (d.mlh) {
+    d.Md = static_cast<int>(ld.Count("moves_left.ip_mov_b"));
+    d.Mh = static_cast<int>(ld.Count("moves_left.ip1_mov_b"));
+    mout = static_cast<int>(ld.Count("moves_left.ip2_mov_b"));
+  }
   d.Kin = static_cast<int>(AlignUp(kPlanes + d.P, 64));
 
   std::ostringstream why;
@@ -405,8 +415,11 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
     why << "body.ip_emb_ln is required; ";
   if (ld.Count("policy.vanilla.encoder.0.mha.q_b") || ld.Count("policy.vanilla.ip_pol_b") == 0)
     why << "policy head must be ip_pol/ip2_pol/ip3_pol/ip4_pol without encoder layers; ";
-  if (ld.Count("value.winner.ip_val_err_b"))
-    why << "value-error head is not supported; ";
+  // The value-error head (value.winner.ip_val_err_*) feeds no NetworkOutput
+  // field (reference network_output_decoder.cpp:31-78), so it is accepted and
+  // not computed.
+  if (d.mlh && (d.Md <= 0 || d.Mh <= 0 || mout != 1 || ld.Count("moves_left.weights")))
+    why << "moves-left head needs ip_mov, ip1_mov and ip2_mov (one output), no convolution; ";
   const std::string w = why.str();
   if (!w.empty())
     return SetError(MFH_ERR_UNSUPPORTED, "HIP backend cannot run this net: " + w);
@@ -541,8 +554,26 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   const float *v1b = need(vp + "ip1_val_b", d.Vh);
   const float *v2w = need(vp + "ip2_val_w", static_cast<size_t>(d.Vout) * d.Vh);
   const float *v2b = need(vp + "ip2_val_b", d.Vout);
+  const float *mw = nullptr, *mb = nullptr, *m1w = nullptr, *m1b = nullptr, *m2w = nullptr,
+              *m2b = nullptr;
+  if (d.mlh) {
+    mw = need("moves_left.ip_mov_w", static_cast<size_t>(d.Md) * E);
+    mb = need("moves_left.ip_mov_b", d.Md);
+    m1w = need("moves_left.ip1_mov_w", static_cast<size_t>(d.Mh) * S * d.Md);
+    m1b = need("moves_left.ip1_mov_b", d.Mh);
+    m2w = need("moves_left.ip2_mov_w", d.Mh);
+    m2b = need("moves_left.ip2_mov_b", 1);
+  }
   if (!ld.error.empty())
     return SetError(MFH_ERR_INVALID, ld.error);
+  if (d.mlh) {
+    SetW(net->mov_w, AddGemmW(blob, net->fp8, {mw}, {d.Md}, E, E));
+    net->mov_b = AddF32(blob, {mb}, {d.Md});
+    SetW(net->mov1_w, AddGemmW(blob, net->fp8, {m1w}, {d.Mh}, S * d.Md, S * d.Md));
+    net->mov1_b = AddF32(blob, {m1b}, {d.Mh});
+    net->mov2_w = AddF32(blob, {m2w}, {d.Mh});
+    net->mov2_b = AddF32(blob, {m2b}, {1});
+  }
   SetW(net->head_w, AddGemmW(blob, net->fp8, {pw, vw}, {d.Dp, d.Vd}, E, E));
   net->head_b = AddF32(blob, {pb, vb}, {d.Dp, d.Vd});
   SetW(net->qk_w, AddGemmW(blob, net->fp8, {q2w, k3w}, {d.Dp, d.Dp}, d.Dp, d.Dp));
@@ -618,6 +649,9 @@ void PlanWorkspace(mfh_net *net) {
   add16("val_emb", M * d.Vd);
   add16("polqk", M * 2 * d.Dp);
   add("val1", skv * B * d.Vh * 4);
+  add16("mov_emb", M * (d.Md ? d.Md : 1));
+  add("mov1", (d.mlh ? SplitK(kSquares * d.Md) : 1) * B * (d.Mh ? d.Mh : 1) * 4);
+  add("mlh", B * 4);
   // Split-K partials of small-batch GEMMs.
   add("splitk", kSplitKFloats * 4);
   add("policy", B * kPolicy * 4);
@@ -689,7 +723,7 @@ std::string GemmKind(const mfh::GemmParams &p, const char *role) {
 }
 
 int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
-            float *policy, float *wdl, hipStream_t st) {
+            float *policy, float *wdl, float *moves_left, hipStream_t st) {
   const Dims &d = net->d;
   const int M = B * kSquares;
   const int E = d.E;
@@ -919,10 +953,33 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
                             mfh::ACT_NONE, mfh::GEMM_OUT_F32, val1, nullptr, d.Vh);
   pv.k_splits = SplitK(vflat);
   MFH_RUN(run(pv, "value_dense1"));
-  StageTimer tv(net, st, "value_head", 0.0, 4.0 * pv.k_splits * B * d.Vh);
-  MFH_RUN(mfh::LaunchValueHead(val1, pv.k_splits, net->W<float>(net->val1_b), d.act_default, B,
-                               d.Vh, net->W<float>(net->val2_w), net->W<float>(net->val2_b),
-                               d.wdl ? 1 : 0, wdl, st, &err_));
+  {
+    StageTimer tv(net, st, "value_head", 0.0, 4.0 * pv.k_splits * B * d.Vh);
+    MFH_RUN(mfh::LaunchValueHead(val1, pv.k_splits, net->W<float>(net->val1_b), d.act_default,
+                                 B, d.Vh, net->W<float>(net->val2_w),
+                                 net->W<float>(net->val2_b),
+                                 d.wdl ? mfh::kHeadSoftmax3 : mfh::kHeadTanh, wdl, st, &err_));
+  }
+  if (d.mlh) {
+    // Moves-left head (reference network_execution_plan.cpp:184-190, acts
+    // 1107-1111): ip_mov on square rows (default activation), flatten,
+    // ip1_mov (default activation), ip2_mov + relu.
+    MFH_RUN(run(gemm("act", E, net->mov_w, E, M, d.Md, E, net->W<float>(net->mov_b),
+                     d.act_default, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("mov_emb"),
+                     net->Lo("mov_emb"), d.Md),
+                "moves_left"));
+    const int mflat = kSquares * d.Md;
+    auto *mov1 = net->S<float>("mov1");
+    mfh::GemmParams pm = gemm("mov_emb", mflat, net->mov1_w, mflat, B, d.Mh, mflat, nullptr,
+                              mfh::ACT_NONE, mfh::GEMM_OUT_F32, mov1, nullptr, d.Mh);
+    pm.k_splits = SplitK(mflat);
+    MFH_RUN(run(pm, "moves_left_dense1"));
+    StageTimer tm(net, st, "moves_left_head", 0.0, 4.0 * pm.k_splits * B * d.Mh);
+    MFH_RUN(mfh::LaunchValueHead(mov1, pm.k_splits, net->W<float>(net->mov1_b), d.act_default,
+                                 B, d.Mh, net->W<float>(net->mov2_w),
+                                 net->W<float>(net->mov2_b), mfh::kHeadRelu, moves_left, st,
+                                 &err_));
+  }
 #undef MFH_RUN
   return MFH_OK;
 }
@@ -978,21 +1035,21 @@ void DropGraphs(mfh_net *net) {
 // launched on `st`), or eagerly while profiling, for a key's first run, or
 // when graphs are off.  A graph bakes in the batch size and the buffers.
 int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
-               float *policy, float *wdl, hipStream_t st) {
+               float *policy, float *wdl, float *moves_left, hipStream_t st) {
   if (!net->graphs || net->profiling)
-    return Forward(net, B, masks, values, policy, wdl, st);
-  const mfh_net::GraphKey key{B, masks, values, policy, wdl};
+    return Forward(net, B, masks, values, policy, wdl, moves_left, st);
+  const mfh_net::GraphKey key{B, masks, values, policy, wdl, moves_left};
   auto it = net->graph_execs.find(key);
   if (it == net->graph_execs.end()) {
     if (!net->graph_warm.count(key)) {
       net->graph_warm.insert(key);
-      return Forward(net, B, masks, values, policy, wdl, st);
+      return Forward(net, B, masks, values, policy, wdl, moves_left, st);
     }
     if (net->graph_execs.size() >= 64)
       DropGraphs(net);
     hipGraph_t graph = nullptr;
     MFH_HIP_CHECK(hipStreamBeginCapture(net->capture_stream, hipStreamCaptureModeThreadLocal));
-    const int rc = Forward(net, B, masks, values, policy, wdl, net->capture_stream);
+    const int rc = Forward(net, B, masks, values, policy, wdl, moves_left, net->capture_stream);
     const hipError_t end = hipStreamEndCapture(net->capture_stream, &graph);
     if (rc != MFH_OK || end != hipSuccess || !graph) {
       if (graph)
@@ -1000,7 +1057,7 @@ int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *val
       (void)hipGetLastError();
       // Capture is not available here: stay eager from now on.
       net->graphs = false;
-      return rc != MFH_OK ? rc : Forward(net, B, masks, values, policy, wdl, st);
+      return rc != MFH_OK ? rc : Forward(net, B, masks, values, policy, wdl, moves_left, st);
     }
     hipGraphExec_t exec = nullptr;
     const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
@@ -1008,12 +1065,19 @@ int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *val
     if (inst != hipSuccess) {
       (void)hipGetLastError();
       net->graphs = false;
-      return Forward(net, B, masks, values, policy, wdl, st);
+      return Forward(net, B, masks, values, policy, wdl, moves_left, st);
     }
     it = net->graph_execs.emplace(key, exec).first;
   }
   MFH_HIP_CHECK(hipGraphLaunch(it->second, st));
   return MFH_OK;
+}
+
+// Pinned output layout: policy [max_batch][1858] (or the priors), value head
+// [max_batch][3], moves left [max_batch].
+float *PinMovesLeft(mfh_net *net) {
+  return reinterpret_cast<float *>(net->pin_out) +
+         static_cast<size_t>(net->max_batch) * (kPolicy + 3);
 }
 
 int RunStaged(mfh_net *net, int batch) {
@@ -1028,7 +1092,7 @@ int RunStaged(mfh_net *net, int batch) {
   MFH_HIP_CHECK(hipSetDevice(net->device));
   MFH_HIP_CHECK(hipMemcpyAsync(d_masks, pin_masks, n_in * 8, hipMemcpyHostToDevice, net->stream));
   MFH_HIP_CHECK(hipMemcpyAsync(d_values, pin_values, n_in * 4, hipMemcpyHostToDevice, net->stream));
-  const int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->stream);
+  const int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), net->stream);
   if (rc != MFH_OK) {
     (void)hipStreamSynchronize(net->stream);
     return rc;
@@ -1039,6 +1103,10 @@ int RunStaged(mfh_net *net, int batch) {
                                hipMemcpyDeviceToHost, net->stream));
   MFH_HIP_CHECK(hipMemcpyAsync(pin_value, d_wdl, static_cast<size_t>(batch) * net->d.Vout * 4,
                                hipMemcpyDeviceToHost, net->stream));
+  if (net->d.mlh)
+    MFH_HIP_CHECK(hipMemcpyAsync(PinMovesLeft(net), net->S<float>("mlh"),
+                                 static_cast<size_t>(batch) * 4, hipMemcpyDeviceToHost,
+                                 net->stream));
   MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
   net->last_batch = batch;
   return MFH_OK;
@@ -1078,7 +1146,7 @@ int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
     MFH_HIP_CHECK(hipMemcpyAsync(d_indices, pin + PinMovesOffset(net->max_batch),
                                  static_cast<size_t>(total_moves) * 2, hipMemcpyHostToDevice,
                                  net->stream));
-  int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->stream);
+  int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), net->stream);
   if (rc == MFH_OK) {
     std::string err;
     if (mfh::LaunchPolicyPriors(d_policy, d_offsets, d_indices, batch, inv_temp, d_priors,
@@ -1096,6 +1164,10 @@ int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
                                  hipMemcpyDeviceToHost, net->stream));
   MFH_HIP_CHECK(hipMemcpyAsync(pin_value, d_wdl, static_cast<size_t>(batch) * net->d.Vout * 4,
                                hipMemcpyDeviceToHost, net->stream));
+  if (net->d.mlh)
+    MFH_HIP_CHECK(hipMemcpyAsync(PinMovesLeft(net), net->S<float>("mlh"),
+                                 static_cast<size_t>(batch) * 4, hipMemcpyDeviceToHost,
+                                 net->stream));
   MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
   net->last_batch = batch;
   return MFH_OK;
@@ -1119,13 +1191,22 @@ int CheckMoves(int batch, const std::int32_t *offsets, int *total) {
   return MFH_OK;
 }
 
-int CopyOut(mfh_net *net, int batch, float *policy, float *wdl) {
+int CopyOut(mfh_net *net, int batch, float *policy, float *wdl, float *moves_left) {
   const auto *pin_policy = reinterpret_cast<const float *>(net->pin_out);
   const auto *pin_value = pin_policy + static_cast<size_t>(net->max_batch) * kPolicy;
   if (policy)
     std::memcpy(policy, pin_policy, static_cast<size_t>(batch) * kPolicy * 4);
   if (wdl)
     std::memcpy(wdl, pin_value, static_cast<size_t>(batch) * net->d.Vout * 4);
+  if (moves_left)
+    std::memcpy(moves_left, PinMovesLeft(net), static_cast<size_t>(batch) * 4);
+  return MFH_OK;
+}
+
+// moves_left may be requested only from a net with a moves-left head.
+int CheckMovesLeftOut(const mfh_net *net, const float *moves_left, const char *fn) {
+  if (moves_left && !net->d.mlh)
+    return SetError(MFH_ERR_INVALID, std::string(fn) + ": the net has no moves-left head");
   return MFH_OK;
 }
 
@@ -1217,7 +1298,7 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
   }
   const size_t in_bytes = PinMovesOffset(net->max_batch) +
                           static_cast<size_t>(net->max_batch) * kMaxMoves * 2;
-  const size_t out_bytes = static_cast<size_t>(net->max_batch) * (kPolicy + 3) * 4;
+  const size_t out_bytes = static_cast<size_t>(net->max_batch) * (kPolicy + 3 + 1) * 4;
   if (hipHostMalloc(reinterpret_cast<void **>(&net->pin_in), in_bytes, hipHostMallocDefault) !=
           hipSuccess ||
       hipHostMalloc(reinterpret_cast<void **>(&net->pin_out), out_bytes,
@@ -1259,8 +1340,11 @@ int mfh_net_eval(mfh_net *net, int batch, const uint64_t *masks, const float *va
   int rc = CheckBatch(net, batch);
   if (rc != MFH_OK)
     return rc;
-  if (!masks || !values || !policy || !wdl || moves_left)
+  if (!masks || !values || !policy || !wdl)
     return SetError(MFH_ERR_INVALID, "mfh_net_eval: bad output/input pointers");
+  rc = CheckMovesLeftOut(net, moves_left, "mfh_net_eval");
+  if (rc != MFH_OK)
+    return rc;
   std::lock_guard<std::mutex> lock(net->mu);
   const size_t n_in = static_cast<size_t>(batch) * kPlanes;
   std::memcpy(net->pin_in, masks, n_in * 8);
@@ -1268,7 +1352,7 @@ int mfh_net_eval(mfh_net *net, int batch, const uint64_t *masks, const float *va
   rc = RunStaged(net, batch);
   if (rc != MFH_OK)
     return rc;
-  return CopyOut(net, batch, policy, wdl);
+  return CopyOut(net, batch, policy, wdl, moves_left);
 }
 
 int mfh_net_eval_planes(mfh_net *net, int batch, const float *planes, float *policy,
@@ -1276,8 +1360,11 @@ int mfh_net_eval_planes(mfh_net *net, int batch, const float *planes, float *pol
   int rc = CheckBatch(net, batch);
   if (rc != MFH_OK)
     return rc;
-  if (!planes || !policy || !wdl || moves_left)
+  if (!planes || !policy || !wdl)
     return SetError(MFH_ERR_INVALID, "mfh_net_eval_planes: bad output/input pointers");
+  rc = CheckMovesLeftOut(net, moves_left, "mfh_net_eval_planes");
+  if (rc != MFH_OK)
+    return rc;
   std::lock_guard<std::mutex> lock(net->mu);
   PackPlanes(planes, batch, reinterpret_cast<std::uint64_t *>(net->pin_in),
              reinterpret_cast<float *>(net->pin_in +
@@ -1285,7 +1372,7 @@ int mfh_net_eval_planes(mfh_net *net, int batch, const float *planes, float *pol
   rc = RunStaged(net, batch);
   if (rc != MFH_OK)
     return rc;
-  return CopyOut(net, batch, policy, wdl);
+  return CopyOut(net, batch, policy, wdl, moves_left);
 }
 
 int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
@@ -1298,7 +1385,27 @@ int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
   std::lock_guard<std::mutex> lock(net->mu);
   MFH_HIP_CHECK(hipSetDevice(net->device));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, st);
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), st);
+  if (rc == MFH_OK)
+    net->last_batch = batch;
+  return rc;
+}
+
+int mfh_net_eval_device_moves_left(mfh_net *net, int batch, const uint64_t *d_masks,
+                                   const float *d_values, float *d_policy, float *d_wdl,
+                                   float *d_moves_left, void *stream) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (!d_masks || !d_values || !d_policy || !d_wdl || !d_moves_left)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_device_moves_left: null pointer");
+  rc = CheckMovesLeftOut(net, d_moves_left, "mfh_net_eval_device_moves_left");
+  if (rc != MFH_OK)
+    return rc;
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, d_moves_left,
+                  static_cast<hipStream_t>(stream));
   if (rc == MFH_OK)
     net->last_batch = batch;
   return rc;
@@ -1310,8 +1417,11 @@ int mfh_net_eval_priors(mfh_net *net, int batch, const uint64_t *masks, const fl
   int rc = CheckBatch(net, batch);
   if (rc != MFH_OK)
     return rc;
-  if (!masks || !values || !wdl || moves_left)
+  if (!masks || !values || !wdl)
     return SetError(MFH_ERR_INVALID, "mfh_net_eval_priors: bad output/input pointers");
+  rc = CheckMovesLeftOut(net, moves_left, "mfh_net_eval_priors");
+  if (rc != MFH_OK)
+    return rc;
   int total = 0;
   rc = CheckMoves(batch, move_offsets, &total);
   if (rc != MFH_OK)
@@ -1336,6 +1446,8 @@ int mfh_net_eval_priors(mfh_net *net, int batch, const uint64_t *masks, const fl
   if (total > 0)
     std::memcpy(priors, pin_priors, static_cast<size_t>(total) * 4);
   std::memcpy(wdl, pin_priors + mb * kPolicy, static_cast<size_t>(batch) * net->d.Vout * 4);
+  if (moves_left)
+    std::memcpy(moves_left, PinMovesLeft(net), static_cast<size_t>(batch) * 4);
   return MFH_OK;
 }
 
@@ -1352,7 +1464,7 @@ int mfh_net_eval_priors_device(mfh_net *net, int batch, const uint64_t *d_masks,
   std::lock_guard<std::mutex> lock(net->mu);
   MFH_HIP_CHECK(hipSetDevice(net->device));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, st);
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), st);
   if (rc != MFH_OK)
     return rc;
   std::string err;
@@ -1374,7 +1486,10 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
   if (d.smolgen)
     o << " smolgen C=" << d.C << "/" << d.Hs << "/" << d.G;
   o << ", policy attention Dp=" << d.Dp << ", value " << (d.wdl ? "wdl" : "scalar") << " "
-    << d.Vd << "/" << d.Vh << ", activations " << ActName(d.act_default) << "/"
+    << d.Vd << "/" << d.Vh;
+  if (d.mlh)
+    o << ", moves left " << d.Md << "/" << d.Mh;
+  o << ", activations " << ActName(d.act_default) << "/"
     << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", precision "
     << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : "bf16") << ", weights bf16 "
     << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
@@ -1389,7 +1504,7 @@ int mfh_net_capabilities(const mfh_net *net, mfh_capabilities *out) {
     return SetError(MFH_ERR_INVALID, "mfh_net_capabilities: null argument");
   std::memset(out, 0, sizeof(*out));
   out->has_wdl = net->d.wdl ? 1 : 0;
-  out->has_moves_left = 0;
+  out->has_moves_left = net->d.mlh ? 1 : 0;
   out->max_batch_size = net->max_batch;
   out->device = net->device;
   std::snprintf(out->device_name, sizeof(out->device_name), "%s", net->device_name.c_str());

@@ -154,11 +154,13 @@ hipError_t LaunchPolicyPriors(const float *policy, const std::int32_t *offsets,
                               const std::int16_t *indices, int batch, float inv_temp,
                               float *priors, hipStream_t stream, std::string *err);
 
-// Value head output: hidden = act(sum of `parts` partials [parts][B][vh] + b1)
-// then dense2 + softmax (WDL, 3 outputs) or tanh (scalar, 1 output).
+// Value / moves-left head output: hidden = act(sum of `parts` partials
+// [parts][B][vh] + b1), then dense2 and the output function: tanh (scalar
+// value, 1 output), softmax (WDL, 3 outputs) or relu (moves left, 1 output).
+enum { kHeadTanh = 0, kHeadSoftmax3 = 1, kHeadRelu = 2 };
 hipError_t LaunchValueHead(const float *hidden, int parts, const float *b1,
                            int act, int batch, int vh, const float *w2,
-                           const float *b2, int wdl, float *out,
+                           const float *b2, int mode, float *out,
                            hipStream_t stream, std::string *err);
 
 }  // namespace mfh

@@ -203,13 +203,13 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
 // (reference network_execution_plan.cpp:1098-1106, cpu_network.cpp:336-351).
 __global__ __launch_bounds__(256) void ValueHeadKernel(
     const float *__restrict__ hidden, int parts, const float *__restrict__ b1, int act,
-    int batch, int vh, const float *__restrict__ w2, const float *__restrict__ b2, int wdl,
+    int batch, int vh, const float *__restrict__ w2, const float *__restrict__ b2, int mode,
     float *__restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= batch)
     return;
-  const int outs = wdl ? 3 : 1;
+  const int outs = mode == kHeadSoftmax3 ? 3 : 1;
   const float *h = hidden + static_cast<size_t>(b) * vh;
   float acc[3] = {0.f, 0.f, 0.f};
   const size_t plane = static_cast<size_t>(batch) * vh;
@@ -227,13 +227,15 @@ __global__ __launch_bounds__(256) void ValueHeadKernel(
     acc[o] = wave_sum(acc[o]) + b2[o];
   if (lane != 0)
     return;
-  if (wdl) {
+  if (mode == kHeadSoftmax3) {
     const float m = fmaxf(acc[0], fmaxf(acc[1], acc[2]));
     const float e0 = expf(acc[0] - m), e1 = expf(acc[1] - m), e2 = expf(acc[2] - m);
     const float inv = 1.f / (e0 + e1 + e2);
     out[static_cast<size_t>(b) * 3 + 0] = e0 * inv;
     out[static_cast<size_t>(b) * 3 + 1] = e1 * inv;
     out[static_cast<size_t>(b) * 3 + 2] = e2 * inv;
+  } else if (mode == kHeadRelu) {
+    out[b] = activate(acc[0], ACT_RELU);
   } else {
     out[b] = tanhf(acc[0]);
   }
@@ -334,14 +336,15 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
 }
 
 hipError_t LaunchValueHead(const float *hidden, int parts, const float *b1, int act,
-                           int batch, int vh, const float *w2, const float *b2, int wdl,
+                           int batch, int vh, const float *w2, const float *b2, int mode,
                            float *out, hipStream_t stream, std::string *err) {
-  if (batch <= 0 || vh <= 0 || parts < 1 || !hidden || !w2 || !b2 || !out) {
+  if (batch <= 0 || vh <= 0 || parts < 1 || !hidden || !w2 || !b2 || !out ||
+      (mode != kHeadTanh && mode != kHeadSoftmax3 && mode != kHeadRelu)) {
     Fail(err, "value_head: invalid arguments");
     return hipErrorInvalidValue;
   }
   hipLaunchKernelGGL(ValueHeadKernel, dim3((batch + 3) / 4), dim3(256), 0, stream, hidden,
-                     parts, b1, act, batch, vh, w2, b2, wdl, out);
+                     parts, b1, act, batch, vh, w2, b2, mode, out);
   return hipGetLastError();
 }
 

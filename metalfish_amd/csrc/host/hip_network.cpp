@@ -93,7 +93,9 @@ void HipNetwork::Create(mfh_net_desc desc, const mfh_tensor *tensors, int count)
   if (rc != MFH_OK)
     throw std::runtime_error(LastError("initialisation", rc));
   wdl_ = desc.value == MFH_VALUE_WDL;
+  mlh_ = desc.moves_left == MFH_MOVES_LEFT_V1;
   max_batch_ = desc.max_batch;
+  moves_.resize(static_cast<std::size_t>(max_batch_));
   policy_.resize(static_cast<std::size_t>(max_batch_) * kPolicyOutputs);
   value_.resize(static_cast<std::size_t>(max_batch_) * 3);
 }
@@ -105,7 +107,8 @@ void HipNetwork::RunChunk(const InputPlanes *inputs, int count, NetworkOutput *o
   // planes[count*112*64] layout the C ABI takes.
   const float *planes = inputs[0][0].data();
   for (int attempt = 0; attempt < 2; ++attempt) {
-    const int rc = mfh_net_eval_planes(net_, count, planes, policy_.data(), value_.data(), nullptr);
+    const int rc = mfh_net_eval_planes(net_, count, planes, policy_.data(), value_.data(),
+                                       mlh_ ? moves_.data() : nullptr);
     if (rc != MFH_OK) {
       if (attempt == 0)
         continue;
@@ -137,8 +140,8 @@ void HipNetwork::RunChunk(const InputPlanes *inputs, int count, NetworkOutput *o
       out.value = value_[b];
       out.wdl[0] = out.wdl[1] = out.wdl[2] = 0.0f;
     }
-    out.has_moves_left = false;
-    out.moves_left = 0.0f;
+    out.has_moves_left = mlh_;
+    out.moves_left = mlh_ ? moves_[b] : 0.0f;
   }
 }
 
@@ -181,7 +184,8 @@ std::vector<PriorsOutput> HipNetwork::EvaluateBatchPriors(
     priors.resize(flat.size());
     if (rc == MFH_OK)
       rc = mfh_net_eval_priors(net_, count, masks_.data(), values_.data(), offsets.data(),
-                               flat.data(), softmax_temp, priors.data(), value_.data(), nullptr);
+                               flat.data(), softmax_temp, priors.data(), value_.data(),
+                               mlh_ ? moves_.data() : nullptr);
     if (rc != MFH_OK)
       throw std::runtime_error(LastError("priors evaluation", rc));
     for (int b = 0; b < count; ++b) {
@@ -195,6 +199,8 @@ std::vector<PriorsOutput> HipNetwork::EvaluateBatchPriors(
       } else {
         out.value = value_[b];
       }
+      out.has_moves_left = mlh_;
+      out.moves_left = mlh_ ? moves_[b] : 0.0f;
     }
   }
   return outputs;

@@ -52,6 +52,8 @@ struct PriorsOutput {
   float value = 0.0f;
   float wdl[3] = {};
   bool has_wdl = false;
+  float moves_left = 0.0f;
+  bool has_moves_left = false;
 };
 
 class HipNetwork : public Network {
@@ -77,7 +79,7 @@ public:
       const std::vector<std::vector<std::int16_t>> &move_indices, float softmax_temp);
   std::string GetNetworkInfo() const override;
   bool HasWDL() const override { return wdl_; }
-  bool HasMovesLeft() const override { return false; }
+  bool HasMovesLeft() const override { return mlh_; }
   BackendCapabilities GetBackendCapabilities() const override;
 
 private:
@@ -86,6 +88,8 @@ private:
 
   mfh_net *net_ = nullptr;
   bool wdl_ = true;
+  bool mlh_ = false;
+  std::vector<float> moves_;
   int max_batch_ = 0;
   std::vector<float> policy_;
   std::vector<float> value_;

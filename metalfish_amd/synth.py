@@ -62,6 +62,8 @@ class NetSpec:
     policy_dim: int = 0
     value_dim: int = 32
     value_hidden: int = 128
+    moves_left_dim: int = 0      # moves-left head square embedding (0: no head)
+    moves_left_hidden: int = 128
     wdl: bool = True
     gates: bool = True
     default_activation: str = "mish"
@@ -75,6 +77,10 @@ SPECS = {
     # BT4-shape net.
     "bt4": NetSpec("bt4", 1024, 15, 32, 1536, input_ffn=1536, smolgen_compress=32,
                    smolgen_hidden=256, smolgen_gen=256, policy_dim=1024),
+    # Test net: config 1 plus a moves-left head (8-channel square embedding,
+    # 128 hidden, the Lc0 widths).
+    "cpu_plumbing_mlh": NetSpec("cpu_plumbing_mlh", 256, 2, 8, 512, input_ffn=512,
+                                policy_dim=256, moves_left_dim=8),
 }
 
 
@@ -148,6 +154,14 @@ def tensor_layout(spec: NetSpec):
     nout = 3 if spec.wdl else 1
     mat("value.winner.ip2_val_w", nout, vh, bf16=False)
     vec("value.winner.ip2_val_b", nout, vh)
+    if spec.moves_left_dim:
+        md, mh = spec.moves_left_dim, spec.moves_left_hidden
+        mat("moves_left.ip_mov_w", md, E)
+        vec("moves_left.ip_mov_b", md, E)
+        mat("moves_left.ip1_mov_w", mh, S * md)
+        vec("moves_left.ip1_mov_b", mh, S * md)
+        mat("moves_left.ip2_mov_w", 1, mh, bf16=False)
+        vec("moves_left.ip2_mov_b", 1, mh)
     return out
 
 

@@ -348,6 +348,51 @@ def test_mcts_priors_device_entry_and_errors():
     net.close()
 
 
+@pytest.mark.parametrize("precision,batch", [("bf16x2", 32), ("bf16", 32), ("bf16x2", 1)])
+def test_moves_left_head(precision, batch):
+    """Moves-left head (ip_mov on square rows, flatten, ip1_mov, ip2_mov +
+    relu; reference network_execution_plan.cpp:184-190, 1107-1111) against
+    the oracle, with the other outputs at the usual gates; the value-error
+    head is accepted and has no output."""
+    spec = synth.SPECS["cpu_plumbing_mlh"]
+    weights = synth.make_weights(spec, seed=0)
+    planes, legal = synth.playout_positions(32, seed=3)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads, moves_left=True),
+                           weights).evaluate_batch(planes)
+    assert np.count_nonzero(ref["moves_left"]) >= 4  # the relu is not always zero
+    extra = dict(weights)
+    extra["value.winner.ip_val_err_w"] = np.ones((1, spec.value_hidden), np.float32)
+    extra["value.winner.ip_val_err_b"] = np.ones(1, np.float32)
+    net = backend.create_network(spec, extra, max_batch=batch, precision=precision)
+    assert net.capabilities()["has_moves_left"]
+    out = net.evaluate_batch(planes)
+    tol = 1e-3 if precision == "bf16x2" else 5e-3
+    assert np.abs(out["moves_left"] - ref["moves_left"]).max() <= tol
+    assert np.abs(out["policy"] - ref["policy"]).max() <= 2e-2
+    assert np.abs(out["wdl"] - ref["wdl"]).max() <= 5e-3
+    # Device entry with an explicit moves-left output equals the host path.
+    dev = _DeviceBuffers()
+    masks, values = backend.pack_planes(planes[:batch])
+    pol = np.zeros((batch, 1858), np.float32)
+    wdl = np.zeros((batch, 3), np.float32)
+    ml = np.zeros(batch, np.float32)
+    d_ml = dev.put(ml)
+    _check_ok = backend.lib().mfh_net_eval_device_moves_left(
+        net._h, batch, dev.put(masks), dev.put(values), dev.put(pol), dev.put(wdl), d_ml, None)
+    assert _check_ok == backend.MFH_OK
+    got = dev.get(d_ml, ml)
+    assert np.array_equal(got.view(np.uint32), out["moves_left"][:batch].view(np.uint32))
+    dev.free()
+    net.close()
+    # A net without the head rejects a moves-left output.
+    plain = backend.create_network(synth.SPECS["cpu_plumbing"],
+                                   synth.make_weights(synth.SPECS["cpu_plumbing"], seed=0),
+                                   max_batch=4)
+    with pytest.raises(RuntimeError, match="no moves-left head"):
+        plain.eval_planes(planes[:2], with_moves_left=True)
+    plain.close()
+
+
 def test_bad_batch_rejected():
     spec = synth.SPECS["cpu_plumbing"]
     net = backend.create_network(spec, synth.make_weights(spec), max_batch=4, device=0)
