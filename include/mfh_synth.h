@@ -64,6 +64,9 @@ int64_t mfs_perft(const char *fen, int depth);
 void mfs_policy_tables(int16_t *attention_map, int16_t *gather,
                        char *move_strings);
 
+/* The static position encoding of PE_MAP nets, out[64*64] ([square][channel]). */
+void mfs_static_position_encoding(float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,7 +40,7 @@ enum { MFH_NETWORK_ATTENTIONBODY_WITH_HEADFORMAT = 6,
 enum { MFH_POLICY_ATTENTION = 3 };
 enum { MFH_VALUE_CLASSICAL = 1, MFH_VALUE_WDL = 2 };
 /* NetworkFormat.InputEmbeddingFormat (net.proto:340-342). */
-enum { MFH_INPUT_EMBEDDING_PE_DENSE = 2 };
+enum { MFH_INPUT_EMBEDDING_PE_MAP = 1, MFH_INPUT_EMBEDDING_PE_DENSE = 2 };
 /* NetworkFormat.ActivationFunction (net.proto:317-326). */
 enum {
   MFH_ACTIVATION_DEFAULT = 0,
@@ -79,7 +79,7 @@ typedef struct {
   int policy;             /* MFH_POLICY_ATTENTION */
   int value;              /* MFH_VALUE_WDL or MFH_VALUE_CLASSICAL */
   int moves_left;         /* 0, or 1 (MOVES_LEFT_V1) for a moves-left head */
-  int input_embedding;    /* MFH_INPUT_EMBEDDING_PE_DENSE */
+  int input_embedding;    /* MFH_INPUT_EMBEDDING_PE_DENSE or _PE_MAP */
   int default_activation; /* MFH_DEFAULT_ACTIVATION_* */
   int ffn_activation;     /* MFH_ACTIVATION_*; DEFAULT follows default_activation */
   int smolgen_activation; /* MFH_ACTIVATION_*; DEFAULT follows default_activation */

@@ -143,7 +143,7 @@ class HipNetwork:
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
                  device=-1, precision="bf16x2", weights_dtype="bf16", net_format=None,
-                 moves_left=False):
+                 moves_left=False, pe_map=False):
         """``net_format``: NetworkFormat fields of a loaded file
         (``WeightsFile.format``); they replace the description the keyword
         arguments give."""
@@ -157,7 +157,7 @@ class HipNetwork:
             tensors[j] = MfhTensor(self._names[j], a.ctypes.data, a.size)
         desc = MfhNetDesc(network=6, policy=3, value=2 if wdl else 1,
                           moves_left=1 if moves_left else 0,
-                          input_embedding=2,
+                          input_embedding=1 if pe_map else 2,
                           default_activation=1 if default_activation == "mish" else 0,
                           ffn_activation=ACTIVATION[ffn_activation],
                           smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
@@ -376,6 +376,7 @@ def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
     "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput);
     ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales)."""
     return HipNetwork(weights, spec.heads, wdl=spec.wdl, moves_left=spec.moves_left_dim > 0,
+                      pe_map=spec.pe_map,
                       default_activation=spec.default_activation,
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,

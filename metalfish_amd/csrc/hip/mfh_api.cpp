@@ -152,6 +152,8 @@ struct Dims {
   int Dp = 0, Vd = 0, Vh = 0, Vout = 0;
   int Md = 0, Mh = 0;  // moves-left head: square embedding, hidden width
   bool gates = false, input_ffn = false, smolgen = false, wdl = true, mlh = false;
+  bool pe_map = false;  // static position encoding (INPUT_EMBEDDING_PE_MAP)
+  float eps_emb = 1e-3f;  // input-embedding LayerNorm
   bool split = false;       // lo planes on dense-layer inputs (BF16X2, BF16X2_GEMM)
   bool split_attn = false;  // lo planes on attention / smolgen operands (BF16X2)
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
@@ -180,6 +182,7 @@ struct mfh_net {
   // GEMM weights are {offset, fp8 row-scale offset} pairs.
   bool fp8 = false;
   size_t pre_b, emb_b, emb_ln_g, emb_ln_b, mult_gate, add_gate;
+  size_t static_pe = 0;  // PE_MAP table, fp32 [64][64]
   size_t pre_w[2], emb_w[2], in_ffn1_w[2], in_ffn2_w[2], global_w[2];
   size_t in_ffn1_b, in_ffn2_b, in_ln_g, in_ln_b;
   std::vector<Layer> layers;
@@ -342,9 +345,10 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
     return SetError(MFH_ERR_UNSUPPORTED, "HIP backend supports WDL or classical value heads");
   if (desc.moves_left != 0 && desc.moves_left != 1)
     return SetError(MFH_ERR_UNSUPPORTED, "unknown moves-left format (MOVES_LEFT_V1 or none)");
-  if (desc.input_embedding != MFH_INPUT_EMBEDDING_PE_DENSE)
+  if (desc.input_embedding != MFH_INPUT_EMBEDDING_PE_DENSE &&
+      desc.input_embedding != MFH_INPUT_EMBEDDING_PE_MAP)
     return SetError(MFH_ERR_UNSUPPORTED,
-                    "HIP backend supports INPUT_EMBEDDING_PE_DENSE only (as the reference CPU backend)");
+                    "HIP backend supports the PE_DENSE and PE_MAP input embeddings");
   if (desc.weights_dtype != MFH_WEIGHTS_BF16 && desc.weights_dtype != MFH_WEIGHTS_FP8)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
   if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2 &&
@@ -362,7 +366,11 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // Shapes follow from bias sizes, as in the reference's shape inference
   // (network_execution_plan.cpp:279-289).
   d.E = static_cast<int>(ld.Count("body.ip_emb_b"));
-  d.P = static_cast<int>(ld.Count("body.ip_emb_preproc_b")) / kSquares;
+  d.pe_map = desc.input_embedding == MFH_INPUT_EMBEDDING_PE_MAP;
+  // PE_MAP: the static encoding's width is what the embedding dense takes
+  // beyond the 112 planes (network_execution_plan.cpp:833-865).
+  d.P = d.pe_map ? (d.E ? static_cast<int>(ld.Count("body.ip_emb_w") / d.E) - kPlanes : 0)
+                 : static_cast<int>(ld.Count("body.ip_emb_preproc_b")) / kSquares;
   d.H = desc.headcount;
   while (ld.Count("body.encoder." + std::to_string(d.L) + ".mha.q_b"))
     ++d.L;
@@ -394,6 +402,11 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   std::ostringstream why;
   if (d.E <= 0 || d.P <= 0)
     why << "missing input embedding (body.ip_emb_*, body.ip_emb_preproc_*); ";
+  if (d.pe_map && d.P != mfh_policy::kPosEncodingChannels)
+    why << "PE_MAP embedding input must be 112 + " << mfh_policy::kPosEncodingChannels
+        << " wide; ";
+  if (d.pe_map && ld.Count("body.ip_emb_preproc_w"))
+    why << "PE_MAP nets carry no dynamic PE weights; ";
   if (d.E % 64)
     why << "embedding width " << d.E << " is not a multiple of 64; ";
   if (d.H <= 0 || d.E != d.H * 32)
@@ -427,7 +440,11 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   d.alpha = std::pow(2.0f * static_cast<float>(n_layers), -0.25f);
   if (n_layers == 0)
     d.alpha = 1.0f;
-  d.eps_body = 1e-3f;  // PE_DENSE nets (network_execution_plan.cpp:1164-1193)
+  // LayerNorm epsilons (network_execution_plan.cpp:1164-1193): encoder
+  // 1e-3 for PE_DENSE nets, 1e-6 otherwise; the embedding norm 1e-3 for
+  // PE_DENSE, 1e-5 otherwise.
+  d.eps_body = d.pe_map ? 1e-6f : 1e-3f;
+  d.eps_emb = d.pe_map ? 1e-5f : 1e-3f;
   return MFH_OK;
 }
 
@@ -440,16 +457,24 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   const Dims &d = net->d;
   const int E = d.E, S = kSquares;
   auto need = [&](const std::string &n, size_t c) { return ld.Need(n, c); };
-  const float *pre_w = need("body.ip_emb_preproc_w", static_cast<size_t>(S) * d.P * S * 12);
-  const float *pre_b = need("body.ip_emb_preproc_b", static_cast<size_t>(S) * d.P);
+  const float *pre_w = d.pe_map ? nullptr
+                                : need("body.ip_emb_preproc_w",
+                                       static_cast<size_t>(S) * d.P * S * 12);
+  const float *pre_b =
+      d.pe_map ? nullptr : need("body.ip_emb_preproc_b", static_cast<size_t>(S) * d.P);
   const float *emb_w = need("body.ip_emb_w", static_cast<size_t>(E) * (kPlanes + d.P));
   const float *emb_b = need("body.ip_emb_b", E);
   const float *ln_g = need("body.ip_emb_ln_gammas", E);
   const float *ln_b = need("body.ip_emb_ln_betas", E);
   if (!ld.error.empty())
     return SetError(MFH_ERR_INVALID, ld.error);
-  SetW(net->pre_w, AddGemmW(blob, net->fp8, {pre_w}, {S * d.P}, S * 12, S * 12));
-  net->pre_b = AddF32(blob, {pre_b}, {S * d.P});
+  if (d.pe_map) {
+    const auto &table = mfh_policy::StaticPositionEncoding();
+    net->static_pe = blob.Add(table.data(), table.size() * sizeof(float));
+  } else {
+    SetW(net->pre_w, AddGemmW(blob, net->fp8, {pre_w}, {S * d.P}, S * 12, S * 12));
+    net->pre_b = AddF32(blob, {pre_b}, {S * d.P});
+  }
   SetW(net->emb_w, AddGemmW(blob, net->fp8, {emb_w}, {E}, kPlanes + d.P, d.Kin));
   net->emb_b = AddF32(blob, {emb_b}, {E});
   net->emb_ln_g = AddF32(blob, {ln_g}, {E});
@@ -808,18 +833,19 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   // 691-890), embedding LayerNorm + gates (1399-1457, 1268-1316).
   {
     StageTimer t(net, st, "input_expand", 0.0, 12.0 * B * kPlanes + 2.0 * M * d.Kin * plane_mult);
-    MFH_RUN(mfh::LaunchExpandInputs(masks, values, B, net->S<std::uint16_t>("emb_in"),
-                                    net->Lo("emb_in"), d.Kin, net->S<std::uint16_t>("pos_in"),
-                                    st, &err_));
+    MFH_RUN(mfh::LaunchExpandInputs(
+        masks, values, B, net->S<std::uint16_t>("emb_in"), net->Lo("emb_in"), d.Kin,
+        d.pe_map ? net->W<float>(net->static_pe) : nullptr, d.P,
+        net->S<std::uint16_t>("pos_in"), st, &err_));
   }
-  {
+  if (!d.pe_map) {
     // The PE input holds exact plane values: single precision suffices.
     mfh::GemmParams p = gemm("pos_in", kSquares * 12, net->pre_w, kSquares * 12, B,
                              kSquares * d.P, kSquares * 12, net->W<float>(net->pre_b),
                              mfh::ACT_NONE, mfh::GEMM_OUT_F32, pe, nullptr, kSquares * d.P);
     MFH_RUN(run(p, "pe"));
   }
-  {
+  if (!d.pe_map) {
     StageTimer tpe(net, st, "pe_scatter", 0.0, 4.0 * B * kSquares * d.P);
     MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, net->S<std::uint16_t>("emb_in"), net->Lo("emb_in"),
                                  d.Kin, st, &err_));
@@ -828,7 +854,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
                    d.act_default, mfh::GEMM_OUT_F32, pre, nullptr, E),
                   "embedding"));
   {
-    mfh::LayerNormParams lp = ln(pre, M, E, 1e-3f, net->W<float>(net->emb_ln_g),
+    mfh::LayerNormParams lp = ln(pre, M, E, d.eps_emb, net->W<float>(net->emb_ln_g),
                                  net->W<float>(net->emb_ln_b), resid, "act");
     lp.mult_gate = net->mult_gate ? net->W<float>(net->mult_gate) : nullptr;
     lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;

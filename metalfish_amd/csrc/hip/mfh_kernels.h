@@ -75,13 +75,16 @@ struct GemmParams {
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
 
 // Packed planes -> embedding input rows and the dynamic-PE input.
-//   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values, rest zero (the PE
-//   columns are filled by LaunchScatterPe); emb_in_lo (split precision, may
-//   be null) gets the zero residual of those exact values.
+//   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values; with static_pe
+//   ([64][pe_ch] fp32, PE_MAP nets) cols 112..111+pe_ch the square's table
+//   row; the rest zero (PE_DENSE columns are filled by LaunchScatterPe);
+//   emb_in_lo (split precision, may be null) gets the zero residual of those
+//   exact values (planes and the table's -1/0/1 are exact in bf16).
 //   pos_in [B, 64*12] bf16: square-major first 12 planes (exact in bf16).
 hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
                               int batch, std::uint16_t *emb_in,
                               std::uint16_t *emb_in_lo, int emb_ld,
+                              const float *static_pe, int pe_ch,
                               std::uint16_t *pos_in, hipStream_t stream,
                               std::string *err);
 

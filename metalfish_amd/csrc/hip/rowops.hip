@@ -19,6 +19,7 @@ __global__ void ExpandInputsKernel(const std::uint64_t *__restrict__ masks,
                                    const float *__restrict__ values, int batch,
                                    std::uint16_t *__restrict__ emb_in,
                                    std::uint16_t *__restrict__ emb_in_lo, int emb_ld,
+                                   const float *__restrict__ static_pe, int pe_ch,
                                    std::uint16_t *__restrict__ pos_in) {
   const int chunks = emb_ld / 8;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -35,6 +36,8 @@ __global__ void ExpandInputsKernel(const std::uint64_t *__restrict__ masks,
       if (col < kPlanes) {
         const std::uint64_t m = masks[static_cast<size_t>(b) * kPlanes + col];
         v = ((m >> sq) & 1ull) ? values[static_cast<size_t>(b) * kPlanes + col] : 0.f;
+      } else if (static_pe && col < kPlanes + pe_ch) {
+        v = static_pe[sq * pe_ch + col - kPlanes];
       }
       out[e] = f32_to_bf16(v);
     }
@@ -251,10 +254,11 @@ std::string Fail(std::string *err, const char *what) {
 
 hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
                               int batch, std::uint16_t *emb_in, std::uint16_t *emb_in_lo,
-                              int emb_ld, std::uint16_t *pos_in, hipStream_t stream,
-                              std::string *err) {
+                              int emb_ld, const float *static_pe, int pe_ch,
+                              std::uint16_t *pos_in, hipStream_t stream, std::string *err) {
   if (batch <= 0 || emb_ld % 8 || emb_ld < kPlanes || !masks || !values || !emb_in ||
-      !pos_in || (reinterpret_cast<std::uintptr_t>(emb_in) & 15u)) {
+      !pos_in || (reinterpret_cast<std::uintptr_t>(emb_in) & 15u) ||
+      (static_pe && (pe_ch <= 0 || kPlanes + pe_ch > emb_ld))) {
     Fail(err, "expand_inputs: invalid arguments");
     return hipErrorInvalidValue;
   }
@@ -262,7 +266,7 @@ hipError_t LaunchExpandInputs(const std::uint64_t *masks, const float *values,
   const int pos_total = batch * kSquares * kPePlanes;
   const int n = total > pos_total ? total : pos_total;
   hipLaunchKernelGGL(ExpandInputsKernel, dim3((n + 255) / 256), dim3(256), 0, stream,
-                     masks, values, batch, emb_in, emb_in_lo, emb_ld, pos_in);
+                     masks, values, batch, emb_in, emb_in_lo, emb_ld, static_pe, pe_ch, pos_in);
   return hipGetLastError();
 }
 

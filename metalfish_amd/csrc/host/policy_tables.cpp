@@ -71,6 +71,18 @@ const std::array<std::int16_t, kPolicyOutputs> &AttentionGather() {
   return B().gather;
 }
 
+const std::array<float, 64 * kPosEncodingChannels> &StaticPositionEncoding() {
+  static const std::array<float, 64 * kPosEncodingChannels> table = [] {
+    std::array<float, 64 * kPosEncodingChannels> t{};
+    for (int sq = 0; sq < 64; ++sq)
+      for (int c = 0; c < kPosEncodingChannels; ++c)
+        t[sq * kPosEncodingChannels + c] =
+            sq == c ? -1.0f : (QueenLine(sq, c) || KnightJump(sq, c) ? 1.0f : 0.0f);
+    return t;
+  }();
+  return table;
+}
+
 int MoveToIndex(int from, int to, char promo) {
   if (from < 0 || from > 63 || to < 0 || to > 63)
     return -1;

@@ -33,6 +33,14 @@ const std::array<std::int16_t, kAttentionRaw> &AttentionMap();
 // policy index -> raw attention-logit index (inverse of AttentionMap).
 const std::array<std::int16_t, kPolicyOutputs> &AttentionGather();
 
+// Static position encoding of INPUT_EMBEDDING_PE_MAP nets, [square][64]:
+// -1 at the square itself, 1 at every square a queen or a knight reaches
+// from it, 0 elsewhere -- the rule behind reference
+// src/nn/tables/attention_policy_map.h:377 (kPosEncoding), checked against a
+// digest of that table.
+constexpr int kPosEncodingChannels = 64;
+const std::array<float, 64 * kPosEncodingChannels> &StaticPositionEncoding();
+
 // Index of a move given in the side-to-move-relative frame, or -1.
 // `promo` is 0 for no promotion or one of 'q','r','b','n'.
 int MoveToIndex(int from, int to, char promo);

@@ -189,6 +189,12 @@ int64_t mfs_perft(const char *fen, int depth) {
   return static_cast<int64_t>(mfh_chess::Perft(game, depth));
 }
 
+void mfs_static_position_encoding(float *out) {
+  const auto &t = mfh_policy::StaticPositionEncoding();
+  if (out)
+    std::memcpy(out, t.data(), sizeof(float) * t.size());
+}
+
 void mfs_policy_tables(int16_t *attention_map, int16_t *gather,
                        char *move_strings) {
   const auto &map = mfh_policy::AttentionMap();

@@ -44,6 +44,7 @@ def lib():
         _lib.mfs_perft.argtypes = [ctypes.c_char_p, ctypes.c_int]
         _lib.mfs_perft.restype = ctypes.c_int64
         _lib.mfs_policy_tables.argtypes = [ctypes.c_void_p] * 3
+        _lib.mfs_static_position_encoding.argtypes = [ctypes.c_void_p]
     return _lib
 
 
@@ -62,6 +63,7 @@ class NetSpec:
     policy_dim: int = 0
     value_dim: int = 32
     value_hidden: int = 128
+    pe_map: bool = False         # static position encoding (PE_MAP) instead of PE_DENSE
     moves_left_dim: int = 0      # moves-left head square embedding (0: no head)
     moves_left_hidden: int = 128
     wdl: bool = True
@@ -81,6 +83,10 @@ SPECS = {
     # 128 hidden, the Lc0 widths).
     "cpu_plumbing_mlh": NetSpec("cpu_plumbing_mlh", 256, 2, 8, 512, input_ffn=512,
                                 policy_dim=256, moves_left_dim=8),
+    # Test net: config 1 with the PE_MAP static position encoding (64
+    # channels, embedding input 112 + 64) in place of the dynamic one.
+    "cpu_plumbing_pe_map": NetSpec("cpu_plumbing_pe_map", 256, 2, 8, 512, pe_channels=64,
+                                   input_ffn=512, policy_dim=256, pe_map=True),
 }
 
 
@@ -99,8 +105,9 @@ def tensor_layout(spec: NetSpec):
         vec(prefix + "_gammas", n, 0, ONE_PLUS_TENTH)
         vec(prefix + "_betas", n, 0, TENTH)
 
-    mat("body.ip_emb_preproc_w", S * P, S * 12)
-    vec("body.ip_emb_preproc_b", S * P, S * 12)
+    if not spec.pe_map:
+        mat("body.ip_emb_preproc_w", S * P, S * 12)
+        vec("body.ip_emb_preproc_b", S * P, S * 12)
     mat("body.ip_emb_w", E, 112 + P)
     vec("body.ip_emb_b", E, 112 + P)
     norm("body.ip_emb_ln", E)
@@ -269,3 +276,10 @@ def policy_tables():
     lib().mfs_policy_tables(amap.ctypes.data, gather.ctypes.data, strings)
     names = [strings.raw[6 * i:6 * i + 6].split(b"\0", 1)[0].decode() for i in range(1858)]
     return amap, gather, names
+
+
+def static_position_encoding():
+    """The PE_MAP static position encoding [64 squares, 64 channels]."""
+    out = np.zeros((64, 64), dtype=np.float32)
+    lib().mfs_static_position_encoding(out.ctypes.data)
+    return out

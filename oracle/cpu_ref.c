@@ -29,6 +29,7 @@ enum {
   OR_ATTENTION = 5,
   OR_POLICY_MAP = 6,
   OR_DYNAMIC_PE = 7,
+  OR_STATIC_PE = 8,
 };
 
 enum {
@@ -228,6 +229,34 @@ static int run_dynamic_pe(const or_step *s, int batch, const uint64_t *masks,
     }
   free(pos_in);
   free(pos_out);
+  return 0;
+}
+
+/* Static position encoding of PE_MAP nets: per square, the 112 planes then
+ * the table row of that square (t[0] = [64][pe_w], d1[0] = pe_w).  The
+ * reference CPU backend has no PE_MAP path; this restates the CUDA backend's
+ * StaticPositionEncodingConcatKernel (cuda/cuda_kernels.cu:1016-1040),
+ * which feeds body.input_embedding (cuda_stage_executor.cpp:487-492). */
+static int run_static_pe(const or_step *s, int batch, const uint64_t *masks,
+                         const float *values, or_buf *out) {
+  const int squares = 64, input_planes = 112;
+  const float *table = s->t[0];
+  const int pe_w = s->d1[0];
+  if (s->d0[0] != squares || pe_w <= 0)
+    return -11;
+  if (set_buf(out, batch * squares, input_planes + pe_w))
+    return -1;
+  for (int bi = 0; bi < batch; ++bi)
+    for (int sq = 0; sq < squares; ++sq) {
+      const uint64_t bit = 1ULL << sq;
+      float *row = out->v + ((size_t)bi * squares + sq) * out->width;
+      for (int p = 0; p < input_planes; ++p) {
+        const size_t pi = (size_t)bi * input_planes + p;
+        row[p] = (masks[pi] & bit) ? values[pi] : 0.0f;
+      }
+      for (int c = 0; c < pe_w; ++c)
+        row[input_planes + c] = table[(size_t)sq * pe_w + c];
+    }
   return 0;
 }
 
@@ -528,6 +557,9 @@ int or_run(int batch, const uint64_t *masks, const float *values,
     switch (s->kind) {
     case OR_DYNAMIC_PE:
       rc = run_dynamic_pe(s, batch, masks, values, dst);
+      break;
+    case OR_STATIC_PE:
+      rc = run_static_pe(s, batch, masks, values, dst);
       break;
     case OR_DENSE:
       rc = run_dense(s, batch, src, dst);

@@ -42,8 +42,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
+from .policy_tables import pos_encoding
 
-DENSE, LAYERNORM, GATE, FFN, ATTENTION, POLICY_MAP, DYNAMIC_PE = 1, 2, 3, 4, 5, 6, 7
+DENSE, LAYERNORM, GATE, FFN, ATTENTION, POLICY_MAP, DYNAMIC_PE, STATIC_PE = 1, 2, 3, 4, 5, 6, 7, 8
 
 ACTIVATIONS = {
     "": -1,
@@ -353,6 +354,28 @@ class ResolvedProgram:
                 remember(s.name, rec.dst)
                 last_executed = s.name
                 continue
+            if (s.kind == "dense" and s.name == "body.input_embedding"
+                    and fmt.input_embedding == "PE_MAP" and fmt.attention_body
+                    and last["body"] is None):
+                # PE_MAP: planes concatenated with the static position
+                # encoding feed the embedding dense (the CUDA backend's
+                # StaticPositionEncodingConcatKernel, cuda_kernels.cu:1016-1040,
+                # for IsStaticPositionEmbeddingStage, cuda_stage_executor.cpp:
+                # 487-492; width = ip_emb_w in-dim - 112,
+                # network_execution_plan.cpp:833-865).
+                pe = np.ascontiguousarray(pos_encoding(), dtype=np.float32)
+                pe_w = self.tensors[s.tensors[0]].shape[1] - 112
+                if pe_w != pe.shape[1]:
+                    raise ValueError("static position encoding width mismatch")
+                self._keep.append(pe)
+                pre = OrStep()
+                pre.parent = -1
+                pre.kind, pre.src, pre.dst = STATIC_PE, 0, new_buf()
+                pre.t[0] = pe.ctypes.data
+                pre.d0[0], pre.d1[0] = pe.shape[0], pe.shape[1]
+                pre.n_tensors = 1
+                self.records.append(pre)
+                remember("body.input_embedding_static_pe", pre.dst)
             src = source_for(s.name)
             if s.kind == "positional":
                 last_executed = s.name

@@ -65,3 +65,17 @@ def uci_strings():
         names.append("%s%d%s%d%s" % ("abcdefgh"[f & 7], (f >> 3) + 1, "abcdefgh"[t & 7],
                                      (t >> 3) + 1, p))
     return names
+
+
+def pos_encoding():
+    """Static position encoding of PE_MAP nets, [square][channel] float32:
+    -1 on the square itself, 1 where a queen or knight move from the square
+    lands, 0 elsewhere (the rule behind reference
+    src/nn/tables/attention_policy_map.h:377, kPosEncoding).  Pinned against
+    the digest of the reference's table by tests/test_policy_tables.py."""
+    t = np.zeros((64, 64), dtype=np.float32)
+    for s_ in range(64):
+        for c in range(64):
+            t[s_, c] = -1.0 if s_ == c else (1.0 if _queen_line(s_, c) or _knight(s_, c)
+                                             else 0.0)
+    return t

@@ -1,4 +1,5 @@
-// Checker-only program: dumps the reference's own policy tables so the tests
+// Checker-only program: dumps the reference's own policy tables (and the
+// static position encoding table) so the tests
 // can pin this repository's independently generated tables against them.
 // Built by oracle/Makefile from the reference sources where they lie
 // (/root/reference/src/nn/policy_map.cpp and
@@ -52,6 +53,12 @@ int main(int argc, char **argv) {
                                m.type_of() == PROMOTION ? m.promotion_type() : 0)};
     std::fwrite(rec, 2, 3, f);
   }
+  // Section 4: kPosEncoding, 64 x 64 little-endian float32.
+  for (int sq = 0; sq < 64; ++sq)
+    for (int c = 0; c < NN::Tables::kNumPosEncodingChannels; ++c) {
+      const float v = NN::Tables::kPosEncoding[sq][c];
+      std::fwrite(&v, 4, 1, f);
+    }
   std::fclose(f);
   return 0;
 }

@@ -36,16 +36,20 @@ def sha(a):
 
 def reference_tables():
     path = os.path.join(ROOT, "oracle", "_ref", "ref_tables.bin")
-    raw = np.fromfile(path, dtype=np.int16)
+    n16 = 4288 + 64 * 64 * 5 + 1858 * 3
+    data = open(path, "rb").read()
+    raw = np.frombuffer(data[:2 * n16], dtype=np.int16)
     amap = raw[:4288]
     idx = raw[4288:4288 + 64 * 64 * 5]
     inv = raw[4288 + 64 * 64 * 5:]
-    assert inv.size == 1858 * 3
+    pos = np.frombuffer(data[2 * n16:], dtype=np.float32)
+    assert inv.size == 1858 * 3 and pos.size == 64 * 64
     return {"source": "oracle/_ref/ref_tables.bin (reference policy_map.cpp + "
                       "tables/attention_policy_map.h)",
             "attn_policy_map_sha256": sha(amap),
             "move_to_nn_index_sha256": sha(idx),
-            "index_to_nn_move_sha256": sha(inv)}
+            "index_to_nn_move_sha256": sha(inv),
+            "pos_encoding_sha256": sha(pos)}
 
 
 def seeded():

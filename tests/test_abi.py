@@ -53,9 +53,15 @@ def _create(desc, weights):
 
 def test_unsupported_structures_are_rejected_before_touching_a_device():
     w = synth.make_weights(synth.SPECS["cpu_plumbing"], seed=0)
+    # PE_MAP declared for a net with dynamic-PE weights and a 112 + 16 input.
     rc, msg = _create(_desc(input_embedding=1), w)
-    assert rc == -3 and "PE_DENSE" in msg
+    assert rc == -3 and "PE_MAP" in msg
+    rc, msg = _create(_desc(input_embedding=0), w)
+    assert rc == -3 and "input embeddings" in msg
+    # Moves-left head declared without its tensors.
     rc, msg = _create(_desc(moves_left=1), w)
+    assert rc == -3 and "moves-left" in msg
+    rc, msg = _create(_desc(moves_left=2), w)
     assert rc == -3 and "moves-left" in msg
     rc, msg = _create(_desc(headcount=4), w)  # head depth 64
     assert rc == -3 and "head depth" in msg

@@ -393,6 +393,26 @@ def test_moves_left_head(precision, batch):
     plain.close()
 
 
+@pytest.mark.parametrize("precision,batch", [("bf16x2", 16), ("bf16", 16), ("bf16x2", 3)])
+def test_pe_map_static_embedding(precision, batch):
+    """PE_MAP nets: planes concatenated with the static position encoding
+    feed the embedding (the CUDA backend's StaticPositionEncodingConcatKernel,
+    reference cuda_kernels.cu:1016-1040), LayerNorm epsilons 1e-5 / 1e-6
+    (network_execution_plan.cpp:1164-1193), against the oracle."""
+    spec = synth.SPECS["cpu_plumbing_pe_map"]
+    weights = synth.make_weights(spec, seed=4)
+    planes, legal = synth.playout_positions(16, seed=8)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads, input_embedding="PE_MAP"),
+                           weights).evaluate_batch(planes)
+    net = backend.create_network(spec, weights, max_batch=batch, precision=precision)
+    out = net.evaluate_batch(planes)
+    net.close()
+    assert np.abs(out["policy"] - ref["policy"]).max() <= 2e-2
+    assert np.abs(out["wdl"] - ref["wdl"]).max() <= 5e-3
+    if precision == "bf16x2":
+        assert _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
+
+
 def test_bad_batch_rejected():
     spec = synth.SPECS["cpu_plumbing"]
     net = backend.create_network(spec, synth.make_weights(spec), max_batch=4, device=0)

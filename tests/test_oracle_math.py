@@ -254,3 +254,26 @@ def test_plan_residual_scale_and_epsilons():
     other = oplan.NetFormat(input_embedding="PE_MAP")
     assert oplan.ffn_ln_eps(other, "body.encoder.3.ffn") == np.float32(1e-6)
     assert oplan.residual_scale(steps, "policy.vanilla.output") == np.float32(1.0)
+
+
+def test_static_pe_step_equals_zero_weight_dynamic_pe():
+    """The oracle's PE_MAP concat (static table) equals its dynamic-PE step
+    (pinned by the reference KATs) run with zero weights and the table as
+    bias, so placement, channel order and square indexing of the static
+    step are fixed by the dynamic one.  Nets without LayerNorms, so the
+    formats' different epsilons play no part."""
+    from metalfish_amd import synth
+    spec = synth.SPECS["cpu_plumbing_pe_map"]
+    w = synth.make_weights(spec, seed=2)
+    keep = {k: v for k, v in w.items()
+            if not k.startswith(("body.encoder.", "body.ip_emb_ln", "body.ip_emb_ffn"))}
+    dense = dict(keep)
+    dense["body.ip_emb_preproc_w"] = np.zeros((64 * 64, 64 * 12), np.float32)
+    dense["body.ip_emb_preproc_b"] = oracle.policy_tables.pos_encoding().reshape(-1)
+    planes, _ = synth.playout_positions(4, seed=5)
+    a = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads, input_embedding="PE_MAP"),
+                         keep).evaluate_batch(planes)
+    b = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads, input_embedding="PE_DENSE"),
+                         dense).evaluate_batch(planes)
+    for k in ("policy", "wdl"):
+        assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), k

@@ -69,6 +69,16 @@ def test_reference_dump_matches_committed_digests():
     raw = np.fromfile(REF_BIN, dtype=np.int16)
     assert sha(raw[:4288]) == GOLD["attn_policy_map_sha256"]
     assert sha(raw[4288:4288 + 64 * 64 * 5]) == GOLD["move_to_nn_index_sha256"]
+    n16 = 4288 + 64 * 64 * 5 + 1858 * 3
+    pos = np.frombuffer(open(REF_BIN, "rb").read()[2 * n16:], dtype=np.float32)
+    assert sha(pos) == GOLD["pos_encoding_sha256"]
+
+
+def test_static_position_encoding_matches_reference():
+    """PE_MAP table (reference tables/attention_policy_map.h:377, kPosEncoding)
+    rebuilt from its rule, in the product and in the oracle."""
+    assert sha(synth.static_position_encoding()) == GOLD["pos_encoding_sha256"]
+    assert sha(opt.pos_encoding()) == GOLD["pos_encoding_sha256"]
 
 
 def test_encoder_policy_roundtrip_g1f3():
