@@ -88,6 +88,8 @@ typedef struct {
   int precision;          /* MFH_PRECISION_* */
   int max_batch;          /* largest batch one eval call accepts (>= 1) */
   int device;             /* HIP device ordinal, -1 = current device */
+  int pol_headcount;      /* policy encoder heads (Weights.pol_headcount); 0 without
+                             policy encoder layers */
 } mfh_net_desc;
 
 /* One weight tensor, named as in the reference's weight inventory
@@ -276,7 +278,7 @@ int mfh_weights_load(const char *path, mfh_weights **out);
 int mfh_weights_parse(const void *data, uint64_t bytes, mfh_weights **out);
 
 /* Format fields and head counts.  With desc non-NULL, also fills the format
- * fields and headcount of a net description, as DescribeNetworkFormat reads
+ * fields, headcount and pol_headcount of a net description, as DescribeNetworkFormat reads
  * them (reference src/nn/network_format.cpp:72-127), leaving weights_dtype,
  * precision, max_batch and device as the caller set them.  Either pointer
  * may be NULL. */

@@ -44,7 +44,7 @@ class MfhNetDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "network", "policy", "value", "moves_left", "input_embedding", "default_activation",
         "ffn_activation", "smolgen_activation", "headcount", "weights_dtype", "precision",
-        "max_batch", "device")]
+        "max_batch", "device", "pol_headcount")]
 
 
 class MfhTensor(ctypes.Structure):
@@ -143,7 +143,7 @@ class HipNetwork:
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
                  device=-1, precision="bf16x2", weights_dtype="bf16", net_format=None,
-                 moves_left=False, pe_map=False):
+                 moves_left=False, pe_map=False, pol_heads=0):
         """``net_format``: NetworkFormat fields of a loaded file
         (``WeightsFile.format``); they replace the description the keyword
         arguments give."""
@@ -162,7 +162,7 @@ class HipNetwork:
                           ffn_activation=ACTIVATION[ffn_activation],
                           smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
                           weights_dtype=WEIGHTS[weights_dtype], precision=PRECISION[precision],
-                          max_batch=max_batch, device=device)
+                          max_batch=max_batch, device=device, pol_headcount=pol_heads)
         if net_format is not None:
             for k in ("network", "policy", "value", "moves_left", "input_embedding",
                       "default_activation", "ffn_activation", "smolgen_activation"):
@@ -376,7 +376,7 @@ def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
     "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput);
     ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales)."""
     return HipNetwork(weights, spec.heads, wdl=spec.wdl, moves_left=spec.moves_left_dim > 0,
-                      pe_map=spec.pe_map,
+                      pe_map=spec.pe_map, pol_heads=spec.policy_heads,
                       default_activation=spec.default_activation,
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,
@@ -424,7 +424,7 @@ class WeightsFile:
         reference src/nn/network.cpp:137-208)."""
         return HipNetwork(self.tensors, self.headcount, max_batch=max_batch, device=device,
                           precision=precision, weights_dtype=weights_dtype,
-                          net_format=self.format)
+                          net_format=self.format, pol_heads=self.pol_headcount)
 
 
 def load_weights(path) -> WeightsFile:

@@ -15,6 +15,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -151,6 +152,7 @@ struct Dims {
   int C = 0, Hs = 0, HG = 0, G = 0;
   int Dp = 0, Vd = 0, Vh = 0, Vout = 0;
   int Md = 0, Mh = 0;  // moves-left head: square embedding, hidden width
+  int PL = 0, PH = 0, PF = 0;  // policy encoder layers: count, heads, FFN width
   bool gates = false, input_ffn = false, smolgen = false, wdl = true, mlh = false;
   bool pe_map = false;  // static position encoding (INPUT_EMBEDDING_PE_MAP)
   float eps_emb = 1e-3f;  // input-embedding LayerNorm
@@ -186,6 +188,7 @@ struct mfh_net {
   size_t pre_w[2], emb_w[2], in_ffn1_w[2], in_ffn2_w[2], global_w[2];
   size_t in_ffn1_b, in_ffn2_b, in_ln_g, in_ln_b;
   std::vector<Layer> layers;
+  std::vector<Layer> pol_layers;  // policy encoder layers
   size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
   size_t head_w[2], qk_w[2], val1_w[2];
   size_t mov_b = 0, mov1_b = 0, mov2_w = 0, mov2_b = 0;  // moves-left head
@@ -426,8 +429,21 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
         << " outputs; ";
   if (!ld.Count("body.ip_emb_ln_gammas"))
     why << "body.ip_emb_ln is required; ";
-  if (ld.Count("policy.vanilla.encoder.0.mha.q_b") || ld.Count("policy.vanilla.ip_pol_b") == 0)
-    why << "policy head must be ip_pol/ip2_pol/ip3_pol/ip4_pol without encoder layers; ";
+  if (ld.Count("policy.vanilla.ip_pol_b") == 0)
+    why << "policy head needs ip_pol/ip2_pol/ip3_pol/ip4_pol; ";
+  while (ld.Count("policy.vanilla.encoder." + std::to_string(d.PL) + ".mha.q_b"))
+    ++d.PL;
+  if (d.PL) {
+    d.PH = desc.pol_headcount;
+    d.PF = static_cast<int>(ld.Count("policy.vanilla.encoder.0.ffn.dense1_b"));
+    if (d.PH <= 0 || d.E != d.PH * 32 || d.PH % 4)
+      why << "policy encoder head depth must be 32 with a multiple of 4 heads (embedding "
+          << d.E << ", heads " << d.PH << "); ";
+    if (d.PF <= 0 || d.PF % 64)
+      why << "policy encoder FFN width must be a positive multiple of 64; ";
+    if (ld.Count("policy.vanilla.encoder.0.mha.smolgen.compress"))
+      why << "policy encoder layers with smolgen are not supported; ";
+  }
   // The value-error head (value.winner.ip_val_err_*) feeds no NetworkOutput
   // field (reference network_output_decoder.cpp:31-78), so it is accepted and
   // not computed.
@@ -513,39 +529,40 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     SetW(net->global_w, AddGemmW(blob, net->fp8, {g}, {S * S}, d.G, d.G));
   }
   net->layers.resize(d.L);
-  for (int i = 0; i < d.L; ++i) {
-    const std::string p = "body.encoder." + std::to_string(i);
-    Layer &L = net->layers[i];
+  // One encoder layer (the reference's EncoderLayer, weights.cpp:162-180):
+  // Q | K | V (| smolgen compression) fused into one weight, out-projection,
+  // LayerNorms, FFN of width ffn, and the smolgen denses when present.
+  auto pack_layer = [&](const std::string &p, Layer &L, int ffn, bool smolgen) -> int {
     const size_t EE = static_cast<size_t>(E) * E;
     const float *qw = need(p + ".mha.q_w", EE), *qb = need(p + ".mha.q_b", E);
     const float *kw = need(p + ".mha.k_w", EE), *kb = need(p + ".mha.k_b", E);
     const float *vw = need(p + ".mha.v_w", EE), *vb = need(p + ".mha.v_b", E);
     const float *ow = need(p + ".mha.dense_w", EE), *ob = need(p + ".mha.dense_b", E);
     const float *l1g = need(p + ".ln1_gammas", E), *l1b = need(p + ".ln1_betas", E);
-    const float *f1w = need(p + ".ffn.dense1_w", static_cast<size_t>(d.F) * E);
-    const float *f1b = need(p + ".ffn.dense1_b", d.F);
-    const float *f2w = need(p + ".ffn.dense2_w", static_cast<size_t>(E) * d.F);
+    const float *f1w = need(p + ".ffn.dense1_w", static_cast<size_t>(ffn) * E);
+    const float *f1b = need(p + ".ffn.dense1_b", ffn);
+    const float *f2w = need(p + ".ffn.dense2_w", static_cast<size_t>(E) * ffn);
     const float *f2b = need(p + ".ffn.dense2_b", E);
     const float *l2g = need(p + ".ln2_gammas", E), *l2b = need(p + ".ln2_betas", E);
     const float *cw = nullptr;
-    if (d.smolgen)
+    if (smolgen)
       cw = need(p + ".mha.smolgen.compress", static_cast<size_t>(d.C) * E);
     if (!ld.error.empty())
       return SetError(MFH_ERR_INVALID, ld.error);
-    SetW(L.qkv_w, AddGemmW(blob, net->fp8, {qw, kw, vw, cw}, {E, E, E, d.smolgen ? d.C : 0}, E, E));
-    L.qkv_b = AddF32(blob, {qb, kb, vb, nullptr}, {E, E, E, d.smolgen ? d.C : 0});
+    SetW(L.qkv_w, AddGemmW(blob, net->fp8, {qw, kw, vw, cw}, {E, E, E, smolgen ? d.C : 0}, E, E));
+    L.qkv_b = AddF32(blob, {qb, kb, vb, nullptr}, {E, E, E, smolgen ? d.C : 0});
     SetW(L.out_w, AddGemmW(blob, net->fp8, {ow}, {E}, E, E));
     L.out_b = AddF32(blob, {ob}, {E});
     L.ln1_g = AddF32(blob, {l1g}, {E});
     L.ln1_b = AddF32(blob, {l1b}, {E});
-    SetW(L.ffn1_w, AddGemmW(blob, net->fp8, {f1w}, {d.F}, E, E));
-    L.ffn1_b = AddF32(blob, {f1b}, {d.F});
-    SetW(L.ffn2_w, AddGemmW(blob, net->fp8, {f2w}, {E}, d.F, d.F));
+    SetW(L.ffn1_w, AddGemmW(blob, net->fp8, {f1w}, {ffn}, E, E));
+    L.ffn1_b = AddF32(blob, {f1b}, {ffn});
+    SetW(L.ffn2_w, AddGemmW(blob, net->fp8, {f2w}, {E}, ffn, ffn));
     L.ffn2_b = AddF32(blob, {f2b}, {E});
     L.ln2_g = AddF32(blob, {l2g}, {E});
     L.ln2_b = AddF32(blob, {l2b}, {E});
-    L.smolgen = d.smolgen;
-    if (d.smolgen) {
+    L.smolgen = smolgen;
+    if (smolgen) {
       const std::string s = p + ".mha.smolgen";
       const float *d1w = need(s + ".dense1_w", static_cast<size_t>(d.Hs) * S * d.C);
       const float *d1b = need(s + ".dense1_b", d.Hs);
@@ -564,6 +581,20 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       L.sg_ln2_g = AddF32(blob, {g2}, {d.HG});
       L.sg_ln2_b = AddF32(blob, {b2}, {d.HG});
     }
+    return MFH_OK;
+  };
+  for (int i = 0; i < d.L; ++i) {
+    const int rc = pack_layer("body.encoder." + std::to_string(i), net->layers[i], d.F, d.smolgen);
+    if (rc != MFH_OK)
+      return rc;
+  }
+  // Policy encoder layers (weights.cpp:188-203), no smolgen.
+  net->pol_layers.resize(d.PL);
+  for (int i = 0; i < d.PL; ++i) {
+    const int rc = pack_layer("policy.vanilla.encoder." + std::to_string(i), net->pol_layers[i],
+                              d.PF, false);
+    if (rc != MFH_OK)
+      return rc;
   }
   const std::string pp = "policy.vanilla.", vp = "value.winner.";
   const float *pw = need(pp + "ip_pol_w", static_cast<size_t>(d.Dp) * E);
@@ -650,7 +681,7 @@ void PlanWorkspace(mfh_net *net) {
     if (d.split_attn)
       add(name + "_lo", elems * 2);
   };
-  const int hid = d.F > d.Fi ? d.F : d.Fi;
+  const int hid = std::max(d.F, std::max(d.Fi, d.PF));
   const int sk1 = d.smolgen ? SplitK(kSquares * d.C) : 1;
   const int skv = SplitK(kSquares * d.Vd);
   add("masks", B * kPlanes * 8);
@@ -861,12 +892,12 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     MFH_RUN(run_ln(lp));
   }
   auto residual_gemm = [&](const std::string &a, int k, const size_t (&w_off)[2],
-                           const float *bias, const char *role) {
+                           const float *bias, const char *role, float alpha) {
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
     p.resid = resid;
     p.ldr = E;
-    p.alpha = d.alpha;
+    p.alpha = alpha;
     return run(p, role);
   };
   if (d.input_ffn) {
@@ -875,13 +906,16 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
                      net->Lo("hid"), d.Fi),
                 "input_ffn1"));
     MFH_RUN(residual_gemm("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
-                          "input_ffn2"));
+                          "input_ffn2", d.alpha));
     MFH_RUN(run_ln(ln(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
                       net->W<float>(net->in_ln_b), resid, "act")));
   }
 
-  // Encoder layers (cpu_network.cpp:1027-1266, 1318-1457).
-  for (const Layer &L : net->layers) {
+  // One encoder layer (cpu_network.cpp:1027-1266, 1318-1457) on resid/act:
+  // `heads` attention heads, FFN width `ffn`, LayerNorm epsilons after the
+  // attention and the FFN, residual scale alpha.
+  auto encoder_layer = [&](const Layer &L, int heads, int ffn, float eps_attn, float eps_ffn,
+                           float alpha) -> int {
     mfh::GemmParams p = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen ? d.C : 0), E,
                              net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
                              net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
@@ -896,7 +930,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     ap.qkv = net->S<std::uint16_t>("qkv");
     ap.qkv_lo = net->Lo("qkv");
     ap.batch = B;
-    ap.heads = d.H;
+    ap.heads = heads;
     ap.ctx = net->S<std::uint16_t>("ctx");
     ap.ctx_lo = net->Lo("ctx");
     if (L.smolgen) {
@@ -932,7 +966,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       ap.bias_f32 = d.split_attn ? 1 : 0;
     }
     {
-      const double heads_total = static_cast<double>(B) * d.H;
+      const double heads_total = static_cast<double>(B) * heads;
       const double flops = heads_total * 2.0 * (2.0 * kSquares * kSquares * 32);
       const double bytes = 2.0 * (d.split_attn ? 2.0 : 1.0) * 3.0 * M * E +
                            2.0 * plane_mult * M * E +
@@ -942,16 +976,23 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       StageTimer t(net, st, "attention", flops, bytes);
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
     }
-    MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b), "out"));
-    MFH_RUN(run_ln(ln(pre, M, E, d.eps_body, net->W<float>(L.ln1_g),
-                      net->W<float>(L.ln1_b), resid, "act")));
-    MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, d.F, E, net->W<float>(L.ffn1_b), d.act_ffn,
-                     mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), d.F),
+    MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha));
+    MFH_RUN(run_ln(ln(pre, M, E, eps_attn, net->W<float>(L.ln1_g), net->W<float>(L.ln1_b),
+                      resid, "act")));
+    MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b), d.act_ffn,
+                     mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), ffn),
                 "ffn1"));
-    MFH_RUN(residual_gemm("hid", d.F, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2"));
-    MFH_RUN(run_ln(ln(pre, M, E, d.eps_body, net->W<float>(L.ln2_g),
-                      net->W<float>(L.ln2_b), resid, "act")));
+    MFH_RUN(residual_gemm("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha));
+    MFH_RUN(run_ln(ln(pre, M, E, eps_ffn, net->W<float>(L.ln2_g), net->W<float>(L.ln2_b),
+                      resid, "act")));
+    return MFH_OK;
+  };
+  for (const Layer &L : net->layers) {
+    const int rc = encoder_layer(L, d.H, d.F, d.eps_body, d.eps_body, d.alpha);
+    if (rc != MFH_OK)
+      return rc;
   }
+
 
   // Heads: policy "output" | value "output" (default activation), policy
   // Q | K, attention policy map, value dense1 (flattened squares) and dense2.
@@ -963,6 +1004,28 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   ph.C2_lo = net->Lo("val_emb");
   ph.ldc2 = d.Vd;
   MFH_RUN(run(ph, "heads"));
+  if (d.mlh)
+    MFH_RUN(run(gemm("act", E, net->mov_w, E, M, d.Md, E, net->W<float>(net->mov_b),
+                     d.act_default, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("mov_emb"),
+                     net->Lo("mov_emb"), d.Md),
+                "moves_left"));
+  if (d.PL) {
+    // Policy encoder layers run on the body output before the policy
+    // "output" dense (network_execution_plan.cpp:199-200; the value and
+    // moves-left heads above have already read the body output): no
+    // residual scale, LayerNorm epsilons 1e-6 after attention and 1e-5 after
+    // the FFN (network_execution_plan.cpp:1152-1193).
+    for (const Layer &L : net->pol_layers) {
+      const int rc = encoder_layer(L, d.PH, d.PF, 1e-6f, 1e-5f, 1.0f);
+      if (rc != MFH_OK)
+        return rc;
+    }
+    // The policy rows of the fused head weight come first.
+    MFH_RUN(run(gemm("act", E, net->head_w, E, M, d.Dp, E, net->W<float>(net->head_b),
+                     d.act_default, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("pol_emb"),
+                     net->Lo("pol_emb"), d.Dp),
+                "heads"));
+  }
   MFH_RUN(run(gemm("pol_emb", d.Dp, net->qk_w, d.Dp, M, 2 * d.Dp, d.Dp,
                    net->W<float>(net->qk_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
                    net->S<std::uint16_t>("polqk"), net->Lo("polqk"), 2 * d.Dp),
@@ -990,10 +1053,6 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     // Moves-left head (reference network_execution_plan.cpp:184-190, acts
     // 1107-1111): ip_mov on square rows (default activation), flatten,
     // ip1_mov (default activation), ip2_mov + relu.
-    MFH_RUN(run(gemm("act", E, net->mov_w, E, M, d.Md, E, net->W<float>(net->mov_b),
-                     d.act_default, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("mov_emb"),
-                     net->Lo("mov_emb"), d.Md),
-                "moves_left"));
     const int mflat = kSquares * d.Md;
     auto *mov1 = net->S<float>("mov1");
     mfh::GemmParams pm = gemm("mov_emb", mflat, net->mov1_w, mflat, B, d.Mh, mflat, nullptr,
@@ -1735,6 +1794,7 @@ int mfh_weights_describe(const mfh_weights *w, mfh_weights_format *format, mfh_n
     desc->ffn_activation = f.ffn_activation;
     desc->smolgen_activation = f.smolgen_activation;
     desc->headcount = static_cast<int>(w->w.headcount);
+    desc->pol_headcount = static_cast<int>(w->w.pol_headcount);
   }
   return MFH_OK;
 }

@@ -44,6 +44,7 @@ mfh_net_desc DescFromConfig(const HipNetworkConfig &config) {
   desc.ffn_activation = config.ffn_activation;
   desc.smolgen_activation = config.smolgen_activation;
   desc.headcount = config.headcount;
+  desc.pol_headcount = config.pol_headcount;
   desc.weights_dtype = MFH_WEIGHTS_BF16;
   desc.precision = config.precision;
   desc.max_batch = config.max_batch;

@@ -39,6 +39,7 @@ struct HipNetworkConfig {
   int ffn_activation = MFH_ACTIVATION_DEFAULT;
   int smolgen_activation = MFH_ACTIVATION_SWISH;
   int headcount = 0;
+  int pol_headcount = 0;  // policy encoder heads (0 without policy encoder layers)
   int precision = MFH_PRECISION_BF16X2;
   int max_batch = 256;  // stable execution batch; larger batches are chunked
   int device = -1;

@@ -64,6 +64,8 @@ class NetSpec:
     value_dim: int = 32
     value_hidden: int = 128
     pe_map: bool = False         # static position encoding (PE_MAP) instead of PE_DENSE
+    policy_encoders: int = 0     # encoder layers in the policy head
+    policy_heads: int = 0        # their attention heads
     moves_left_dim: int = 0      # moves-left head square embedding (0: no head)
     moves_left_hidden: int = 128
     wdl: bool = True
@@ -87,6 +89,9 @@ SPECS = {
     # channels, embedding input 112 + 64) in place of the dynamic one.
     "cpu_plumbing_pe_map": NetSpec("cpu_plumbing_pe_map", 256, 2, 8, 512, pe_channels=64,
                                    input_ffn=512, policy_dim=256, pe_map=True),
+    # Test net: config 1 with one encoder layer (8 heads) in the policy head.
+    "cpu_plumbing_pol_enc": NetSpec("cpu_plumbing_pol_enc", 256, 2, 8, 512, input_ffn=512,
+                                    policy_dim=256, policy_encoders=1, policy_heads=8),
 }
 
 
@@ -139,6 +144,19 @@ def tensor_layout(spec: NetSpec):
             vec(sg + ".dense2_b", spec.heads * g, h)
             norm(sg + ".ln1", h)
             norm(sg + ".ln2", spec.heads * g)
+        norm(f"{p}.ln1", E)
+        mat(f"{p}.ffn.dense1_w", spec.ffn, E)
+        vec(f"{p}.ffn.dense1_b", spec.ffn, E)
+        mat(f"{p}.ffn.dense2_w", E, spec.ffn)
+        vec(f"{p}.ffn.dense2_b", E, spec.ffn)
+        norm(f"{p}.ln2", E)
+    for i in range(spec.policy_encoders):
+        p = f"policy.vanilla.encoder.{i}"
+        for t in ("q", "k", "v"):
+            mat(f"{p}.mha.{t}_w", E, E)
+            vec(f"{p}.mha.{t}_b", E, E)
+        mat(f"{p}.mha.dense_w", E, E)
+        vec(f"{p}.mha.dense_b", E, E)
         norm(f"{p}.ln1", E)
         mat(f"{p}.ffn.dense1_w", spec.ffn, E)
         vec(f"{p}.ffn.dense1_b", spec.ffn, E)

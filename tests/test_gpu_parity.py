@@ -413,6 +413,46 @@ def test_pe_map_static_embedding(precision, batch):
         assert _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
 
 
+@pytest.mark.parametrize("precision,batch", [("bf16x2", 16), ("bf16", 16), ("bf16x2", 3)])
+def test_policy_encoder_layers(precision, batch, tmp_path):
+    """Encoder layers inside the policy head (reference
+    network_execution_plan.cpp:192-210: on the body output, before the policy
+    "output" dense; LayerNorm eps 1e-6 / 1e-5, no residual scale) against the
+    oracle; the value head still reads the body output.  The same net read
+    back from a network file (pol_headcount from the file) gives the same
+    bits."""
+    spec = synth.SPECS["cpu_plumbing_pol_enc"]
+    weights = synth.make_weights(spec, seed=6)
+    planes, legal = synth.playout_positions(16, seed=9)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads,
+                                            policy_heads=spec.policy_heads),
+                           weights).evaluate_batch(planes)
+    net = backend.create_network(spec, weights, max_batch=batch, precision=precision)
+    out = net.evaluate_batch(planes)
+    net.close()
+    assert np.abs(out["policy"] - ref["policy"]).max() <= 2e-2
+    assert np.abs(out["wdl"] - ref["wdl"]).max() <= 5e-3
+    if precision == "bf16x2":
+        assert _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
+        layout = synth.tensor_layout(spec)
+        data = netfile.spec_net_bytes(spec, weights, layout)
+        wf = backend.parse_weights(data)
+        assert wf.pol_headcount == 0  # the writer call above sets none
+        data = netfile.net_bytes(weights, dict(network=7, policy=3, value=2, input_embedding=2,
+                                               default_activation=1, smolgen_activation=7,
+                                               ffn_activation=1), spec.heads,
+                                 pol_headcount=spec.policy_heads,
+                                 encoding={n: ("bf16" if b16 else "f32")
+                                           for n, _, _, _, b16 in layout})
+        wf = backend.parse_weights(data)
+        assert wf.pol_headcount == spec.policy_heads
+        fnet = wf.create_network(max_batch=batch)
+        got = fnet.evaluate_batch(planes)
+        fnet.close()
+        for k in ("policy", "wdl"):
+            assert np.array_equal(got[k].view(np.uint32), out[k].view(np.uint32)), k
+
+
 def test_bad_batch_rejected():
     spec = synth.SPECS["cpu_plumbing"]
     net = backend.create_network(spec, synth.make_weights(spec), max_batch=4, device=0)
