@@ -55,7 +55,8 @@ mfh_net_desc DescFromConfig(const HipNetworkConfig &config) {
 }  // namespace
 
 HipNetwork::HipNetwork(const std::vector<WeightTensor> &weights,
-                       const HipNetworkConfig &config) {
+                       const HipNetworkConfig &config)
+    : graphs_(config.graphs) {
   std::vector<mfh_tensor> tensors;
   tensors.reserve(weights.size());
   for (const auto &w : weights)
@@ -63,7 +64,8 @@ HipNetwork::HipNetwork(const std::vector<WeightTensor> &weights,
   Create(DescFromConfig(config), tensors.data(), static_cast<int>(tensors.size()));
 }
 
-HipNetwork::HipNetwork(const std::string &weights_path, const HipNetworkConfig &config) {
+HipNetwork::HipNetwork(const std::string &weights_path, const HipNetworkConfig &config)
+    : graphs_(config.graphs) {
   mfh_weights *file = nullptr;
   int rc = mfh_weights_load(weights_path.c_str(), &file);
   if (rc != MFH_OK)
@@ -90,9 +92,17 @@ HipNetwork::HipNetwork(const std::string &weights_path, const HipNetworkConfig &
 }
 
 void HipNetwork::Create(mfh_net_desc desc, const mfh_tensor *tensors, int count) {
-  const int rc = mfh_net_create(&desc, tensors, count, &net_);
+  int rc = mfh_net_create(&desc, tensors, count, &net_);
   if (rc != MFH_OK)
     throw std::runtime_error(LastError("initialisation", rc));
+  if (!graphs_) {
+    rc = mfh_net_set_graphs(net_, 0);
+    if (rc != MFH_OK) {
+      mfh_net_destroy(net_);
+      net_ = nullptr;
+      throw std::runtime_error(LastError("initialisation", rc));
+    }
+  }
   wdl_ = desc.value == MFH_VALUE_WDL;
   mlh_ = desc.moves_left == MFH_MOVES_LEFT_V1;
   max_batch_ = desc.max_batch;
@@ -226,6 +236,18 @@ BackendCapabilities HipNetwork::GetBackendCapabilities() const {
     caps.device_name = std::string(c.device_name) + " (" + c.arch_name + ")";
   }
   return caps;
+}
+
+std::unique_ptr<Network> CreateHipNetwork(const std::string &weights_path,
+                                          const BackendConfig &config) {
+  if (config.backend != "hip" && config.backend != "auto" && config.backend != "accelerator")
+    throw std::runtime_error("HIP backend cannot serve backend \"" + config.backend + "\"");
+  HipNetworkConfig hc;
+  hc.device = config.cuda_device;
+  hc.graphs = config.cuda_graph_execution;
+  if (config.cuda_stable_execution_batch_size > 0)
+    hc.max_batch = config.cuda_stable_execution_batch_size;
+  return std::make_unique<HipNetwork>(weights_path, hc);
 }
 
 }  // namespace Hip

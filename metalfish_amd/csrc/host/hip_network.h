@@ -8,6 +8,7 @@
 #pragma once
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -43,6 +44,7 @@ struct HipNetworkConfig {
   int precision = MFH_PRECISION_BF16X2;
   int max_batch = 256;  // stable execution batch; larger batches are chunked
   int device = -1;
+  bool graphs = true;   // HIP graph capture/replay of the forward
 };
 
 // Result of EvaluateBatchPriors for one position: the MCTS priors of its
@@ -88,6 +90,7 @@ private:
   void RunChunk(const InputPlanes *inputs, int count, NetworkOutput *outputs);
 
   mfh_net *net_ = nullptr;
+  bool graphs_ = true;
   bool wdl_ = true;
   bool mlh_ = false;
   std::vector<float> moves_;
@@ -97,6 +100,16 @@ private:
   std::vector<std::uint64_t> masks_;
   std::vector<float> values_;
 };
+
+// The "hip" branch of NN::CreateNetwork (reference src/nn/network.cpp:
+// 137-208, path overloads 226-258): loads a `.pb` / `.pb.gz` network file and
+// builds a HipNetwork with the BackendConfig knobs the HIP backend honours
+// (cuda_device -> device, cuda_graph_execution -> graph replay,
+// cuda_stable_execution_batch_size -> max_batch when positive).  Accepts the
+// backend names "hip", "auto" and "accelerator"; any other name throws
+// std::runtime_error, as does a file or net the backend cannot run.
+std::unique_ptr<Network> CreateHipNetwork(const std::string &weights_path,
+                                          const BackendConfig &config);
 
 }  // namespace Hip
 }  // namespace NN

@@ -4,7 +4,9 @@
 //
 // Usage: hip_network_test NET PLANES OUT HEADS PRECISION MAX_BATCH [MOVES TEMP]
 //   NET    : u32 count, then per tensor u32 name_len, name, u64 n, n floats;
-//            or a network file ending in ".pb" / ".pb.gz" (HEADS unused)
+//            or a network file ending in ".pb" / ".pb.gz" (HEADS unused;
+//            built through CreateHipNetwork with backend $MFH_TEST_BACKEND,
+//            default "hip")
 //   PLANES : u32 batch, then batch*112*64 floats
 //   OUT    : batch*(1858+3+1) floats from EvaluateBatch, then the same for
 //            Evaluate of each position; with MOVES, then the priors of
@@ -96,10 +98,19 @@ int main(int argc, char **argv) {
     config.headcount = std::atoi(argv[4]);
     config.precision = std::string(argv[5]) == "bf16" ? MFH_PRECISION_BF16 : MFH_PRECISION_BF16X2;
     config.max_batch = std::atoi(argv[6]);
-    std::unique_ptr<Hip::HipNetwork> owner =
-        net_file ? std::make_unique<Hip::HipNetwork>(net_path, config)
-                 : std::make_unique<Hip::HipNetwork>(weights, config);
-    Hip::HipNetwork &net = *owner;
+    // Network files go through the factory branch, with the backend name
+    // from MFH_TEST_BACKEND (default "hip").
+    std::unique_ptr<Network> owner;
+    if (net_file) {
+      BackendConfig bc;
+      const char *backend = std::getenv("MFH_TEST_BACKEND");
+      bc.backend = backend ? backend : "hip";
+      bc.cuda_stable_execution_batch_size = config.max_batch;
+      owner = Hip::CreateHipNetwork(net_path, bc);
+    } else {
+      owner = std::make_unique<Hip::HipNetwork>(weights, config);
+    }
+    Hip::HipNetwork &net = dynamic_cast<Hip::HipNetwork &>(*owner);
     std::fprintf(stderr, "%s\n", net.GetNetworkInfo().c_str());
     const BackendCapabilities caps = net.GetBackendCapabilities();
     if (caps.actual_backend != "hip" || !caps.has_wdl || caps.max_batch_size != config.max_batch)

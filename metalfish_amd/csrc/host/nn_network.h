@@ -46,6 +46,17 @@ struct BackendCapabilities {
   std::string compute_units;
 };
 
+struct BackendConfig {
+  std::string backend = "auto";
+  std::string coreml_model_path;
+  std::string coreml_compute_units = "cpu-ne";
+  int cuda_device = -1;
+  bool cuda_graph_execution = true;
+  int cuda_stable_execution_batch_size = 0;
+  bool cuda_deterministic_attention_softmax = true;
+  bool cuda_full_buffer_clear = true;
+};
+
 class Network {
 public:
   virtual ~Network() = default;

@@ -98,10 +98,14 @@ def test_adapter_file_errors_without_a_device(tmp_path, plumbing):
     proc = subprocess.run([DRIVER, str(bad), pl, out, "0", "bf16x2", "8"], capture_output=True,
                           text=True, timeout=300)
     assert proc.returncode == 3 and "bad magic number" in proc.stderr, proc.stderr
-    if backend.device_count() > 0:
-        return
     good = tmp_path / "net.pb.gz"
     _write_pb(good, spec, weights)
+    # The factory serves "hip", "auto" and "accelerator" only.
+    proc = subprocess.run([DRIVER, str(good), pl, out, "0", "bf16x2", "8"], capture_output=True,
+                          text=True, timeout=300, env={**os.environ, "MFH_TEST_BACKEND": "cuda"})
+    assert proc.returncode == 3 and 'cannot serve backend "cuda"' in proc.stderr, proc.stderr
+    if backend.device_count() > 0:
+        return
     proc = subprocess.run([DRIVER, str(good), pl, out, "0", "bf16x2", "8"], capture_output=True,
                           text=True, timeout=300)
     # The file loads; creating the net needs the device.

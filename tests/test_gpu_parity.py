@@ -453,6 +453,37 @@ def test_policy_encoder_layers(precision, batch, tmp_path):
             assert np.array_equal(got[k].view(np.uint32), out[k].view(np.uint32)), k
 
 
+def test_concurrent_callers_share_one_net():
+    """Several threads evaluating on one net at once (MCTS workers calling
+    the backend concurrently, reference search.cpp:433 and
+    backend_adapter.cpp:244-276) each get exactly their serial results: calls
+    serialise on the net (cuda_network.cpp:442) around the shared staging
+    buffers.  ctypes releases the GIL, so the calls overlap in the library."""
+    import threading
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=0)
+    net = backend.create_network(spec, weights, max_batch=8)
+    sets = [synth.playout_positions(8, seed=40 + i)[0] for i in range(4)]
+    serial = [net.eval_planes(p) for p in sets]
+    bad = []
+
+    def worker(i):
+        for _ in range(6):
+            pol, val = net.eval_planes(sets[i])
+            if not (np.array_equal(pol.view(np.uint32), serial[i][0].view(np.uint32)) and
+                    np.array_equal(val.view(np.uint32), serial[i][1].view(np.uint32))):
+                bad.append(i)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    net.close()
+    assert not any(t.is_alive() for t in threads)
+    assert not bad, bad
+
+
 def test_bad_batch_rejected():
     spec = synth.SPECS["cpu_plumbing"]
     net = backend.create_network(spec, synth.make_weights(spec), max_batch=4, device=0)
