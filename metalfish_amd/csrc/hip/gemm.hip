@@ -572,13 +572,25 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   const int kslice = p.K / p.k_splits;
   // Tile choice measured on MI355X at the BT4 body shapes (M = 16384): for
   // K <= 1024, eight waves per workgroup on BK = 32 steps (split precision
-  // 128 x 128 tiles as 2 x 4 waves, bf16 256 x 128 tiles as 4 x 2 waves,
-  // 48 KiB of LDS for two stages); for longer K, four waves on BK = 64
-  // (split 64 x 128, bf16 128 x 128).
+  // 128 x 128 tiles as 2 x 4 waves with two 48 KiB stages, bf16 256 x 128
+  // tiles as 4 x 2 waves with three 24 KiB stages); for longer K, four waves
+  // on BK = 64 (split 64 x 128, bf16 128 x 128).
+  // Whole rounds of 256 workgroups: 256 x 256 tiles of eight waves (4 x 2,
+  // 64 x 128 per wave) and a three-stage (split) or four-stage (bf16) LDS
+  // ring, 144 / 128 KiB, one workgroup per CU.  They halve the L2 traffic
+  // per MFMA of the 128-wide tiles; measured faster in the forward on the
+  // out-projection, FFN2 and smolgen-global shapes, slower on QKV (832 tiles,
+  // a partial last round) and FFN1 (384).  bf16 weights only (the fp8 path
+  // keeps two stages).
+  const long big_tiles = static_cast<long>((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (large && !p.W8 && p.k_splits == 1 && big_tiles % 256 == 0)
+    return split ? LaunchW<256, 256, 32, 3, 4, 2, true, false>(p, stream)
+                 : LaunchW<256, 256, 32, 4, 4, 2, false, false>(p, stream);
   if (large && kslice % 64 == 0) {
     if (kslice <= 1024)
       return split ? Launch<128, 128, 32, 2, 2, 4, true>(p, stream)
-                   : Launch<256, 128, 32, 2, 4, 2, false>(p, stream);
+             : p.W8 ? Launch<256, 128, 32, 2, 4, 2, false>(p, stream)
+                    : LaunchW<256, 128, 32, 3, 4, 2, false, false>(p, stream);
     return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
                  : Launch<128, 128, 64, 2, 2, 2, false>(p, stream);
   }
