@@ -89,18 +89,46 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
   float v[4];
   if constexpr (MODE == GEMM_OUT_RESID_F32) {
     float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
-    const float *res = p.resid + static_cast<size_t>(row) * p.ldr + col;
-    if (full) {
-      const f32x4 rv = *reinterpret_cast<const f32x4 *>(res);
+    const size_t roff = static_cast<size_t>(row) * p.ldr + col;
+    float rv[4];
+    if (p.resid16) {
+      // Split residual: hi + lo bf16 planes.
+      if (full) {
+        const u32x2 h = *reinterpret_cast<const u32x2 *>(p.resid16 + roff);
+        const u32x2 l = *reinterpret_cast<const u32x2 *>(p.resid16_lo + roff);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const unsigned hw = h[r >> 1], lw = l[r >> 1];
+          rv[r] = __uint_as_float((r & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
+                  __uint_as_float((r & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          rv[r] = col + r < p.N
+                      ? bf16_to_f32(p.resid16[roff + r]) + bf16_to_f32(p.resid16_lo[roff + r])
+                      : 0.f;
+      }
+    } else if (full) {
+      const f32x4 x = *reinterpret_cast<const f32x4 *>(p.resid + roff);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        v[r] = rv[r] + p.alpha * (acc[r] + b[r]);
+        rv[r] = x[r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        rv[r] = col + r < p.N ? p.resid[roff + r] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      v[r] = rv[r] + p.alpha * (acc[r] + b[r]);
+    if (full) {
       *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (col + r < p.N)
-          c[r] = res[r] + p.alpha * (acc[r] + b[r]);
+          c[r] = v[r];
     }
   } else {
 #pragma unroll
@@ -514,8 +542,14 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       (p.A_lo && !Aligned(p.A_lo, 16)) || p.lda % 8 || p.ldw % 8 || p.lda < p.K ||
       p.ldw < p.K)
     return fail("operands must be 16-byte aligned with ld >= K, ld % 8 == 0");
-  if (p.out_mode == GEMM_OUT_RESID_F32 && (!p.resid || p.split_n < p.N))
-    return fail("residual mode needs resid and no split");
+  if (p.out_mode == GEMM_OUT_RESID_F32 &&
+      ((!p.resid && !p.resid16) || (p.resid && p.resid16) ||
+       (p.resid16 != nullptr) != (p.resid16_lo != nullptr) || p.split_n < p.N))
+    return fail("residual mode needs resid (fp32) or resid16 + resid16_lo (split), and no "
+                "split output");
+  if (p.out_mode == GEMM_OUT_RESID_F32 && p.resid16 &&
+      (!Aligned(p.resid16, 2) || !Aligned(p.resid16_lo, 2)))
+    return fail("split residual planes must be 2-byte aligned");
   if (p.split_n < p.N && (!p.C2 || p.ldc2 < p.N - p.split_n || p.split_n % 4))
     return fail("split output needs C2 wide enough and split_n % 4 == 0");
   if (p.split_n < p.N && (p.C_lo != nullptr) != (p.C2_lo != nullptr))
@@ -529,7 +563,9 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   p.vec = Aligned(p.C, vb) && p.ldc % 4 == 0 && (!p.C_lo || Aligned(p.C_lo, vb)) &&
           (p.split_n >= p.N ||
            (Aligned(p.C2, vb) && p.ldc2 % 4 == 0 && (!p.C2_lo || Aligned(p.C2_lo, vb)))) &&
-          (p.out_mode != GEMM_OUT_RESID_F32 || (Aligned(p.resid, 16) && p.ldr % 4 == 0));
+          (p.out_mode != GEMM_OUT_RESID_F32 ||
+           (p.ldr % 4 == 0 && (p.resid16 ? Aligned(p.resid16, 8) && Aligned(p.resid16_lo, 8)
+                                          : Aligned(p.resid, 16))));
   const bool split = p.A_lo != nullptr;
   const bool large = p.M >= 2048 && p.N >= 128;
   // Small problems (few positions): 64 x 64 tiles leave most CUs idle and

@@ -856,6 +856,11 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   auto *pe = net->S<float>("pe");
   auto *pre = net->S<float>("pre");
   auto *resid = net->S<float>("resid");
+  // In the split precisions a LayerNorm's hi + lo output planes ("act") are
+  // both the next GEMM's input and the residual of the next residual GEMM,
+  // so its fp32 copy is written only where something reads it: the bf16
+  // precision's residual, and the body output (debug tensor "body").
+  float *res32 = d.split ? nullptr : resid;
   auto *sg1 = net->S<float>("sg1");
   auto *sg2 = net->S<float>("sg2");
   auto *val1 = net->S<float>("val1");
@@ -886,7 +891,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
                   "embedding"));
   {
     mfh::LayerNormParams lp = ln(pre, M, E, d.eps_emb, net->W<float>(net->emb_ln_g),
-                                 net->W<float>(net->emb_ln_b), resid, "act");
+                                 net->W<float>(net->emb_ln_b), res32, "act");
     lp.mult_gate = net->mult_gate ? net->W<float>(net->mult_gate) : nullptr;
     lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;
     MFH_RUN(run_ln(lp));
@@ -895,7 +900,12 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
                            const float *bias, const char *role, float alpha) {
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
-    p.resid = resid;
+    if (d.split) {
+      p.resid16 = net->S<std::uint16_t>("act");
+      p.resid16_lo = net->Lo("act");
+    } else {
+      p.resid = resid;
+    }
     p.ldr = E;
     p.alpha = alpha;
     return run(p, role);
@@ -908,14 +918,14 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     MFH_RUN(residual_gemm("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
                           "input_ffn2", d.alpha));
     MFH_RUN(run_ln(ln(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
-                      net->W<float>(net->in_ln_b), resid, "act")));
+                      net->W<float>(net->in_ln_b), res32, "act")));
   }
 
   // One encoder layer (cpu_network.cpp:1027-1266, 1318-1457) on resid/act:
   // `heads` attention heads, FFN width `ffn`, LayerNorm epsilons after the
   // attention and the FFN, residual scale alpha.
   auto encoder_layer = [&](const Layer &L, int heads, int ffn, float eps_attn, float eps_ffn,
-                           float alpha) -> int {
+                           float alpha, bool body_out) -> int {
     mfh::GemmParams p = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen ? d.C : 0), E,
                              net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
                              net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
@@ -978,17 +988,18 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     }
     MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha));
     MFH_RUN(run_ln(ln(pre, M, E, eps_attn, net->W<float>(L.ln1_g), net->W<float>(L.ln1_b),
-                      resid, "act")));
+                      res32, "act")));
     MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b), d.act_ffn,
                      mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), ffn),
                 "ffn1"));
     MFH_RUN(residual_gemm("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha));
     MFH_RUN(run_ln(ln(pre, M, E, eps_ffn, net->W<float>(L.ln2_g), net->W<float>(L.ln2_b),
-                      resid, "act")));
+                      body_out ? resid : res32, "act")));
     return MFH_OK;
   };
   for (const Layer &L : net->layers) {
-    const int rc = encoder_layer(L, d.H, d.F, d.eps_body, d.eps_body, d.alpha);
+    const int rc = encoder_layer(L, d.H, d.F, d.eps_body, d.eps_body, d.alpha,
+                                 &L == &net->layers.back());
     if (rc != MFH_OK)
       return rc;
   }
@@ -1016,7 +1027,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     // residual scale, LayerNorm epsilons 1e-6 after attention and 1e-5 after
     // the FFN (network_execution_plan.cpp:1152-1193).
     for (const Layer &L : net->pol_layers) {
-      const int rc = encoder_layer(L, d.PH, d.PF, 1e-6f, 1e-5f, 1.0f);
+      const int rc = encoder_layer(L, d.PH, d.PF, 1e-6f, 1e-5f, 1.0f, false);
       if (rc != MFH_OK)
         return rc;
     }

@@ -30,6 +30,10 @@ enum GemmOut : int {
   GEMM_OUT_F32 = 1,        // C = act(A.W^T + b) as fp32
   GEMM_OUT_RESID_F32 = 2,  // C = resid + alpha * (A.W^T + b) as fp32
 };
+// The residual of GEMM_OUT_RESID_F32 is fp32 `resid`, or, when resid16 is
+// set, the split pair resid16 + resid16_lo (bf16 hi and lo planes, same ldr):
+// the split-precision activation that the previous LayerNorm wrote for the
+// next layer's input.
 
 // C[M,N] = A[M,K] . W[N,K]^T with bf16 operands and fp32 accumulation.
 // Columns >= split_n are written to C2 (column index minus split_n) so one
@@ -59,6 +63,8 @@ struct GemmParams {
   int ldc2 = 0;
   int split_n = 1 << 30;
   const float *resid = nullptr;
+  const std::uint16_t *resid16 = nullptr;
+  const std::uint16_t *resid16_lo = nullptr;
   int ldr = 0;
   float alpha = 1.0f;
   // K split over blockIdx.y; each slice writes fp32 partials to
