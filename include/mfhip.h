@@ -315,6 +315,23 @@ int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A,
                         const uint16_t *W, const float *bias, int act,
                         float *C);
 
+/* Row-panel GEMM (the kernel behind the batch >= 128 residual + LayerNorm
+ * steps, reference cpu_network.cpp:1256-1259 / 1318-1397 then 1399-1457) on
+ * host arrays, for tests.  A [M,K] bf16 bits (A_lo: optional split-precision
+ * lo plane), weights W [N,K] bf16 bits or W8 e4m3 codes with wscale[N].
+ * layernorm = 0: out = act(A.W^T + bias) as bf16 hi (+ lo) planes.
+ * layernorm = 1: out = LN(resid + alpha (A.W^T + bias)) with gamma, beta,
+ * eps over each row of N, residual fp32 resid32 or the pair resid_hi +
+ * resid_lo; bf16 hi (+ lo) planes and optionally fp32 out_f32. */
+int mfh_debug_panel_gemm(int M, int N, int K, const uint16_t *A,
+                         const uint16_t *A_lo, const uint16_t *W,
+                         const uint8_t *W8, const float *wscale,
+                         const float *bias, int act, int layernorm,
+                         const float *resid32, const uint16_t *resid_hi,
+                         const uint16_t *resid_lo, float alpha, float eps,
+                         const float *gamma, const float *beta,
+                         uint16_t *out_hi, uint16_t *out_lo, float *out_f32);
+
 /* Copies a named workspace tensor left by the last eval call to host
  * memory: "body" (fp32 [B*64,E], encoder output; with no encoder layers
  * the input-embedding output) or "policy_qk" (bf16 [B*64,2Dp], the hi plane

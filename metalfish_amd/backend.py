@@ -31,7 +31,7 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_net_set_graphs", "mfh_net_set_profiling", "mfh_net_profile",
            "mfh_net_profile_reset",
            "mfh_pack_planes", "mfh_device_count", "mfh_last_error", "mfh_debug_unpack_planes",
-           "mfh_debug_gemm_bf16", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8",
+           "mfh_debug_gemm_bf16", "mfh_debug_panel_gemm", "mfh_net_debug_tensor", "mfh_debug_quantize_fp8",
            "mfh_weights_load", "mfh_weights_parse", "mfh_weights_describe",
            "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
            "mfh_net_eval_priors", "mfh_net_eval_priors_device",
@@ -97,6 +97,8 @@ def lib():
             "mfh_last_error": ([], ctypes.c_char_p),
             "mfh_debug_unpack_planes": ([i, vp, vp, vp], i),
             "mfh_debug_gemm_bf16": ([i, i, i, vp, vp, vp, i, vp], i),
+            "mfh_debug_panel_gemm": ([i, i, i, vp, vp, vp, vp, vp, vp, i, i, vp, vp, vp,
+                                      ctypes.c_float, ctypes.c_float, vp, vp, vp, vp, vp], i),
             "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
             "mfh_debug_quantize_fp8": ([i, i, vp, vp, vp], i),
             "mfh_weights_load": ([ctypes.c_char_p, ctypes.POINTER(vp)], i),
@@ -367,6 +369,32 @@ def gemm_bf16(a_bits, w_bits, bias=None, act="none"):
     _check(lib().mfh_debug_gemm_bf16(m, n, k, _ptr(a_bits), _ptr(w_bits), _ptr(b),
                                      ACTIVATION[act], _ptr(out)), "mfh_debug_gemm_bf16")
     return out
+
+
+def panel_gemm(a_bits, w_bits=None, a_lo_bits=None, w8_codes=None, wscale=None, bias=None,
+               act="none", layernorm=None):
+    """Row-panel GEMM through mfh_debug_panel_gemm (a test hook).  Without
+    ``layernorm``: act(A.W^T + b) as (hi, lo) bf16 bit planes.  With
+    ``layernorm`` = dict(gamma, beta, eps, alpha, resid32 | resid_hi +
+    resid_lo): LN(resid + alpha (A.W^T + b)) as (hi, lo, fp32)."""
+    u16 = lambda x: None if x is None else np.ascontiguousarray(x, dtype=np.uint16)
+    f32 = lambda x: None if x is None else np.ascontiguousarray(x, dtype=np.float32)
+    a_bits, a_lo_bits, w_bits = u16(a_bits), u16(a_lo_bits), u16(w_bits)
+    w8 = None if w8_codes is None else np.ascontiguousarray(w8_codes, dtype=np.uint8)
+    m, k = a_bits.shape
+    n = (w_bits if w_bits is not None else w8).shape[0]
+    hi = np.zeros((m, n), np.uint16)
+    lo = np.zeros((m, n), np.uint16)
+    ln = layernorm or {}
+    y32 = np.zeros((m, n), np.float32) if layernorm is not None else None
+    keep = [f32(wscale), f32(bias), f32(ln.get("resid32")), u16(ln.get("resid_hi")),
+            u16(ln.get("resid_lo")), f32(ln.get("gamma")), f32(ln.get("beta"))]
+    _check(lib().mfh_debug_panel_gemm(
+        m, n, k, _ptr(a_bits), _ptr(a_lo_bits), _ptr(w_bits), _ptr(w8), _ptr(keep[0]),
+        _ptr(keep[1]), ACTIVATION[act], 1 if layernorm is not None else 0, _ptr(keep[2]),
+        _ptr(keep[3]), _ptr(keep[4]), float(ln.get("alpha", 1.0)), float(ln.get("eps", 1e-3)),
+        _ptr(keep[5]), _ptr(keep[6]), _ptr(hi), _ptr(lo), _ptr(y32)), "mfh_debug_panel_gemm")
+    return (hi, lo, y32) if layernorm is not None else (hi, lo)
 
 
 def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",

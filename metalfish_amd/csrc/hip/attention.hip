@@ -37,7 +37,6 @@ constexpr int kHeadsPerBlock = 4;
 // depths d and d + 16 land on different banks.
 constexpr int kVtStride = kSq + 8;
 
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 Mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

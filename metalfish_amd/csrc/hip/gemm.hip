@@ -37,10 +37,6 @@
 namespace mfh {
 namespace {
 
-#define MFH_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
-
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
 // Element offset of 16-byte chunk `chunk` of LDS row `row` (rows of BK bf16).
 // BK = 64: 8 chunks per 128-byte row, XOR with row & 7.  BK = 32: two rows
 // per 128 bytes, XOR with (row >> 1) & 3, so rows r..r+7 cover all eight
@@ -51,25 +47,6 @@ __device__ __forceinline__ int Swz(int row, int chunk) {
     return row * 64 + ((chunk ^ (row & 7)) << 3);
   else
     return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3);
-}
-
-// Eight e4m3 codes (bytes of q, lowest first) as eight bf16 values; exact.
-__device__ __forceinline__ bf16x8 Fp8x8ToBf16(u32x2 q) {
-  const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, false);
-  const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, true);
-  const auto c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, false);
-  const auto d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, true);
-  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// Activation with a compile-time kind; ACT_RUNTIME defers to p.act.
-constexpr int ACT_RUNTIME = -2;
-template <int ACT>
-__device__ __forceinline__ float Act(float v, int runtime_act) {
-  if constexpr (ACT == ACT_RUNTIME)
-    return activate(v, runtime_act);
-  else
-    return activate(v, ACT);
 }
 
 // Epilogue for four consecutive outputs (row, col .. col + 3) of C, given

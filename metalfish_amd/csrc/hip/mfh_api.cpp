@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -27,6 +28,7 @@
 #include <sstream>
 #include <string>
 #include <tuple>
+#include <stdexcept>
 #include <vector>
 
 #include "../host/policy_tables.h"
@@ -771,6 +773,18 @@ int CollectProfile(mfh_net *net) {
   return MFH_OK;
 }
 
+// Smallest token-row count (positions x 64) at which residual GEMMs run as
+// row-panel GEMMs with the LayerNorm fused; below it the tiled (and, for few
+// positions, split-K) GEMM plus the LayerNorm kernel fill the GPU better.
+// MFH_PANEL_MIN_ROWS overrides it (tuning).
+int PanelMinRows() {
+  static const int rows = [] {
+    const char *env = std::getenv("MFH_PANEL_MIN_ROWS");
+    return env ? std::atoi(env) : 8192;
+  }();
+  return rows;
+}
+
 // Profiler name of a GEMM launch: "gemm_bf16:<role>", or
 // "gemm_bf16_splitk:<role>" when the caller splits K (partials summed by the
 // consumer).
@@ -910,15 +924,67 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     p.alpha = alpha;
     return run(p, role);
   };
+  // Residual GEMM followed by its LayerNorm, y = LN(x + alpha (A.W^T + b)),
+  // onto the "act" planes (and y32 when set).  At large batches one
+  // row-panel launch does both, the pre-LayerNorm rows never leaving the
+  // workgroup; otherwise the tiled GEMM writes them to `pre` for the
+  // LayerNorm kernel.
+  auto residual_ln = [&](const std::string &a, int k, const size_t (&w_off)[2],
+                         const float *bias, const char *role, float alpha, float eps,
+                         const float *g, const float *b, float *y32) -> int {
+    if (M >= PanelMinRows() && mfh::PanelGemmShapeOk(mfh::PANEL_OUT_LN, E, k)) {
+      mfh::PanelGemmParams pp;
+      pp.A = net->S<std::uint16_t>(a);
+      pp.A_lo = net->Lo(a);
+      pp.lda = k;
+      if (net->fp8) {
+        pp.W8 = net->W<std::uint8_t>(w_off[0]);
+        pp.wscale = net->W<float>(w_off[1]);
+      } else {
+        pp.W = net->W<std::uint16_t>(w_off[0]);
+      }
+      pp.ldw = k;
+      pp.M = M;
+      pp.N = E;
+      pp.K = k;
+      pp.bias = bias;
+      pp.out_mode = mfh::PANEL_OUT_LN;
+      pp.C = net->S<std::uint16_t>("act");
+      pp.C_lo = net->Lo("act");
+      pp.ldc = E;
+      if (d.split) {
+        pp.resid16 = pp.C;
+        pp.resid16_lo = pp.C_lo;
+      } else {
+        pp.resid = resid;
+      }
+      pp.alpha = alpha;
+      pp.eps = eps;
+      pp.gamma = g;
+      pp.beta = b;
+      pp.y_f32 = y32;
+      const double flops = 2.0 * M * E * k;
+      const double bytes = 2.0 * M * k * (pp.A_lo ? 2.0 : 1.0) + (pp.W8 ? 1.0 : 2.0) * E * k +
+                           2.0 * (2.0 * plane_mult * M * E) + (y32 ? 4.0 * M * E : 0.0) +
+                           (d.split ? 0.0 : 4.0 * M * E);
+      StageTimer t(net, st, std::string("gemm_bf16:") + role, flops, bytes);
+      const hipError_t e = mfh::LaunchPanelGemm(pp, st, &err_);
+      return e == hipSuccess ? MFH_OK : fail(e);
+    }
+    MFH_RUN(residual_gemm(a, k, w_off, bias, role, alpha));
+    MFH_RUN(run_ln(ln(pre, M, E, eps, g, b, y32, "act")));
+    return MFH_OK;
+  };
   if (d.input_ffn) {
     MFH_RUN(run(gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
                      d.act_ffn, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"),
                      net->Lo("hid"), d.Fi),
                 "input_ffn1"));
-    MFH_RUN(residual_gemm("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
-                          "input_ffn2", d.alpha));
-    MFH_RUN(run_ln(ln(pre, M, E, 1e-3f, net->W<float>(net->in_ln_g),
-                      net->W<float>(net->in_ln_b), res32, "act")));
+    const int rc = residual_ln("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
+                               "input_ffn2", d.alpha, 1e-3f, net->W<float>(net->in_ln_g),
+                               net->W<float>(net->in_ln_b), res32);
+    if (rc != MFH_OK)
+      return rc;
   }
 
   // One encoder layer (cpu_network.cpp:1027-1266, 1318-1457) on resid/act:
@@ -986,16 +1052,16 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       StageTimer t(net, st, "attention", flops, bytes);
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
     }
-    MFH_RUN(residual_gemm("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha));
-    MFH_RUN(run_ln(ln(pre, M, E, eps_attn, net->W<float>(L.ln1_g), net->W<float>(L.ln1_b),
-                      res32, "act")));
+    int rc = residual_ln("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha, eps_attn,
+                         net->W<float>(L.ln1_g), net->W<float>(L.ln1_b), res32);
+    if (rc != MFH_OK)
+      return rc;
     MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b), d.act_ffn,
                      mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), ffn),
                 "ffn1"));
-    MFH_RUN(residual_gemm("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha));
-    MFH_RUN(run_ln(ln(pre, M, E, eps_ffn, net->W<float>(L.ln2_g), net->W<float>(L.ln2_b),
-                      body_out ? resid : res32, "act")));
-    return MFH_OK;
+    rc = residual_ln("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, eps_ffn,
+                     net->W<float>(L.ln2_g), net->W<float>(L.ln2_b), body_out ? resid : res32);
+    return rc;
   };
   for (const Layer &L : net->layers) {
     const int rc = encoder_layer(L, d.H, d.F, d.eps_body, d.eps_body, d.alpha,
@@ -1880,3 +1946,84 @@ int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A, const uint16_t *
 }
 
 }  // extern "C"
+
+// Device copies of host arrays for the debug entry points; frees on exit.
+struct DebugBuffers {
+  std::vector<void *> ptrs;
+  ~DebugBuffers() {
+    for (void *q : ptrs)
+      (void)hipFree(q);
+  }
+  // Device buffer of `bytes`, filled from `host` when given; null for a null
+  // host array when `keep_null`.
+  template <typename T>
+  T *Put(const T *host, size_t count, bool keep_null = true) {
+    if (!host && keep_null)
+      return nullptr;
+    void *d = nullptr;
+    if (hipMalloc(&d, count * sizeof(T)) != hipSuccess)
+      throw std::runtime_error("hipMalloc failed");
+    ptrs.push_back(d);
+    if (host && hipMemcpy(d, host, count * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+      throw std::runtime_error("copy to device failed");
+    return static_cast<T *>(d);
+  }
+};
+
+int mfh_debug_panel_gemm(int M, int N, int K, const uint16_t *A, const uint16_t *A_lo,
+                         const uint16_t *W, const uint8_t *W8, const float *wscale,
+                         const float *bias, int act, int layernorm, const float *resid32,
+                         const uint16_t *resid_hi, const uint16_t *resid_lo, float alpha,
+                         float eps, const float *gamma, const float *beta, uint16_t *out_hi,
+                         uint16_t *out_lo, float *out_f32) {
+  if (M <= 0 || N <= 0 || K <= 0 || !A || !out_hi)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_panel_gemm: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  const size_t na = static_cast<size_t>(M) * K, nw = static_cast<size_t>(N) * K,
+               nc = static_cast<size_t>(M) * N;
+  try {
+    DebugBuffers buf;
+    mfh::PanelGemmParams p;
+    p.A = buf.Put(A, na);
+    p.A_lo = buf.Put(A_lo, na);
+    p.lda = K;
+    p.W = buf.Put(W, nw);
+    p.W8 = buf.Put(W8, nw);
+    p.wscale = buf.Put(wscale, N);
+    p.ldw = K;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.bias = buf.Put(bias, N);
+    p.act = ActFromProto(act, mfh::ACT_RELU);
+    if (act == MFH_ACTIVATION_NONE || act == MFH_ACTIVATION_DEFAULT)
+      p.act = mfh::ACT_NONE;
+    p.out_mode = layernorm ? mfh::PANEL_OUT_LN : mfh::PANEL_OUT_BF16;
+    p.C = buf.Put<std::uint16_t>(nullptr, nc, false);
+    p.C_lo = out_lo ? buf.Put<std::uint16_t>(nullptr, nc, false) : nullptr;
+    p.ldc = N;
+    if (layernorm) {
+      p.resid = buf.Put(resid32, nc);
+      p.resid16 = buf.Put(resid_hi, nc);
+      p.resid16_lo = buf.Put(resid_lo, nc);
+      p.alpha = alpha;
+      p.eps = eps;
+      p.gamma = buf.Put(gamma, N);
+      p.beta = buf.Put(beta, N);
+      p.y_f32 = out_f32 ? buf.Put<float>(nullptr, nc, false) : nullptr;
+    }
+    std::string err;
+    if (mfh::LaunchPanelGemm(p, nullptr, &err) != hipSuccess)
+      return SetError(MFH_ERR_INVALID, err);
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out_hi, p.C, nc * 2, hipMemcpyDeviceToHost) != hipSuccess ||
+        (out_lo && hipMemcpy(out_lo, p.C_lo, nc * 2, hipMemcpyDeviceToHost) != hipSuccess) ||
+        (p.y_f32 && hipMemcpy(out_f32, p.y_f32, nc * 4, hipMemcpyDeviceToHost) != hipSuccess))
+      return SetError(MFH_ERR_HIP, "panel gemm execution failed");
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_HIP, e.what());
+  }
+  return MFH_OK;
+}

@@ -13,6 +13,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_to_f32(std::uint16_t h) {
   return __uint_as_float(static_cast<std::uint32_t>(h) << 16);
@@ -60,6 +61,31 @@ __device__ __forceinline__ float activate(float x, int act) {
     return x;
   }
 }
+
+// Activation with a compile-time kind; ACT_RUNTIME defers to the runtime
+// id passed as the second argument.
+constexpr int ACT_RUNTIME = -2;
+template <int ACT>
+__device__ __forceinline__ float Act(float v, int runtime_act) {
+  if constexpr (ACT == ACT_RUNTIME)
+    return activate(v, runtime_act);
+  else
+    return activate(v, ACT);
+}
+
+// Eight OCP e4m3 codes (bytes of q, lowest first) as eight bf16 values;
+// exact, since every e4m3 value is a bf16 value.
+__device__ __forceinline__ bf16x8 Fp8x8ToBf16(u32x2 q) {
+  const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, false);
+  const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], 1.0f, true);
+  const auto c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, false);
+  const auto d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Generic pointer to LDS memory as the address-space-3 pointer that the
+// direct global->LDS load builtin takes.
+#define MFH_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
 
 // Wave-wide (64 lanes) reductions.
 __device__ __forceinline__ float wave_sum(float v) {

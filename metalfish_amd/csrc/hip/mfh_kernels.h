@@ -80,6 +80,54 @@ struct GemmParams {
 
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
 
+// Row-panel GEMM: one workgroup of eight waves owns 64 whole output rows
+// and a panel of 128 * TN columns (TN = 2, 4, 6 or 8), so a row's outputs
+// never leave the workgroup.  The activation panel goes through LDS (every
+// wave reads all 64 rows); each wave streams its own 16 * TN weight rows
+// from L2 straight into registers, one K step ahead.  Two epilogues:
+//   PANEL_OUT_BF16: C = act(A.W^T + b) as bf16 (+ lo plane), row stride ldc;
+//   PANEL_OUT_LN:   y = LayerNorm(resid + alpha * (A.W^T + b)) over the N
+//                   columns of each row (N = 128 * TN, one column panel):
+//                   mean = sum/N, var = sum(x^2)/N - mean^2 clamped at 0,
+//                   y = (x - mean) / sqrt(var + eps) * gamma + beta
+//                   (reference cpu_network.cpp:424-460, 1399-1457), written
+//                   as bf16 hi (+ lo) planes to C / C_lo (ldc = N) and
+//                   optionally fp32 to y_f32.  The residual is fp32 `resid`
+//                   or the split pair resid16 + resid16_lo, stride N; it may
+//                   alias the outputs (each element is read before the
+//                   workgroup's statistics barrier and written after it by
+//                   the same lane).
+// Operands as GemmParams (A / A_lo K-contiguous, W bf16 or W8 e4m3 codes
+// with row scales).  Constraints, checked by LaunchPanelGemm: M >= 1;
+// K % 64 == 0 and K >= 128; N a multiple of the panel width.
+enum PanelOut : int { PANEL_OUT_BF16 = 0, PANEL_OUT_LN = 1 };
+struct PanelGemmParams {
+  const std::uint16_t *A = nullptr;
+  const std::uint16_t *A_lo = nullptr;
+  int lda = 0;
+  const std::uint16_t *W = nullptr;
+  const std::uint8_t *W8 = nullptr;
+  const float *wscale = nullptr;
+  int ldw = 0;
+  int M = 0, N = 0, K = 0;
+  const float *bias = nullptr;
+  int act = -1;
+  int out_mode = PANEL_OUT_BF16;
+  std::uint16_t *C = nullptr;
+  std::uint16_t *C_lo = nullptr;
+  int ldc = 0;
+  const float *resid = nullptr;
+  const std::uint16_t *resid16 = nullptr;
+  const std::uint16_t *resid16_lo = nullptr;
+  float alpha = 1.0f;
+  float eps = 1e-3f;
+  const float *gamma = nullptr, *beta = nullptr;
+  float *y_f32 = nullptr;
+};
+// True when LaunchPanelGemm takes this shape (panel width for N exists).
+bool PanelGemmShapeOk(int out_mode, int N, int K);
+hipError_t LaunchPanelGemm(const PanelGemmParams &p, hipStream_t stream, std::string *err);
+
 // Packed planes -> embedding input rows and the dynamic-PE input.
 //   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values; with static_pe
 //   ([64][pe_ch] fp32, PE_MAP nets) cols 112..111+pe_ch the square's table

@@ -102,7 +102,6 @@ __global__ void ScatterPeKernel(const float *__restrict__ pe, int batch, int pe_
 // var = E[x^2] - mean^2 clamped at 0, inv_std = 1 / sqrt(var + eps)
 // (cpu_network.cpp:424-460).  Loads are 16 bytes, stores 16 (fp32) or 8
 // (bf16) bytes per lane.
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 template <int T, int NV>
 __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {

@@ -65,16 +65,24 @@ def test_row_quantisation_library_matches_numpy():
     assert np.allclose(deq3, deq, rtol=2 ** -22, atol=0)
 
 
-def _fp8_parity(spec_name, n, seed=0):
+def _fp8_parity(spec_name, n, seed=0, batch=None):
+    """Parity of an fp8 net on n positions against the oracle; with `batch`,
+    the positions fill a batch of that size cyclically (large batches take
+    the row-panel GEMMs) and every copy is compared."""
     import oracle
 
     spec = synth.SPECS[spec_name]
     weights = synth.make_weights(spec, seed=seed, fp8=True)
     planes, legal = synth.playout_positions(n, seed=seed)
     ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads), weights).evaluate_batch(planes)
-    net = backend.create_network(spec, weights, max_batch=n, device=0, weights_dtype="fp8")
-    gpu = net.evaluate_batch(planes)
+    batch = batch or n
+    idx = np.arange(batch) % n
+    net = backend.create_network(spec, weights, max_batch=batch, device=0, weights_dtype="fp8")
+    gpu = net.evaluate_batch(planes[idx])
     net.close()
+    planes, legal = planes[idx], legal[idx]
+    ref = {k: v[idx] for k, v in ref.items()}
+    n = batch
     perr = np.abs(gpu["policy"] - ref["policy"]).max()
     werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
     agree = np.mean([legal[i][legal[i] >= 0][np.argmax(gpu["policy"][i, legal[i][legal[i] >= 0]])] ==
@@ -85,11 +93,13 @@ def _fp8_parity(spec_name, n, seed=0):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("spec_name,n", [("cpu_plumbing", 16), ("bt4", 8), ("bt4", 40)])
-def test_fp8_weight_parity(spec_name, n):
+@pytest.mark.parametrize("spec_name,n,batch", [("cpu_plumbing", 16, None), ("bt4", 8, None),
+                                              ("bt4", 40, None), ("bt4", 40, 128)])
+def test_fp8_weight_parity(spec_name, n, batch):
     """fp8-weight nets (bf16x2 activations) against the oracle running on the
-    same dequantised weights; 40 BT4 positions reach the large-M tiles."""
+    same dequantised weights; 40 BT4 positions reach the large-M tiles, a
+    batch of 128 the row-panel GEMMs with the fused LayerNorm."""
     if backend.device_count() < 1:
         pytest.fail("GPU tests need an MI355X; none visible")
-    perr, werr, agree = _fp8_parity(spec_name, n)
+    perr, werr, agree = _fp8_parity(spec_name, n, batch=batch)
     assert perr <= 1e-3 and werr <= 1e-4 and agree == 1.0

@@ -183,6 +183,38 @@ def test_bt4_batch_256_whole_round_tiles():
         assert np.abs(wdl - small["wdl"][:hi - lo]).max() <= 1e-5
 
 
+@pytest.mark.parametrize("spec_name,n,precision", [
+    ("cpu_plumbing", 16, "bf16x2"), ("cpu_plumbing", 16, "bf16"),
+    ("bt4", 40, "bf16x2_gemm"), ("bt4", 40, "bf16")])
+def test_row_panel_layernorm_path(spec_name, n, precision):
+    """Batch 128 (8192 token rows) runs every residual GEMM as a row-panel
+    GEMM with the LayerNorm fused into its epilogue (panel widths 256 and
+    1024 for the two nets).  The n oracle-checked positions fill the batch
+    cyclically; each copy meets the gates against the oracle, and in split
+    precision agrees with the batch-n run (tiled GEMM + LayerNorm kernel) to
+    summation-order noise."""
+    spec = synth.SPECS[spec_name]
+    weights, planes, legal, ref = _reference(spec_name, n, 0, 0)
+    idx = np.arange(128) % n
+    net = backend.create_network(spec, weights, max_batch=128, device=0, precision=precision)
+    big = net.evaluate_batch(planes[idx])
+    small = net.evaluate_batch(planes)
+    net.close()
+    for lo in range(0, 128, n):
+        hi = min(lo + n, 128)
+        pol, wdl = big["policy"][lo:hi], big["wdl"][lo:hi]
+        perr = np.abs(pol - ref["policy"][:hi - lo]).max()
+        werr = np.abs(wdl - ref["wdl"][:hi - lo]).max()
+        top1 = _top1_agreement(pol, ref["policy"][:hi - lo], legal[:hi - lo])
+        print(f"{spec_name} x128 {precision} rows {lo}..{hi}: policy max-abs {perr:.3e} "
+              f"wdl max-abs {werr:.3e} top1 {top1:.3f}")
+        assert perr <= POLICY_TOL and werr <= WDL_TOL
+        if precision == "bf16x2":
+            assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
+            assert np.abs(pol - small["policy"][:hi - lo]).max() <= 1e-4
+            assert np.abs(wdl - small["wdl"][:hi - lo]).max() <= 1e-5
+
+
 def test_batch_neighbours_and_chunking():
     """A position's outputs do not depend on its batch neighbours or on
     chunking (reference single-vs-batched parity, test_nn_comparison.cpp:
