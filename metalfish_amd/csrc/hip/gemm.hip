@@ -495,6 +495,21 @@ bool Aligned(const void *ptr, std::uintptr_t bytes) {
 
 }  // namespace
 
+int GemmAutoSplits(const GemmParams &p) {
+  const bool large = p.M >= 2048 && p.N >= 128;
+  if (large || p.k_splits != 1 || !p.partials || p.N % 4 || p.K % 64 || p.M <= 0 || p.N <= 0)
+    return 1;
+  const long tiles = static_cast<long>((p.M + 63) / 64) * ((p.N + 63) / 64);
+  const int steps = p.K / 64;
+  int splits = 1;
+  if (tiles < 256)
+    for (int s = 2; s <= steps; ++s)
+      if (steps % s == 0 && tiles * s <= 512 &&
+          static_cast<size_t>(s) * p.M * p.N <= p.partials_floats)
+        splits = s;
+  return splits;
+}
+
 hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *err) {
   auto fail = [&](const char *why) {
     if (err)
@@ -552,14 +567,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   // only: a batch size always takes the same path and gives the same bits.
   if (!large && p.k_splits == 1 && p.partials && Aligned(p.partials, 16) && p.vec &&
       p.N % 4 == 0) {
-    const long tiles = static_cast<long>((p.M + 63) / 64) * ((p.N + 63) / 64);
-    const int steps = p.K / 64;
-    int splits = 1;
-    if (p.K % 64 == 0 && tiles < 256)
-      for (int s = 2; s <= steps; ++s)
-        if (steps % s == 0 && tiles * s <= 512 &&
-            static_cast<size_t>(s) * p.M * p.N <= p.partials_floats)
-          splits = s;
+    const int splits = GemmAutoSplits(p);
     if (splits > 1) {
       GemmParams q = p;
       q.bias = nullptr;

@@ -875,6 +875,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   // so its fp32 copy is written only where something reads it: the bf16
   // precision's residual, and the body output (debug tensor "body").
   float *res32 = d.split ? nullptr : resid;
+  auto *splitk = net->S<float>("splitk");
   auto *sg1 = net->S<float>("sg1");
   auto *sg2 = net->S<float>("sg2");
   auto *val1 = net->S<float>("val1");
@@ -927,12 +928,16 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   // Residual GEMM followed by its LayerNorm, y = LN(x + alpha (A.W^T + b)),
   // onto the "act" planes (and y32 when set).  At large batches one
   // row-panel launch does both, the pre-LayerNorm rows never leaving the
-  // workgroup; otherwise the tiled GEMM writes them to `pre` for the
-  // LayerNorm kernel.
+  // workgroup; at small batches the LayerNorm kernel sums the GEMM's split-K
+  // partials with the bias and residual; otherwise the tiled GEMM writes the
+  // pre-LayerNorm rows to `pre` for the LayerNorm kernel.
   auto residual_ln = [&](const std::string &a, int k, const size_t (&w_off)[2],
                          const float *bias, const char *role, float alpha, float eps,
                          const float *g, const float *b, float *y32) -> int {
-    if (M >= PanelMinRows() && mfh::PanelGemmShapeOk(mfh::PANEL_OUT_LN, E, k)) {
+    // The panel streams each weight row from L2 for only 64 activation rows,
+    // which pays off when every weight fragment feeds two MFMAs (split
+    // activations); single bf16 activations take the tiled GEMM.
+    if (d.split && M >= PanelMinRows() && mfh::PanelGemmShapeOk(mfh::PANEL_OUT_LN, E, k)) {
       mfh::PanelGemmParams pp;
       pp.A = net->S<std::uint16_t>(a);
       pp.A_lo = net->Lo(a);
@@ -970,6 +975,33 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       StageTimer t(net, st, std::string("gemm_bf16:") + role, flops, bytes);
       const hipError_t e = mfh::LaunchPanelGemm(pp, st, &err_);
       return e == hipSuccess ? MFH_OK : fail(e);
+    }
+    mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
+                             mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
+    const int splits = mfh::GemmAutoSplits(p);
+    if (splits > 1) {
+      // Few positions: the K slices' raw partials go straight to the
+      // LayerNorm kernel, which sums them in slice order with the bias and
+      // the residual (no separate reduce launch).
+      p.bias = nullptr;
+      p.out_mode = mfh::GEMM_OUT_F32;
+      p.C = splitk;
+      p.ldc = E;
+      p.k_splits = splits;
+      p.partials = nullptr;
+      MFH_RUN(run(p, role));
+      mfh::LayerNormParams lp = ln(splitk, M, E, eps, g, b, y32, "act");
+      lp.parts = splits;
+      lp.bias = bias;
+      if (d.split) {
+        lp.resid16 = net->S<std::uint16_t>("act");
+        lp.resid16_lo = net->Lo("act");
+      } else {
+        lp.resid = resid;
+      }
+      lp.alpha = alpha;
+      MFH_RUN(run_ln(lp));
+      return MFH_OK;
     }
     MFH_RUN(residual_gemm(a, k, w_off, bias, role, alpha));
     MFH_RUN(run_ln(ln(pre, M, E, eps, g, b, y32, "act")));
@@ -1024,11 +1056,21 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       l1.bias = net->W<float>(L.sg_d1_b);
       l1.act = d.act_smolgen;
       MFH_RUN(run_ln(l1));
-      MFH_RUN(run(gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr, mfh::ACT_NONE,
-                       mfh::GEMM_OUT_F32, sg2, nullptr, d.HG),
-                  "smolgen_dense2"));
-      mfh::LayerNormParams l2 = ln(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
-                                   net->W<float>(L.sg_ln2_b), nullptr, "sg2n");
+      // Dense2's K slices (few positions) are summed by the LayerNorm
+      // kernel, like dense1's.
+      mfh::GemmParams p2 = gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr,
+                                mfh::ACT_NONE, mfh::GEMM_OUT_F32, sg2, nullptr, d.HG);
+      const int s2 = mfh::GemmAutoSplits(p2);
+      if (s2 > 1) {
+        p2.C = splitk;
+        p2.k_splits = s2;
+        p2.partials = nullptr;
+      }
+      MFH_RUN(run(p2, "smolgen_dense2"));
+      mfh::LayerNormParams l2 = ln(s2 > 1 ? splitk : sg2, B, d.HG, 1e-3f,
+                                   net->W<float>(L.sg_ln2_g), net->W<float>(L.sg_ln2_b),
+                                   nullptr, "sg2n");
+      l2.parts = s2;
       l2.bias = net->W<float>(L.sg_d2_b);
       l2.act = d.act_smolgen;
       MFH_RUN(run_ln(l2));

@@ -79,6 +79,10 @@ struct GemmParams {
 };
 
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
+// Number of K slices LaunchGemm splits this (small-M) problem into when
+// p.partials is set and p.k_splits == 1, or 1.  A caller that sums the
+// partials itself launches with k_splits set to this value instead.
+int GemmAutoSplits(const GemmParams &p);
 
 // Row-panel GEMM: one workgroup of eight waves owns 64 whole output rows
 // and a panel of 128 * TN columns (TN = 2, 4, 6 or 8), so a row's outputs
@@ -165,6 +169,13 @@ struct LayerNormParams {
   int parts = 1;
   const float *bias = nullptr;
   int act = -1;
+  // Residual LayerNorm input: x = resid + alpha * (sum of parts + bias), the
+  // residual fp32 or the split pair resid16 + resid16_lo (row stride width;
+  // may alias the outputs).  No activation with a residual.
+  const float *resid = nullptr;
+  const std::uint16_t *resid16 = nullptr;
+  const std::uint16_t *resid16_lo = nullptr;
+  float alpha = 1.0f;
   int rows = 0, width = 0;
   float eps = 1e-3f;
   const float *gamma = nullptr, *beta = nullptr;

@@ -94,19 +94,23 @@ __global__ void ScatterPeKernel(const float *__restrict__ pe, int batch, int pe_
     emb_in_lo[off] = f32_to_bf16(pe[idx] - bf16_to_f32(hi));
 }
 
-// Row LayerNorm.  T threads per row (64: one wave, 256: one workgroup),
-// each holding NV float4 vectors of the row in registers: element
-// c = 4 (i T + t) + e for vector i of thread t.  The input is the sum of
-// `parts` partial rows plus bias, through the activation, as produced by a
-// split-K GEMM; statistics in fp32 with the reference formula
-// var = E[x^2] - mean^2 clamped at 0, inv_std = 1 / sqrt(var + eps)
-// (cpu_network.cpp:424-460).  Loads are 16 bytes, stores 16 (fp32) or 8
-// (bf16) bytes per lane.
+// Row LayerNorm.  T threads per row (64: one wave; 256 or 1024: one
+// workgroup), each holding NV float4 vectors of the row in registers:
+// element c = 4 (i T + t) + e for vector i of thread t.  The input is the
+// sum of `parts` partial rows plus bias, through the activation, as produced
+// by a split-K GEMM; with a residual, x = resid + alpha * (sum + bias) (the
+// residual LayerNorm, reference cpu_network.cpp:1399-1457).  Statistics in
+// fp32 with the reference formula var = E[x^2] - mean^2 clamped at 0,
+// inv_std = 1 / sqrt(var + eps) (cpu_network.cpp:424-460).  Loads are 16
+// bytes, stores 16 (fp32) or 8 (bf16) bytes per lane.  Each element is read
+// and written by the same thread, so the output may alias the residual.
 
 template <int T, int NV>
-__global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
-  constexpr int kRowsPerBlock = 256 / T;
-  __shared__ float red[2][4];
+__global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormParams lp) {
+  constexpr int kBlock = T > 256 ? T : 256;
+  constexpr int kRowsPerBlock = kBlock / T;
+  constexpr int kWaves = T / 64;
+  __shared__ float red[2][kWaves > 4 ? kWaves : 4];
   const int t = threadIdx.x % T;
   const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / T;
   const bool active = row < lp.rows;
@@ -121,10 +125,27 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
     f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
     if (active && c < width) {
       x = *reinterpret_cast<const f32x4 *>(lp.x + row_off + c);
+#pragma unroll 4
       for (int part = 1; part < lp.parts; ++part)
         x += *reinterpret_cast<const f32x4 *>(lp.x + part * plane + row_off + c);
       if (lp.bias)
         x += *reinterpret_cast<const f32x4 *>(lp.bias + c);
+      if (lp.resid) {
+        const f32x4 r = *reinterpret_cast<const f32x4 *>(lp.resid + row_off + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          x[e] = r[e] + lp.alpha * x[e];
+      } else if (lp.resid16) {
+        const u32x2 h = *reinterpret_cast<const u32x2 *>(lp.resid16 + row_off + c);
+        const u32x2 l = *reinterpret_cast<const u32x2 *>(lp.resid16_lo + row_off + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const unsigned hw = h[e >> 1], lw = l[e >> 1];
+          const float r = __uint_as_float((e & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
+                          __uint_as_float((e & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
+          x[e] = r + lp.alpha * x[e];
+        }
+      }
       if (lp.act != ACT_NONE) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -151,14 +172,19 @@ __global__ __launch_bounds__(256) void LayerNormKernel(LayerNormParams lp) {
   }
   s = wave_sum(s);
   ss = wave_sum(ss);
-  if (T == 256) {
+  if (T >= 256) {
     if ((threadIdx.x & 63) == 0) {
       red[0][threadIdx.x >> 6] = s;
       red[1][threadIdx.x >> 6] = ss;
     }
     __syncthreads();
-    s = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    ss = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    s = 0.f;
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      s += red[0][w];
+      ss += red[1][w];
+    }
   }
   if (!active)
     return;
@@ -301,6 +327,11 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
     Fail(err, "layernorm: invalid arguments");
     return hipErrorInvalidValue;
   }
+  if ((lp.resid && lp.resid16) || (lp.resid16 != nullptr) != (lp.resid16_lo != nullptr) ||
+      ((lp.resid || lp.resid16) && lp.act != ACT_NONE)) {
+    Fail(err, "layernorm: residual is fp32 or a hi + lo pair, without an activation");
+    return hipErrorInvalidValue;
+  }
   if ((lp.mult_gate || lp.add_gate) && lp.rows % kSquares) {
     Fail(err, "layernorm: gates need square rows");
     return hipErrorInvalidValue;
@@ -310,16 +341,25 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
   };
   if (lp.width % 4 || !aligned(lp.x, 16) || (lp.bias && !aligned(lp.bias, 16)) ||
       !aligned(lp.gamma, 16) || !aligned(lp.beta, 16) || (lp.y_f32 && !aligned(lp.y_f32, 16)) ||
-      (lp.y_bf16 && !aligned(lp.y_bf16, 8)) || (lp.y_bf16_lo && !aligned(lp.y_bf16_lo, 8))) {
+      (lp.y_bf16 && !aligned(lp.y_bf16, 8)) || (lp.y_bf16_lo && !aligned(lp.y_bf16_lo, 8)) ||
+      (lp.resid && !aligned(lp.resid, 16)) ||
+      (lp.resid16 && (!aligned(lp.resid16, 8) || !aligned(lp.resid16_lo, 8)))) {
     Fail(err, "layernorm: width % 4 == 0 and 16-byte aligned rows required");
     return hipErrorInvalidValue;
   }
-  // The thread count per row depends on the width only, so a row's
-  // reduction order (and result bits) never depends on the batch size.
+  // The thread count per row depends on the width and the number of split-K
+  // parts only, so at one batch size a row's reduction order (and result
+  // bits) never changes.  Rows that sum split-K parts (few positions) take
+  // 256 threads per row, so the part loads spread over more lanes.
   const int nv64 = (lp.width + 255) / 256;      // float4s per lane, one wave per row
   const int nv256 = (lp.width + 1023) / 1024;   // float4s per lane, 256 threads per row
+  const int nv1024 = (lp.width + 4095) / 4096;  // float4s per lane, 1024 threads per row
   const dim3 g64((lp.rows + 3) / 4), g256(lp.rows), blk(256);
-  if (nv64 <= 1)
+  if (lp.parts > 1 && nv256 <= 1 && lp.width > 256)
+    hipLaunchKernelGGL((LayerNormKernel<256, 1>), g256, blk, 0, stream, lp);
+  else if (lp.parts > 1 && nv256 <= 2 && lp.width > 256)
+    hipLaunchKernelGGL((LayerNormKernel<256, 2>), g256, blk, 0, stream, lp);
+  else if (nv64 <= 1)
     hipLaunchKernelGGL((LayerNormKernel<64, 1>), g64, blk, 0, stream, lp);
   else if (nv64 <= 2)
     hipLaunchKernelGGL((LayerNormKernel<64, 2>), g64, blk, 0, stream, lp);
@@ -329,8 +369,8 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
     hipLaunchKernelGGL((LayerNormKernel<64, 8>), g64, blk, 0, stream, lp);
   else if (nv256 <= 4)
     hipLaunchKernelGGL((LayerNormKernel<256, 4>), g256, blk, 0, stream, lp);
-  else if (nv256 <= 8)
-    hipLaunchKernelGGL((LayerNormKernel<256, 8>), g256, blk, 0, stream, lp);
+  else if (nv1024 <= 2)
+    hipLaunchKernelGGL((LayerNormKernel<1024, 2>), g256, dim3(1024), 0, stream, lp);
   else {
     Fail(err, "layernorm: row wider than 8192");
     return hipErrorInvalidValue;
