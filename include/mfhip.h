@@ -90,6 +90,11 @@ typedef struct {
   int device;             /* HIP device ordinal, -1 = current device */
   int pol_headcount;      /* policy encoder heads (Weights.pol_headcount); 0 without
                              policy encoder layers */
+  int fused_layernorm;    /* residual GEMM + the LayerNorm after it as one
+                             row-panel launch (batches >= 128, split precisions):
+                             1 always; 0 chooses as measured on MI355X: on with
+                             fp8 weights, off with bf16 weights (tiled GEMM,
+                             then the LayerNorm kernel) */
 } mfh_net_desc;
 
 /* One weight tensor, named as in the reference's weight inventory

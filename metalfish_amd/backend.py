@@ -44,7 +44,7 @@ class MfhNetDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "network", "policy", "value", "moves_left", "input_embedding", "default_activation",
         "ffn_activation", "smolgen_activation", "headcount", "weights_dtype", "precision",
-        "max_batch", "device", "pol_headcount")]
+        "max_batch", "device", "pol_headcount", "fused_layernorm")]
 
 
 class MfhTensor(ctypes.Structure):
@@ -145,10 +145,11 @@ class HipNetwork:
     def __init__(self, weights: dict, heads: int, *, wdl=True, default_activation="mish",
                  ffn_activation="default", smolgen_activation="swish", max_batch=256,
                  device=-1, precision="bf16x2", weights_dtype="bf16", net_format=None,
-                 moves_left=False, pe_map=False, pol_heads=0):
+                 moves_left=False, pe_map=False, pol_heads=0, fused_layernorm=False):
         """``net_format``: NetworkFormat fields of a loaded file
         (``WeightsFile.format``); they replace the description the keyword
-        arguments give."""
+        arguments give.  ``fused_layernorm``: residual GEMM + LayerNorm as one
+        row-panel launch at batches >= 128 (split precisions)."""
         self._weights = {k: np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
                          for k, v in weights.items()}
         names = list(self._weights)
@@ -164,7 +165,8 @@ class HipNetwork:
                           ffn_activation=ACTIVATION[ffn_activation],
                           smolgen_activation=ACTIVATION[smolgen_activation], headcount=heads,
                           weights_dtype=WEIGHTS[weights_dtype], precision=PRECISION[precision],
-                          max_batch=max_batch, device=device, pol_headcount=pol_heads)
+                          max_batch=max_batch, device=device, pol_headcount=pol_heads,
+                          fused_layernorm=1 if fused_layernorm else 0)
         if net_format is not None:
             for k in ("network", "policy", "value", "moves_left", "input_embedding",
                       "default_activation", "ffn_activation", "smolgen_activation"):
@@ -398,17 +400,19 @@ def panel_gemm(a_bits, w_bits=None, a_lo_bits=None, w8_codes=None, wscale=None, 
 
 
 def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
-                   weights_dtype="bf16"):
+                   weights_dtype="bf16", fused_layernorm=False):
     """HipNetwork for a synth.NetSpec and its weights.  ``precision`` is
     "bf16x2" (split activations, default: meets every parity gate),
     "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput);
-    ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales)."""
+    ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales);
+    ``fused_layernorm`` selects the row-panel residual GEMM + LayerNorm."""
     return HipNetwork(weights, spec.heads, wdl=spec.wdl, moves_left=spec.moves_left_dim > 0,
                       pe_map=spec.pe_map, pol_heads=spec.policy_heads,
                       default_activation=spec.default_activation,
                       ffn_activation=spec.ffn_activation,
                       smolgen_activation=spec.smolgen_activation, max_batch=max_batch,
-                      device=device, precision=precision, weights_dtype=weights_dtype)
+                      device=device, precision=precision, weights_dtype=weights_dtype,
+                      fused_layernorm=fused_layernorm)
 
 
 class WeightsFile:

@@ -155,6 +155,112 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
   }
 }
 
+// Epilogue for eight consecutive outputs (row, col .. col + 7) given as two
+// fp32 accumulator quads: one 16-byte store per output plane when the group
+// is whole, aligned (p.vec8) and on one side of split_n; otherwise two
+// four-column epilogues.
+template <int MODE, int ACT>
+__device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col, f32x4 a0,
+                                          f32x4 a1) {
+  if (!(p.vec8 && col + 7 < p.N && (col >= p.split_n || col + 8 <= p.split_n))) {
+    float b[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
+    Epilogue4<MODE, ACT>(p, row, col, a0, b);
+    if (col + 4 < p.N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        b[r] = (p.bias && col + 4 + r < p.N) ? p.bias[col + 4 + r] : 0.f;
+      Epilogue4<MODE, ACT>(p, row, col + 4, a1, b);
+    }
+    return;
+  }
+  float v[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    v[r] = a0[r];
+    v[4 + r] = a1[r];
+  }
+  if (p.wscale) {
+    const f32x4 s0 = *reinterpret_cast<const f32x4 *>(p.wscale + col);
+    const f32x4 s1 = *reinterpret_cast<const f32x4 *>(p.wscale + col + 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v[r] *= s0[r];
+      v[4 + r] *= s1[r];
+    }
+  }
+  float b[8];
+  if (p.bias) {
+    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(p.bias + col);
+    const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.bias + col + 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      b[r] = b0[r];
+      b[4 + r] = b1[r];
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      b[r] = 0.f;
+  }
+  if constexpr (MODE == GEMM_OUT_RESID_F32) {
+    const size_t roff = static_cast<size_t>(row) * p.ldr + col;
+    float rv[8];
+    if (p.resid16) {
+      const u32x4 h = *reinterpret_cast<const u32x4 *>(p.resid16 + roff);
+      const u32x4 l = *reinterpret_cast<const u32x4 *>(p.resid16_lo + roff);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const unsigned hw = h[r >> 1], lw = l[r >> 1];
+        rv[r] = __uint_as_float((r & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
+                __uint_as_float((r & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
+      }
+    } else {
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(p.resid + roff);
+      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(p.resid + roff + 4);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        rv[r] = x0[r];
+        rv[4 + r] = x1[r];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      v[r] = rv[r] + p.alpha * (v[r] + b[r]);
+    float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
+    *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4 *>(c + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      v[r] = Act<ACT>(v[r] + b[r], p.act);
+    const bool second = col >= p.split_n;
+    const int cc = second ? col - p.split_n : col;
+    const size_t off = static_cast<size_t>(row) * (second ? p.ldc2 : p.ldc) + cc;
+    if constexpr (MODE == GEMM_OUT_F32) {
+      float *c = static_cast<float *>(second ? p.C2 : p.C) + off;
+      *reinterpret_cast<f32x4 *>(c) = f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<f32x4 *>(c + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    } else {
+      std::uint16_t *c = static_cast<std::uint16_t *>(second ? p.C2 : p.C) + off;
+      std::uint16_t *c_lo = static_cast<std::uint16_t *>(second ? p.C2_lo : p.C_lo);
+      u32x4 hi, lo;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const std::uint16_t h0 = f32_to_bf16(v[2 * h]), h1 = f32_to_bf16(v[2 * h + 1]);
+        hi[h] = h0 | (static_cast<unsigned>(h1) << 16);
+        lo[h] = f32_to_bf16(v[2 * h] - bf16_to_f32(h0)) |
+                (static_cast<unsigned>(f32_to_bf16(v[2 * h + 1] - bf16_to_f32(h1))) << 16);
+      }
+      *reinterpret_cast<u32x4 *>(c) = hi;
+      if (c_lo)
+        *reinterpret_cast<u32x4 *>(c_lo + off) = lo;
+    }
+  }
+}
+
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
           bool W8>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
@@ -371,21 +477,66 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     }
     return;
   }
-  // Epilogue, specialised at compile time on the output mode and activation.
+  if constexpr (MODE == GEMM_OUT_F32) {
+    // fp32 outputs: each lane already stores 16 bytes per row; straight out.
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int col = col_base + j * 16;
-    if (col >= p.N)
-      continue;
-    float b[4];
+    for (int j = 0; j < TN; ++j) {
+      const int col = col_base + j * 16;
+      if (col >= p.N)
+        continue;
+      float b[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
+      for (int r = 0; r < 4; ++r)
+        b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = row_base + i * 16;
+        if (row < p.M)
+          Epilogue4<MODE, ACT>(p, row, col, acc[i][j], b);
+      }
+    }
+    return;
+  }
+  // Staged epilogue (bf16 outputs, and the residual mode, which also reads
+  // the residual): the fp32 accumulator tile passes through LDS (reusing
+  // the operand ring, in row chunks of RB rows that fit it), then each
+  // thread applies the epilogue to eight consecutive columns of a row and
+  // stores them with 16-byte accesses: a wave writes whole 128-byte lines of
+  // consecutive rows instead of 32-byte pieces of sixteen rows.
+  constexpr int PITCH = BN + 4;  // floats per staged row (+4: bank spread)
+  constexpr int RING_FLOATS = ST * STAGE / 2;
+  constexpr int RB = RING_FLOATS >= BM * PITCH         ? BM
+                     : RING_FLOATS >= 128 * PITCH      ? 128
+                     : RING_FLOATS >= 64 * PITCH       ? 64
+                     : RING_FLOATS >= 32 * PITCH       ? 32
+                                                       : 16;
+  static_assert(RB * PITCH <= RING_FLOATS && BM % RB == 0 && RB % 16 == 0,
+                "staged epilogue rows must fit the LDS ring");
+  constexpr int GPR = BN / 8;  // 8-column groups per row
+  float *tile = reinterpret_cast<float *>(lds);
+#pragma unroll 1
+  for (int pass = 0; pass < BM / RB; ++pass) {
+    // The ring is no longer read (first pass) / the previous chunk is stored.
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int row = row_base + i * 16;
-      if (row < p.M)
-        Epilogue4<MODE, ACT>(p, row, col, acc[i][j], b);
+      const int rl = wm * WTM + i * 16 + (lane & 15);
+      if (rl / RB != pass)
+        continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<f32x4 *>(tile + (rl % RB) * PITCH + wn * WTN + j * 16 +
+                                   (lane >> 4) * 4) = acc[i][j];
+    }
+    __syncthreads();
+    for (int g = tid; g < RB * GPR; g += NWAVES * 64) {
+      const int rl = g / GPR, c8 = (g % GPR) * 8;
+      const int row = m0 + pass * RB + rl, col = n0 + c8;
+      if (row >= p.M || col >= p.N)
+        continue;
+      const float *src = tile + rl * PITCH + c8;
+      Epilogue8<MODE, ACT>(p, row, col, *reinterpret_cast<const f32x4 *>(src),
+                           *reinterpret_cast<const f32x4 *>(src + 4));
     }
   }
 }
@@ -558,6 +709,17 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
           (p.out_mode != GEMM_OUT_RESID_F32 ||
            (p.ldr % 4 == 0 && (p.resid16 ? Aligned(p.resid16, 8) && Aligned(p.resid16_lo, 8)
                                           : Aligned(p.resid, 16))));
+  // Eight-column groups with 16-byte accesses (staged epilogue).
+  const bool out_bf16 = p.out_mode == GEMM_OUT_BF16;
+  const int gcols = out_bf16 ? 8 : 4;  // elements per 16 bytes
+  p.vec8 = p.vec && Aligned(p.C, 16) && p.ldc % gcols == 0 &&
+           (!p.C_lo || Aligned(p.C_lo, 16)) &&
+           (p.split_n >= p.N || (p.split_n % 8 == 0 && Aligned(p.C2, 16) &&
+                                 p.ldc2 % gcols == 0 && (!p.C2_lo || Aligned(p.C2_lo, 16)))) &&
+           (!p.bias || Aligned(p.bias, 16)) && (!p.wscale || Aligned(p.wscale, 16)) &&
+           (p.out_mode != GEMM_OUT_RESID_F32 ||
+            (p.resid16 ? Aligned(p.resid16, 16) && Aligned(p.resid16_lo, 16) && p.ldr % 8 == 0
+                       : Aligned(p.resid, 16) && p.ldr % 4 == 0));
   const bool split = p.A_lo != nullptr;
   const bool large = p.M >= 2048 && p.N >= 128;
   // Small problems (few positions): 64 x 64 tiles leave most CUs idle and

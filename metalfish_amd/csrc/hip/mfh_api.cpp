@@ -18,7 +18,6 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
-#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -160,6 +159,7 @@ struct Dims {
   float eps_emb = 1e-3f;  // input-embedding LayerNorm
   bool split = false;       // lo planes on dense-layer inputs (BF16X2, BF16X2_GEMM)
   bool split_attn = false;  // lo planes on attention / smolgen operands (BF16X2)
+  bool fused_ln = false;    // residual GEMM + LayerNorm as one row-panel launch
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -361,6 +361,9 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported precision mode");
   d.split = desc.precision != MFH_PRECISION_BF16;
   d.split_attn = desc.precision == MFH_PRECISION_BF16X2;
+  // Measured at the BT4 shape: the panel wins with e4m3 weights (half the
+  // weight bytes to stream), the tiled GEMM + LayerNorm kernel with bf16.
+  d.fused_ln = desc.fused_layernorm != 0 || desc.weights_dtype == MFH_WEIGHTS_FP8;
   d.wdl = desc.value == MFH_VALUE_WDL;
   d.mlh = desc.moves_left == 1;
   d.act_default = desc.default_activation == MFH_DEFAULT_ACTIVATION_MISH ? mfh::ACT_MISH
@@ -773,17 +776,10 @@ int CollectProfile(mfh_net *net) {
   return MFH_OK;
 }
 
-// Smallest token-row count (positions x 64) at which residual GEMMs run as
-// row-panel GEMMs with the LayerNorm fused; below it the tiled (and, for few
-// positions, split-K) GEMM plus the LayerNorm kernel fill the GPU better.
-// MFH_PANEL_MIN_ROWS overrides it (tuning).
-int PanelMinRows() {
-  static const int rows = [] {
-    const char *env = std::getenv("MFH_PANEL_MIN_ROWS");
-    return env ? std::atoi(env) : 8192;
-  }();
-  return rows;
-}
+// Smallest token-row count (positions x 64) at which residual GEMMs may run
+// as row-panel GEMMs with the LayerNorm fused (128 positions: 128 panels
+// half-fill the 256 CUs; fewer leave most of them idle).
+constexpr int kPanelMinRows = 8192;
 
 // Profiler name of a GEMM launch: "gemm_bf16:<role>", or
 // "gemm_bf16_splitk:<role>" when the caller splits K (partials summed by the
@@ -934,10 +930,13 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   auto residual_ln = [&](const std::string &a, int k, const size_t (&w_off)[2],
                          const float *bias, const char *role, float alpha, float eps,
                          const float *g, const float *b, float *y32) -> int {
-    // The panel streams each weight row from L2 for only 64 activation rows,
-    // which pays off when every weight fragment feeds two MFMAs (split
-    // activations); single bf16 activations take the tiled GEMM.
-    if (d.split && M >= PanelMinRows() && mfh::PanelGemmShapeOk(mfh::PANEL_OUT_LN, E, k)) {
+    // fused_layernorm (default with fp8 weights).  The panel streams each
+    // weight row from L2 for only 64 activation rows, which needs every
+    // weight fragment to feed two MFMAs (split activations); with bf16
+    // weights the tiled GEMM's staged epilogue plus the LayerNorm kernel
+    // measured faster on the BT4 shape.
+    if (d.fused_ln && d.split && M >= kPanelMinRows &&
+        mfh::PanelGemmShapeOk(mfh::PANEL_OUT_LN, E, k)) {
       mfh::PanelGemmParams pp;
       pp.A = net->S<std::uint16_t>(a);
       pp.A_lo = net->Lo(a);
@@ -1024,16 +1023,36 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   // attention and the FFN, residual scale alpha.
   auto encoder_layer = [&](const Layer &L, int heads, int ffn, float eps_attn, float eps_ffn,
                            float alpha, bool body_out) -> int {
-    mfh::GemmParams p = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen ? d.C : 0), E,
+    // Large batches run the smolgen compression rows (3E .. 3E + C of the
+    // fused weight) as a GEMM of their own: 3E columns tile into whole
+    // rounds of workgroups, 3E + C leave a mostly idle last round.  Small
+    // batches keep one launch.
+    const bool own_comp = L.smolgen && M >= 2048;
+    mfh::GemmParams p = gemm("act", E, L.qkv_w, E, M,
+                             3 * E + (L.smolgen && !own_comp ? d.C : 0), E,
                              net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
                              net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
-    if (L.smolgen) {
+    if (L.smolgen && !own_comp) {
       p.split_n = 3 * E;
       p.C2 = net->S<std::uint16_t>("comp");
       p.C2_lo = net->Lo("comp");
       p.ldc2 = d.C;
     }
     MFH_RUN(run(p, "qkv"));
+    if (own_comp) {
+      const size_t skip = static_cast<size_t>(3) * E;  // rows of Q | K | V
+      mfh::GemmParams pc = gemm("act", E, L.qkv_w, E, M, d.C, E,
+                                net->W<float>(L.qkv_b) + skip, mfh::ACT_NONE,
+                                mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("comp"),
+                                net->Lo("comp"), d.C);
+      if (pc.W8) {
+        pc.W8 += skip * E;
+        pc.wscale += skip;
+      } else {
+        pc.W += skip * E;
+      }
+      MFH_RUN(run(pc, "smolgen_compress"));
+    }
     mfh::AttentionParams ap;
     ap.qkv = net->S<std::uint16_t>("qkv");
     ap.qkv_lo = net->Lo("qkv");

@@ -74,8 +74,10 @@ struct GemmParams {
   // K for small problems (partials summed by a second kernel).
   float *partials = nullptr;
   size_t partials_floats = 0;
-  // Set by LaunchGemm: every output row start allows 4-column vector stores.
+  // Set by LaunchGemm: every output row start allows 4-column vector stores
+  // (vec), and 8-column groups allow 16-byte accesses everywhere (vec8).
   bool vec = false;
+  bool vec8 = false;
 };
 
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);

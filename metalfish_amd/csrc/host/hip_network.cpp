@@ -49,6 +49,7 @@ mfh_net_desc DescFromConfig(const HipNetworkConfig &config) {
   desc.precision = config.precision;
   desc.max_batch = config.max_batch;
   desc.device = config.device;
+  desc.fused_layernorm = config.fused_layernorm ? 1 : 0;
   return desc;
 }
 

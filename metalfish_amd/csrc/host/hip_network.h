@@ -45,6 +45,7 @@ struct HipNetworkConfig {
   int max_batch = 256;  // stable execution batch; larger batches are chunked
   int device = -1;
   bool graphs = true;   // HIP graph capture/replay of the forward
+  bool fused_layernorm = false;  // row-panel residual GEMM + LayerNorm (batch >= 128)
 };
 
 // Result of EvaluateBatchPriors for one position: the MCTS priors of its

@@ -204,7 +204,8 @@ def test_row_panel_layernorm_path(spec_name, n, precision):
     spec = synth.SPECS[spec_name]
     weights, planes, legal, ref = _reference(spec_name, n, 0, 0)
     idx = np.arange(128) % n
-    net = backend.create_network(spec, weights, max_batch=128, device=0, precision=precision)
+    net = backend.create_network(spec, weights, max_batch=128, device=0, precision=precision,
+                                 fused_layernorm=True)
     big = net.evaluate_batch(planes[idx])
     small = net.evaluate_batch(planes)
     net.close()
