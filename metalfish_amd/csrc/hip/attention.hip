@@ -290,7 +290,6 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::s
   if (ap.batch <= 0 || ap.heads <= 0 || ap.heads % kHeadsPerBlock || !ap.qkv || !ap.ctx ||
       Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 8) ||
       (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
-
       (split && (!split_out || Misaligned(ap.qkv_lo, 16))) ||
       (split_out && Misaligned(ap.ctx_lo, 8))) {
     if (err)

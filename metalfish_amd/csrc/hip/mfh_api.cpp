@@ -228,6 +228,11 @@ struct mfh_net {
   };
   bool graphs = true;
   hipStream_t capture_stream = nullptr;
+  // Second stream of the forward: each encoder layer's smolgen chain
+  // (compression .. global projection) runs on it while Q|K|V runs on the
+  // main stream; fork / join events per layer (two each).
+  hipStream_t side = nullptr;
+  std::vector<hipEvent_t> fork_join;
   std::map<GraphKey, hipGraphExec_t> graph_execs;
   std::set<GraphKey> graph_warm;
   std::vector<hipEvent_t> event_pool;
@@ -713,8 +718,11 @@ void PlanWorkspace(mfh_net *net) {
   add16("mov_emb", M * (d.Md ? d.Md : 1));
   add("mov1", (d.mlh ? SplitK(kSquares * d.Md) : 1) * B * (d.Mh ? d.Mh : 1) * 4);
   add("mlh", B * 4);
-  // Split-K partials of small-batch GEMMs.
+  // Split-K partials of small-batch GEMMs (main stream, and the smolgen
+  // chain on the side stream).
   add("splitk", kSplitKFloats * 4);
+  if (d.smolgen)
+    add("splitk_sg", kSplitKFloats * 4);
   add("policy", B * kPolicy * 4);
   add("wdl", B * 3 * 4);
   // Legal-move priors (mfh_net_eval_priors): offsets, policy indices, priors.
@@ -832,21 +840,24 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     return p;
   };
   const double plane_mult = d.split ? 2.0 : 1.0;  // bytes of a bf16 activation
-  auto run = [&](const mfh::GemmParams &p, const char *role) {
+  // Launch on the main stream, or on `on` (the side stream's smolgen chain).
+  auto run = [&](const mfh::GemmParams &p, const char *role, hipStream_t on = nullptr) {
     const double flops = 2.0 * p.M * p.N * p.K;
     const double out_bytes = p.out_mode == mfh::GEMM_OUT_BF16 ? 2.0 * plane_mult : 4.0;
     const double bytes = 2.0 * p.M * p.K * (p.A_lo ? 2.0 : 1.0) + (p.W8 ? 1.0 : 2.0) * p.N * p.K +
                          out_bytes * p.M * p.N * p.k_splits +
                          (p.out_mode == mfh::GEMM_OUT_RESID_F32 ? 4.0 * p.M * p.N : 0.0);
-    StageTimer t(net, st, GemmKind(p, role), flops, bytes);
-    return mfh::LaunchGemm(p, st, &err_);
+    hipStream_t s = on ? on : st;
+    StageTimer t(net, s, GemmKind(p, role), flops, bytes);
+    return mfh::LaunchGemm(p, s, &err_);
   };
-  auto run_ln = [&](const mfh::LayerNormParams &lp) {
+  auto run_ln = [&](const mfh::LayerNormParams &lp, hipStream_t on = nullptr) {
     const double n = static_cast<double>(lp.rows) * lp.width;
     const double bytes = 4.0 * n * lp.parts + (lp.y_f32 ? 4.0 * n : 0.0) +
                          (lp.y_bf16 ? 2.0 * n * (lp.y_bf16_lo ? 2.0 : 1.0) : 0.0);
-    StageTimer t(net, st, "layernorm", 0.0, bytes);
-    return mfh::LaunchLayerNorm(lp, st, &err_);
+    hipStream_t s = on ? on : st;
+    StageTimer t(net, s, "layernorm", 0.0, bytes);
+    return mfh::LaunchLayerNorm(lp, s, &err_);
   };
   auto ln = [&](const float *x, int rows, int width, float eps, const float *g, const float *b,
                 float *y32, const std::string &y16) {
@@ -1018,41 +1029,25 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       return rc;
   }
 
+  int layer_index = 0;  // encoder layers run so far (their fork / join events)
   // One encoder layer (cpu_network.cpp:1027-1266, 1318-1457) on resid/act:
   // `heads` attention heads, FFN width `ffn`, LayerNorm epsilons after the
   // attention and the FFN, residual scale alpha.
   auto encoder_layer = [&](const Layer &L, int heads, int ffn, float eps_attn, float eps_ffn,
                            float alpha, bool body_out) -> int {
-    // Large batches run the smolgen compression rows (3E .. 3E + C of the
-    // fused weight) as a GEMM of their own: 3E columns tile into whole
-    // rounds of workgroups, 3E + C leave a mostly idle last round.  Small
-    // batches keep one launch.
-    const bool own_comp = L.smolgen && M >= 2048;
-    mfh::GemmParams p = gemm("act", E, L.qkv_w, E, M,
-                             3 * E + (L.smolgen && !own_comp ? d.C : 0), E,
-                             net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
-                             net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
-    if (L.smolgen && !own_comp) {
-      p.split_n = 3 * E;
-      p.C2 = net->S<std::uint16_t>("comp");
-      p.C2_lo = net->Lo("comp");
-      p.ldc2 = d.C;
-    }
-    MFH_RUN(run(p, "qkv"));
-    if (own_comp) {
-      const size_t skip = static_cast<size_t>(3) * E;  // rows of Q | K | V
-      mfh::GemmParams pc = gemm("act", E, L.qkv_w, E, M, d.C, E,
-                                net->W<float>(L.qkv_b) + skip, mfh::ACT_NONE,
-                                mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("comp"),
-                                net->Lo("comp"), d.C);
-      if (pc.W8) {
-        pc.W8 += skip * E;
-        pc.wscale += skip;
-      } else {
-        pc.W += skip * E;
-      }
-      MFH_RUN(run(pc, "smolgen_compress"));
-    }
+    // The smolgen chain (compression, dense1, LayerNorm, dense2, LayerNorm,
+    // global projection; cpu_network.cpp:1065-1173) reads only the layer
+    // input, like Q|K|V.  At large batches (M >= 2048) the compression rows
+    // (3E .. 3E + C of the fused weight) run as their own GEMM and the whole
+    // chain runs on the side stream while Q|K|V runs on the main stream; the
+    // attention waits for both.  At small batches, where the cross-stream
+    // fork and join cost more than the overlap saves, the compression stays
+    // fused into the Q|K|V launch and the chain follows it on the main
+    // stream.  With the stage profiler on, everything stays on the main
+    // stream so each launch is timed alone.
+    const int li = layer_index++;
+    const bool big = M >= 2048;
+    hipStream_t sg_stream = big && !net->profiling ? net->side : st;
     mfh::AttentionParams ap;
     ap.qkv = net->S<std::uint16_t>("qkv");
     ap.qkv_lo = net->Lo("qkv");
@@ -1060,48 +1055,99 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     ap.heads = heads;
     ap.ctx = net->S<std::uint16_t>("ctx");
     ap.ctx_lo = net->Lo("ctx");
-    if (L.smolgen) {
-      // Smolgen (cpu_network.cpp:1065-1173): dense1 on the flattened
-      // compression (split-K partials summed by the LayerNorm kernel with
-      // bias and activation), dense2, then the shared global projection.
+    // Dense1 on the flattened compression (split-K partials summed by the
+    // LayerNorm kernel with bias and activation), dense2 (its K slices at
+    // few positions summed the same way), then the shared global projection
+    // into the attention bias.
+    auto smolgen_chain = [&](hipStream_t on) -> int {
+      float *sk = net->S<float>(on == st ? "splitk" : "splitk_sg");
+      auto chain_gemm = [&](const std::string &a, int lda, const size_t (&w)[2], int ldw, int m,
+                            int n, int k, const float *bias, int mode, void *C, void *C_lo,
+                            int ldc) {
+        mfh::GemmParams q = gemm(a, lda, w, ldw, m, n, k, bias, mfh::ACT_NONE, mode, C, C_lo,
+                                 ldc);
+        q.partials = sk;
+        return q;
+      };
+      if (big) {
+        const size_t skip = static_cast<size_t>(3) * E;  // rows of Q | K | V
+        mfh::GemmParams pc = chain_gemm("act", E, L.qkv_w, E, M, d.C, E,
+                                        net->W<float>(L.qkv_b) + skip, mfh::GEMM_OUT_BF16,
+                                        net->S<std::uint16_t>("comp"), net->Lo("comp"), d.C);
+        if (pc.W8) {
+          pc.W8 += skip * E;
+          pc.wscale += skip;
+        } else {
+          pc.W += skip * E;
+        }
+        MFH_RUN(run(pc, "smolgen_compress", on));
+      }
       const int flat = kSquares * d.C;
-      mfh::GemmParams p1 = gemm("comp", flat, L.sg_d1_w, flat, B, d.Hs, flat, nullptr,
-                                mfh::ACT_NONE, mfh::GEMM_OUT_F32, sg1, nullptr, d.Hs);
+      mfh::GemmParams p1 = chain_gemm("comp", flat, L.sg_d1_w, flat, B, d.Hs, flat, nullptr,
+                                      mfh::GEMM_OUT_F32, sg1, nullptr, d.Hs);
       p1.k_splits = SplitK(flat);
-      MFH_RUN(run(p1, "smolgen_dense1"));
+      MFH_RUN(run(p1, "smolgen_dense1", on));
       mfh::LayerNormParams l1 = ln(sg1, B, d.Hs, 1e-3f, net->W<float>(L.sg_ln1_g),
                                    net->W<float>(L.sg_ln1_b), nullptr, "sg1n");
       l1.parts = p1.k_splits;
       l1.bias = net->W<float>(L.sg_d1_b);
       l1.act = d.act_smolgen;
-      MFH_RUN(run_ln(l1));
-      // Dense2's K slices (few positions) are summed by the LayerNorm
-      // kernel, like dense1's.
-      mfh::GemmParams p2 = gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr,
-                                mfh::ACT_NONE, mfh::GEMM_OUT_F32, sg2, nullptr, d.HG);
+      MFH_RUN(run_ln(l1, on));
+      mfh::GemmParams p2 = chain_gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr,
+                                      mfh::GEMM_OUT_F32, sg2, nullptr, d.HG);
       const int s2 = mfh::GemmAutoSplits(p2);
       if (s2 > 1) {
-        p2.C = splitk;
+        p2.C = sk;
         p2.k_splits = s2;
         p2.partials = nullptr;
       }
-      MFH_RUN(run(p2, "smolgen_dense2"));
-      mfh::LayerNormParams l2 = ln(s2 > 1 ? splitk : sg2, B, d.HG, 1e-3f,
+      MFH_RUN(run(p2, "smolgen_dense2", on));
+      mfh::LayerNormParams l2 = ln(s2 > 1 ? sk : sg2, B, d.HG, 1e-3f,
                                    net->W<float>(L.sg_ln2_g), net->W<float>(L.sg_ln2_b),
                                    nullptr, "sg2n");
       l2.parts = s2;
       l2.bias = net->W<float>(L.sg_d2_b);
       l2.act = d.act_smolgen;
-      MFH_RUN(run_ln(l2));
-      void *bias = net->S<void>("bias");
-      MFH_RUN(run(gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares, d.G,
-                       nullptr, mfh::ACT_NONE,
-                       d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16, bias, nullptr,
-                       kSquares * kSquares),
-                  "smolgen_global"));
-      ap.bias = bias;
+      MFH_RUN(run_ln(l2, on));
+      MFH_RUN(run(chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares,
+                             d.G, nullptr,
+                             d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
+                             net->S<void>("bias"), nullptr, kSquares * kSquares),
+                  "smolgen_global", on));
+      return MFH_OK;
+    };
+    if (L.smolgen) {
+      ap.bias = net->S<void>("bias");
       ap.bias_f32 = d.split_attn ? 1 : 0;
     }
+    if (L.smolgen && big) {
+      if (sg_stream != st) {
+        MFH_HIP_CHECK(hipEventRecord(net->fork_join[2 * li], st));
+        MFH_HIP_CHECK(hipStreamWaitEvent(sg_stream, net->fork_join[2 * li], 0));
+      }
+      const int rc = smolgen_chain(sg_stream);
+      if (rc != MFH_OK)
+        return rc;
+      if (sg_stream != st)
+        MFH_HIP_CHECK(hipEventRecord(net->fork_join[2 * li + 1], sg_stream));
+    }
+    mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen && !big ? d.C : 0),
+                              E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
+                              net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
+    if (L.smolgen && !big) {
+      pq.split_n = 3 * E;
+      pq.C2 = net->S<std::uint16_t>("comp");
+      pq.C2_lo = net->Lo("comp");
+      pq.ldc2 = d.C;
+    }
+    MFH_RUN(run(pq, "qkv"));
+    if (L.smolgen && !big) {
+      const int rc = smolgen_chain(st);
+      if (rc != MFH_OK)
+        return rc;
+    }
+    if (L.smolgen && big && sg_stream != st)
+      MFH_HIP_CHECK(hipStreamWaitEvent(st, net->fork_join[2 * li + 1], 0));
     {
       const double heads_total = static_cast<double>(B) * heads;
       const double flops = heads_total * 2.0 * (2.0 * kSquares * kSquares * 32);
@@ -1507,8 +1553,12 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     if (raw->pin_out) (void)hipHostFree(raw->pin_out);
     if (raw->stream) (void)hipStreamDestroy(raw->stream);
     if (raw->capture_stream) (void)hipStreamDestroy(raw->capture_stream);
+    if (raw->side) (void)hipStreamDestroy(raw->side);
+    for (hipEvent_t e : raw->fork_join)
+      (void)hipEventDestroy(e);
+    raw->fork_join.clear();
     raw->weights = raw->ws = raw->pin_in = raw->pin_out = nullptr;
-    raw->stream = raw->capture_stream = nullptr;
+    raw->stream = raw->capture_stream = raw->side = nullptr;
   };
   if (hipMemcpy(net->weights, blob.bytes.data(), net->weight_bytes, hipMemcpyHostToDevice) !=
       hipSuccess) {
@@ -1530,9 +1580,18 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     return SetError(MFH_ERR_OUT_OF_MEMORY, "pinned staging allocation failed");
   }
   if (hipStreamCreateWithFlags(&net->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipStreamCreateWithFlags(&net->capture_stream, hipStreamNonBlocking) != hipSuccess) {
+      hipStreamCreateWithFlags(&net->capture_stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&net->side, hipStreamNonBlocking) != hipSuccess) {
     cleanup();
     return SetError(MFH_ERR_HIP, "stream creation failed");
+  }
+  for (size_t i = 0; i < 2 * (net->layers.size() + net->pol_layers.size()); ++i) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      cleanup();
+      return SetError(MFH_ERR_HIP, "event creation failed");
+    }
+    net->fork_join.push_back(e);
   }
   *out = net.release();
   return MFH_OK;
@@ -1548,6 +1607,10 @@ void mfh_net_destroy(mfh_net *net) {
     (void)hipStreamDestroy(net->stream);
   if (net->capture_stream)
     (void)hipStreamDestroy(net->capture_stream);
+  if (net->side)
+    (void)hipStreamDestroy(net->side);
+  for (hipEvent_t e : net->fork_join)
+    (void)hipEventDestroy(e);
   (void)CollectProfile(net);
   for (hipEvent_t e : net->event_pool)
     (void)hipEventDestroy(e);
