@@ -64,11 +64,11 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   const int qcol = h * kDepth, kcol = E + h * kDepth, vcol = 2 * E + h * kDepth;
   const int fr = lane & 15, g = lane >> 4;
 
-  // All of the head's global loads go out before any is used, so their
-  // latencies overlap: V rows (for V^T), Q and K fragments, and the bias of
-  // the first query tile (the bias of tile q + 1 is fetched while tile q is
-  // processed).  Lane l's V rows: the key pair 2 (l % 32), 2 (l % 32) + 1,
-  // depths 16 (l / 32) .. + 16.
+  // The head's V rows (for V^T), its K fragments and the first query tile's
+  // Q fragments and bias go out first, so their latencies overlap; each
+  // later query tile's Q fragments and bias are fetched while the tile
+  // before it is processed.  Lane l's V rows: the key pair 2 (l % 32),
+  // 2 (l % 32) + 1, depths 16 (l / 32) .. + 16.
   const int kp = lane & 31, dh = (lane >> 5) * 16;
   u32x4 vrow[PLANES][4];
 #pragma unroll
@@ -81,23 +81,22 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     vrow[pl][2] = r1[0];
     vrow[pl][3] = r1[1];
   }
-  // S^T = K Q^T operands: tile (t, s) holds keys 16 t + 4 g + r (rows) for
-  // queries 16 s + fr (columns).
+  // S^T = K Q^T operands: tile (t, q) holds keys 16 t + 4 g + r (rows) for
+  // queries 16 q + fr (columns).
   const std::uint16_t *qh = ap.qkv + pos;
-  bf16x8 kf[4], qf[4], kl[4], qlo[4];
+  const std::uint16_t *ql = SPLIT ? ap.qkv_lo + pos : ap.qkv + pos;
+  bf16x8 kf[4], kl[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     kf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + kcol + g * 8);
-    qf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + qcol + g * 8);
-  }
-  if constexpr (SPLIT) {
-    const std::uint16_t *ql = ap.qkv_lo + pos;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    if constexpr (SPLIT)
       kl[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + kcol + g * 8);
-      qlo[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + qcol + g * 8);
-    }
   }
+  auto load_q = [&](int q, bf16x8 &hi, bf16x8 &lo) {
+    hi = *reinterpret_cast<const bf16x8 *>(qh + (q * 16 + fr) * ld + qcol + g * 8);
+    if constexpr (SPLIT)
+      lo = *reinterpret_cast<const bf16x8 *>(ql + (q * 16 + fr) * ld + qcol + g * 8);
+  };
   const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
   // Bias of query tile q for the lane's keys 16 t + 4 g .. + 3, t = 0..3.
   auto load_bias = [&](int q, float (&bb)[4][4]) {
@@ -125,10 +124,13 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       }
     }
   };
-  float bcur[4][4], bnext[4][4];
+  bf16x8 qcur, qlcur;
+  float bcur[4][4];
+  load_q(0, qcur, qlcur);
   load_bias(0, bcur);
 
-  // V^T into LDS, one packed dword (two keys) per depth.
+  // V^T into LDS, one packed dword (two keys) per depth.  Each wave reads
+  // only its own head's V^T.
 #pragma unroll
   for (int pl = 0; pl < PLANES; ++pl) {
     std::uint32_t *vt = reinterpret_cast<std::uint32_t *>(vt_lds[wave][pl]);
@@ -141,40 +143,37 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       vt[((dh + e) * kVtStride) / 2 + kp] = lo | (hi << 16);
     }
   }
+  __syncthreads();
 
-  f32x4 s[4][4];  // [t][s]
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      s[t][q] = Mfma(kf[t], qf[q], f32x4{0.f, 0.f, 0.f, 0.f});
-  if constexpr (SPLIT) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        s[t][q] = Mfma(kl[t], qf[q], Mfma(kf[t], qlo[q], s[t][q]));
-  }
-
-  // Scale, bias, softmax over the 64 keys of each query 16 q + fr; the lane
-  // holds 16 of them, lanes fr, fr + 16, fr + 32, fr + 48 hold the rest.
+  // One query tile at a time: scores, scale + bias, softmax over the 64 keys
+  // of each query 16 q + fr (the lane holds 16 of them, lanes fr, fr + 16,
+  // fr + 32, fr + 48 the rest), then ctx^T = V^T P^T for the tile and its
+  // store.  Only one tile's scores and probabilities are live at a time.
   const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
-  bf16x8 pf[4][2], pl[4][2];  // [query tile][key-tile pair]: B operands of ctx^T
+  const size_t out_off = static_cast<size_t>(b) * kSq * E + h * kDepth;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    if (q + 1 < 4)
+    bf16x8 qnext, qlnext;
+    float bnext[4][4];
+    if (q + 1 < 4) {
+      load_q(q + 1, qnext, qlnext);
       load_bias(q + 1, bnext);
+    }
+    f32x4 s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      s[t] = Mfma(kf[t], qcur, f32x4{0.f, 0.f, 0.f, 0.f});
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        s[t] = Mfma(kl[t], qcur, Mfma(kf[t], qlcur, s[t]));
+    }
     float v[4][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        v[t][r] = s[t][q][r] * scale + bcur[t][r];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        bcur[t][r] = bnext[t][r];
+        v[t][r] = s[t][r] * scale + bcur[t][r];
     float m = v[0][0];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -194,8 +193,10 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     const float inv = 1.f / sum;
-    // K-slot j of pair u: key 32 u + 4 g + (j % 4) + 16 (j / 4), i.e. tile
-    // t = 2 u + j / 4, element r = j % 4.
+    // B operands of ctx^T: K-slot j of pair u is key 32 u + 4 g + (j % 4) +
+    // 16 (j / 4), i.e. tile t = 2 u + j / 4, element r = j % 4 (the MFMA
+    // sums over K, so only the pairing of P and V slots matters).
+    bf16x8 pf[2], plo[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       std::uint32_t hw[4], lw[4];
@@ -209,66 +210,61 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
           lw[j / 2] = f32_to_bf16(p0 - bf16_to_f32(h0)) |
                       (static_cast<std::uint32_t>(f32_to_bf16(p1 - bf16_to_f32(h1))) << 16);
       }
-      pf[q][u] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+      pf[u] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
       if constexpr (SPLIT)
-        pl[q][u] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+        plo[u] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
     }
-  }
-  __syncthreads();
-
-  // ctx^T = V^T P^T: A = V^T fragment (depth 16 dt + fr, the lane's 8 keys),
-  // B = P fragment; tile (dt, q) holds depths 16 dt + 4 g + r for query
-  // 16 q + fr.
-  f32x4 o[2][4];
+    // ctx^T = V^T P^T: A = V^T fragment (depth 16 dt + fr, the lane's 8
+    // keys), B = P fragment; tile dt holds depths 16 dt + 4 g + r for query
+    // 16 q + fr.
+    f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      o[dt][q] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
+      for (int dt = 0; dt < 2; ++dt) {
+        const int row = (dt * 16 + fr) * kVtStride + 32 * u + 4 * g;
+        const std::uint16_t *vh = vt_lds[wave][0];
+        const bf16x8 va = Join(*reinterpret_cast<const u32x2 *>(vh + row),
+                               *reinterpret_cast<const u32x2 *>(vh + row + 16));
+        o[dt] = Mfma(va, pf[u], o[dt]);
+        if constexpr (SPLIT) {
+          const std::uint16_t *vl = vt_lds[wave][1];
+          const bf16x8 vb = Join(*reinterpret_cast<const u32x2 *>(vl + row),
+                                 *reinterpret_cast<const u32x2 *>(vl + row + 16));
+          o[dt] = Mfma(vb, pf[u], Mfma(va, plo[u], o[dt]));
+        }
+      }
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
-      const int row = (dt * 16 + fr) * kVtStride + 32 * u + 4 * g;
-      const std::uint16_t *vh = vt_lds[wave][0];
-      const bf16x8 va = Join(*reinterpret_cast<const u32x2 *>(vh + row),
-                             *reinterpret_cast<const u32x2 *>(vh + row + 16));
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        o[dt][q] = Mfma(va, pf[q][u], o[dt][q]);
-      if constexpr (SPLIT) {
-        const std::uint16_t *vl = vt_lds[wave][1];
-        const bf16x8 vb = Join(*reinterpret_cast<const u32x2 *>(vl + row),
-                               *reinterpret_cast<const u32x2 *>(vl + row + 16));
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          o[dt][q] = Mfma(vb, pf[q][u], Mfma(va, pl[q][u], o[dt][q]));
-      }
-    }
-  const size_t out_off = static_cast<size_t>(b) * kSq * E + h * kDepth;
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
       const size_t idx = out_off + static_cast<size_t>(q * 16 + fr) * E + dt * 16 + g * 4;
       std::uint16_t hi[4];
       std::uint32_t lw[2];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        hi[r] = f32_to_bf16(o[dt][q][r]);
+        hi[r] = f32_to_bf16(o[dt][r]);
       *reinterpret_cast<u32x2 *>(ap.ctx + idx) =
           u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
                 hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
       if constexpr (SPLIT_OUT) {
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
-          lw[r / 2] = f32_to_bf16(o[dt][q][r] - bf16_to_f32(hi[r])) |
+          lw[r / 2] = f32_to_bf16(o[dt][r] - bf16_to_f32(hi[r])) |
                       (static_cast<std::uint32_t>(
-                           f32_to_bf16(o[dt][q][r + 1] - bf16_to_f32(hi[r + 1])))
+                           f32_to_bf16(o[dt][r + 1] - bf16_to_f32(hi[r + 1])))
                        << 16);
         *reinterpret_cast<u32x2 *>(ap.ctx_lo + idx) = u32x2{lw[0], lw[1]};
       }
     }
+    if (q + 1 < 4) {
+      qcur = qnext;
+      qlcur = qlnext;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bcur[t][r] = bnext[t][r];
+    }
+  }
 }
 
 template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
