@@ -95,21 +95,24 @@ __global__ void ScatterPeKernel(const float *__restrict__ pe, int batch, int pe_
 }
 
 // Row LayerNorm.  T threads per row (64: one wave; 256 or 1024: one
-// workgroup), each holding NV float4 vectors of the row in registers:
-// element c = 4 (i T + t) + e for vector i of thread t.  The input is the
+// workgroup), each holding NV groups of G (4 or 8) consecutive elements of
+// the row in registers: element c = G (i T + t) + e of group i of thread t.
+// The input is the
 // sum of `parts` partial rows plus bias, through the activation, as produced
 // by a split-K GEMM; with a residual, x = resid + alpha * (sum + bias) (the
 // residual LayerNorm, reference cpu_network.cpp:1399-1457).  Statistics in
 // fp32 with the reference formula var = E[x^2] - mean^2 clamped at 0,
 // inv_std = 1 / sqrt(var + eps) (cpu_network.cpp:424-460).  Loads are 16
-// bytes, stores 16 (fp32) or 8 (bf16) bytes per lane.  Each element is read
-// and written by the same thread, so the output may alias the residual.
+// bytes, bf16 stores 2G bytes per lane.  Each element is read and written by
+// the same thread, so the output may alias the residual.
 
-template <int T, int NV>
+template <int T, int NV, int G = 4>
 __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormParams lp) {
   constexpr int kBlock = T > 256 ? T : 256;
   constexpr int kRowsPerBlock = kBlock / T;
   constexpr int kWaves = T / 64;
+  constexpr int Q = G / 4;  // float4 vectors per group
+  static_assert(G == 4 || G == 8, "groups of 4 or 8 elements");
   __shared__ float red[2][kWaves > 4 ? kWaves : 4];
   const int t = threadIdx.x % T;
   const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / T;
@@ -117,57 +120,64 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
   const int width = lp.width;
   const size_t plane = static_cast<size_t>(lp.rows) * width;
   const size_t row_off = static_cast<size_t>(row) * width;
-  f32x4 v[NV];
+  f32x4 v[NV][Q];
   float s = 0.f, ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int c = 4 * (i * T + t);
-    f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (active && c < width) {
-      x = *reinterpret_cast<const f32x4 *>(lp.x + row_off + c);
-#pragma unroll 4
-      for (int part = 1; part < lp.parts; ++part)
-        x += *reinterpret_cast<const f32x4 *>(lp.x + part * plane + row_off + c);
-      if (lp.bias)
-        x += *reinterpret_cast<const f32x4 *>(lp.bias + c);
-      if (lp.resid) {
-        const f32x4 r = *reinterpret_cast<const f32x4 *>(lp.resid + row_off + c);
+    const int c0 = G * (i * T + t);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          x[e] = r[e] + lp.alpha * x[e];
-      } else if (lp.resid16) {
-        const u32x2 h = *reinterpret_cast<const u32x2 *>(lp.resid16 + row_off + c);
-        const u32x2 l = *reinterpret_cast<const u32x2 *>(lp.resid16_lo + row_off + c);
+    for (int q = 0; q < Q; ++q) {
+      const int c = c0 + 4 * q;
+      f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (active && c0 < width) {
+        x = *reinterpret_cast<const f32x4 *>(lp.x + row_off + c);
+#pragma unroll 4
+        for (int part = 1; part < lp.parts; ++part)
+          x += *reinterpret_cast<const f32x4 *>(lp.x + part * plane + row_off + c);
+        if (lp.bias)
+          x += *reinterpret_cast<const f32x4 *>(lp.bias + c);
+        if (lp.resid) {
+          const f32x4 r = *reinterpret_cast<const f32x4 *>(lp.resid + row_off + c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            x[e] = r[e] + lp.alpha * x[e];
+        } else if (lp.resid16) {
+          const u32x2 h = *reinterpret_cast<const u32x2 *>(lp.resid16 + row_off + c);
+          const u32x2 l = *reinterpret_cast<const u32x2 *>(lp.resid16_lo + row_off + c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const unsigned hw = h[e >> 1], lw = l[e >> 1];
+            const float r = __uint_as_float((e & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
+                            __uint_as_float((e & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
+            x[e] = r + lp.alpha * x[e];
+          }
+        }
+        if (lp.act != ACT_NONE) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            x[e] = activate(x[e], lp.act);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const unsigned hw = h[e >> 1], lw = l[e >> 1];
-          const float r = __uint_as_float((e & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
-                          __uint_as_float((e & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
-          x[e] = r + lp.alpha * x[e];
+          s += x[e];
+          ss += x[e] * x[e];
         }
       }
-      if (lp.act != ACT_NONE) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          x[e] = activate(x[e], lp.act);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s += x[e];
-        ss += x[e] * x[e];
-      }
+      v[i][q] = x;
     }
-    v[i] = x;
   }
   // gamma / beta are independent of the statistics: fetch them before the
   // reductions so their latency overlaps.
-  f32x4 gm[NV], bt[NV];
+  f32x4 gm[NV][Q], bt[NV][Q];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int c = 4 * (i * T + t);
-    if (c < width) {
-      gm[i] = *reinterpret_cast<const f32x4 *>(lp.gamma + c);
-      bt[i] = *reinterpret_cast<const f32x4 *>(lp.beta + c);
+    const int c0 = G * (i * T + t);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      if (c0 < width) {
+        gm[i][q] = *reinterpret_cast<const f32x4 *>(lp.gamma + c0 + 4 * q);
+        bt[i][q] = *reinterpret_cast<const f32x4 *>(lp.beta + c0 + 4 * q);
+      }
     }
   }
   s = wave_sum(s);
@@ -195,34 +205,47 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
   const int sq = row % kSquares;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int c = 4 * (i * T + t);
-    if (c >= width)
+    const int c0 = G * (i * T + t);
+    if (c0 >= width)
       break;
-    f32x4 y;
+    unsigned hi2[2 * Q], lo2[2 * Q];  // bf16 pairs of the group
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      y[e] = (v[i][e] - mean) * inv_std * gm[i][e] + bt[i][e];
-      if (lp.mult_gate)
-        y[e] = y[e] * lp.mult_gate[static_cast<size_t>(c + e) * kSquares + sq];
-      if (lp.add_gate)
-        y[e] = y[e] + lp.add_gate[static_cast<size_t>(c + e) * kSquares + sq];
-    }
-    if (lp.y_f32)
-      *reinterpret_cast<f32x4 *>(lp.y_f32 + row_off + c) = y;
-    if (lp.y_bf16) {
+    for (int q = 0; q < Q; ++q) {
+      const int c = c0 + 4 * q;
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[e] = (v[i][q][e] - mean) * inv_std * gm[i][q][e] + bt[i][q][e];
+        if (lp.mult_gate)
+          y[e] = y[e] * lp.mult_gate[static_cast<size_t>(c + e) * kSquares + sq];
+        if (lp.add_gate)
+          y[e] = y[e] + lp.add_gate[static_cast<size_t>(c + e) * kSquares + sq];
+      }
+      if (lp.y_f32)
+        *reinterpret_cast<f32x4 *>(lp.y_f32 + row_off + c) = y;
       std::uint16_t hi[4], lo[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         hi[e] = f32_to_bf16(y[e]);
         lo[e] = f32_to_bf16(y[e] - bf16_to_f32(hi[e]));
       }
-      *reinterpret_cast<u32x2 *>(lp.y_bf16 + row_off + c) =
-          u32x2{hi[0] | (static_cast<unsigned>(hi[1]) << 16),
-                hi[2] | (static_cast<unsigned>(hi[3]) << 16)};
-      if (lp.y_bf16_lo)
-        *reinterpret_cast<u32x2 *>(lp.y_bf16_lo + row_off + c) =
-            u32x2{lo[0] | (static_cast<unsigned>(lo[1]) << 16),
-                  lo[2] | (static_cast<unsigned>(lo[3]) << 16)};
+      hi2[2 * q] = hi[0] | (static_cast<unsigned>(hi[1]) << 16);
+      hi2[2 * q + 1] = hi[2] | (static_cast<unsigned>(hi[3]) << 16);
+      lo2[2 * q] = lo[0] | (static_cast<unsigned>(lo[1]) << 16);
+      lo2[2 * q + 1] = lo[2] | (static_cast<unsigned>(lo[3]) << 16);
+    }
+    if (lp.y_bf16) {
+      if constexpr (G == 8) {
+        *reinterpret_cast<u32x4 *>(lp.y_bf16 + row_off + c0) =
+            u32x4{hi2[0], hi2[1], hi2[2], hi2[3]};
+        if (lp.y_bf16_lo)
+          *reinterpret_cast<u32x4 *>(lp.y_bf16_lo + row_off + c0) =
+              u32x4{lo2[0], lo2[1], lo2[2], lo2[3]};
+      } else {
+        *reinterpret_cast<u32x2 *>(lp.y_bf16 + row_off + c0) = u32x2{hi2[0], hi2[1]};
+        if (lp.y_bf16_lo)
+          *reinterpret_cast<u32x2 *>(lp.y_bf16_lo + row_off + c0) = u32x2{lo2[0], lo2[1]};
+      }
     }
   }
 }
@@ -351,6 +374,13 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
   // parts only, so at one batch size a row's reduction order (and result
   // bits) never changes.  Rows that sum split-K parts (few positions) take
   // 256 threads per row, so the part loads spread over more lanes.
+  // One wave per row with 8-element groups (16-byte bf16 stores) when the
+  // width is a whole number of 512-element chunks and rows are 16-byte
+  // aligned in every bf16 output.
+  const bool g8 = lp.width % 512 == 0 && lp.width <= 2048 && lp.parts == 1 &&
+                  (!lp.y_bf16 || aligned(lp.y_bf16, 16)) &&
+                  (!lp.y_bf16_lo || aligned(lp.y_bf16_lo, 16)) &&
+                  (!lp.resid16 || (aligned(lp.resid16, 16) && aligned(lp.resid16_lo, 16)));
   const int nv64 = (lp.width + 255) / 256;      // float4s per lane, one wave per row
   const int nv256 = (lp.width + 1023) / 1024;   // float4s per lane, 256 threads per row
   const int nv1024 = (lp.width + 4095) / 4096;  // float4s per lane, 1024 threads per row
@@ -359,6 +389,12 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
     hipLaunchKernelGGL((LayerNormKernel<256, 1>), g256, blk, 0, stream, lp);
   else if (lp.parts > 1 && nv256 <= 2 && lp.width > 256)
     hipLaunchKernelGGL((LayerNormKernel<256, 2>), g256, blk, 0, stream, lp);
+  else if (g8 && lp.width == 512)
+    hipLaunchKernelGGL((LayerNormKernel<64, 1, 8>), g64, blk, 0, stream, lp);
+  else if (g8 && lp.width == 1024)
+    hipLaunchKernelGGL((LayerNormKernel<64, 2, 8>), g64, blk, 0, stream, lp);
+  else if (g8)
+    hipLaunchKernelGGL((LayerNormKernel<64, 4, 8>), g64, blk, 0, stream, lp);
   else if (nv64 <= 1)
     hipLaunchKernelGGL((LayerNormKernel<64, 1>), g64, blk, 0, stream, lp);
   else if (nv64 <= 2)
