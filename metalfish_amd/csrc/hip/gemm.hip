@@ -155,77 +155,14 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
   }
 }
 
-// Epilogue for eight consecutive outputs (row, col .. col + 7) given as two
-// fp32 accumulator quads: one 16-byte store per output plane when the group
-// is whole, aligned (p.vec8) and on one side of split_n; otherwise two
-// four-column epilogues.
+// Output of eight consecutive columns (row, col .. col + 7) of a whole,
+// aligned group on one side of split_n: v holds the scaled accumulators, b
+// the bias and rv the residual (residual mode only).  One 16-byte store per
+// output plane (two for fp32).
 template <int MODE, int ACT>
-__device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col, f32x4 a0,
-                                          f32x4 a1) {
-  if (!(p.vec8 && col + 7 < p.N && (col >= p.split_n || col + 8 <= p.split_n))) {
-    float b[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
-    Epilogue4<MODE, ACT>(p, row, col, a0, b);
-    if (col + 4 < p.N) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        b[r] = (p.bias && col + 4 + r < p.N) ? p.bias[col + 4 + r] : 0.f;
-      Epilogue4<MODE, ACT>(p, row, col + 4, a1, b);
-    }
-    return;
-  }
-  float v[8];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    v[r] = a0[r];
-    v[4 + r] = a1[r];
-  }
-  if (p.wscale) {
-    const f32x4 s0 = *reinterpret_cast<const f32x4 *>(p.wscale + col);
-    const f32x4 s1 = *reinterpret_cast<const f32x4 *>(p.wscale + col + 4);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      v[r] *= s0[r];
-      v[4 + r] *= s1[r];
-    }
-  }
-  float b[8];
-  if (p.bias) {
-    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(p.bias + col);
-    const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.bias + col + 4);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      b[r] = b0[r];
-      b[4 + r] = b1[r];
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < 8; ++r)
-      b[r] = 0.f;
-  }
+__device__ __forceinline__ void Finish8(const GemmParams &p, int row, int col, float (&v)[8],
+                                        const float (&b)[8], const float (&rv)[8]) {
   if constexpr (MODE == GEMM_OUT_RESID_F32) {
-    const size_t roff = static_cast<size_t>(row) * p.ldr + col;
-    float rv[8];
-    if (p.resid16) {
-      const u32x4 h = *reinterpret_cast<const u32x4 *>(p.resid16 + roff);
-      const u32x4 l = *reinterpret_cast<const u32x4 *>(p.resid16_lo + roff);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const unsigned hw = h[r >> 1], lw = l[r >> 1];
-        rv[r] = __uint_as_float((r & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
-                __uint_as_float((r & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
-      }
-    } else {
-      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(p.resid + roff);
-      const f32x4 x1 = *reinterpret_cast<const f32x4 *>(p.resid + roff + 4);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        rv[r] = x0[r];
-        rv[4 + r] = x1[r];
-      }
-    }
 #pragma unroll
     for (int r = 0; r < 8; ++r)
       v[r] = rv[r] + p.alpha * (v[r] + b[r]);
@@ -259,6 +196,93 @@ __device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col,
         *reinterpret_cast<u32x4 *>(c_lo + off) = lo;
     }
   }
+}
+
+// The residual of eight consecutive columns as fp32 (hi + lo bf16 planes,
+// or fp32).
+__device__ __forceinline__ void LoadResid8(const GemmParams &p, int row, int col,
+                                           float (&rv)[8]) {
+  const size_t roff = static_cast<size_t>(row) * p.ldr + col;
+  if (p.resid16) {
+    const u32x4 h = *reinterpret_cast<const u32x4 *>(p.resid16 + roff);
+    const u32x4 l = *reinterpret_cast<const u32x4 *>(p.resid16_lo + roff);
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const unsigned hw = h[r >> 1], lw = l[r >> 1];
+      rv[r] = __uint_as_float((r & 1) ? (hw & 0xFFFF0000u) : (hw << 16)) +
+              __uint_as_float((r & 1) ? (lw & 0xFFFF0000u) : (lw << 16));
+    }
+  } else {
+    const f32x4 x0 = *reinterpret_cast<const f32x4 *>(p.resid + roff);
+    const f32x4 x1 = *reinterpret_cast<const f32x4 *>(p.resid + roff + 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      rv[r] = x0[r];
+      rv[4 + r] = x1[r];
+    }
+  }
+}
+
+// Bias and fp8 row scale of eight consecutive columns (zero / one when
+// absent).
+__device__ __forceinline__ void LoadBiasScale8(const GemmParams &p, int col, float (&b)[8],
+                                               float (&sc)[8]) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    b[r] = 0.f;
+    sc[r] = 1.f;
+  }
+  if (p.bias) {
+    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(p.bias + col);
+    const f32x4 b1 = *reinterpret_cast<const f32x4 *>(p.bias + col + 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      b[r] = b0[r];
+      b[4 + r] = b1[r];
+    }
+  }
+  if (p.wscale) {
+    const f32x4 s0 = *reinterpret_cast<const f32x4 *>(p.wscale + col);
+    const f32x4 s1 = *reinterpret_cast<const f32x4 *>(p.wscale + col + 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sc[r] = s0[r];
+      sc[4 + r] = s1[r];
+    }
+  }
+}
+
+// Epilogue for eight consecutive outputs (row, col .. col + 7) given as two
+// fp32 accumulator quads: one 16-byte store per output plane when the group
+// is whole, aligned (p.vec8) and on one side of split_n; otherwise two
+// four-column epilogues.
+template <int MODE, int ACT>
+__device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col, f32x4 a0,
+                                          f32x4 a1) {
+  if (!(p.vec8 && col + 7 < p.N && (col >= p.split_n || col + 8 <= p.split_n))) {
+    float b[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
+    Epilogue4<MODE, ACT>(p, row, col, a0, b);
+    if (col + 4 < p.N) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        b[r] = (p.bias && col + 4 + r < p.N) ? p.bias[col + 4 + r] : 0.f;
+      Epilogue4<MODE, ACT>(p, row, col + 4, a1, b);
+    }
+    return;
+  }
+  float v[8], b[8], sc[8], rv[8];
+  LoadBiasScale8(p, col, b, sc);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    v[r] = a0[r] * sc[r];
+    v[4 + r] = a1[r] * sc[4 + r];
+  }
+  if constexpr (MODE == GEMM_OUT_RESID_F32)
+    LoadResid8(p, row, col, rv);
+  Finish8<MODE, ACT>(p, row, col, v, b, rv);
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
@@ -514,8 +538,8 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
                 "staged epilogue rows must fit the LDS ring");
   constexpr int GPR = BN / 8;  // 8-column groups per row
   float *tile = reinterpret_cast<float *>(lds);
-#pragma unroll 1
-  for (int pass = 0; pass < BM / RB; ++pass) {
+  // Rows pass * RB .. + RB of the accumulator tile into the ring.
+  auto stage = [&](int pass) {
     // The ring is no longer read (first pass) / the previous chunk is stored.
     __syncthreads();
 #pragma unroll
@@ -529,6 +553,50 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
                                    (lane >> 4) * 4) = acc[i][j];
     }
     __syncthreads();
+  };
+  // Whole, aligned tiles on one side of split_n, bf16 outputs: when the
+  // thread count is a multiple of the groups per row, a thread keeps one
+  // column group for the whole tile (bias and scale loaded once) and its
+  // rows of a chunk are ITER rows RSTEP apart.  (The residual mode keeps the
+  // loop below: requesting a chunk's residual rows ahead of the staging
+  // measured slower.)
+  constexpr int THREADS = NWAVES * 64;
+  if constexpr (MODE == GEMM_OUT_BF16 && THREADS % GPR == 0 && (RB * GPR) % THREADS == 0) {
+    constexpr int ITER = RB * GPR / THREADS;
+    constexpr int RSTEP = THREADS / GPR;
+    const int c8 = (tid % GPR) * 8, r0 = tid / GPR;
+    const int col = n0 + c8;
+    if (p.vec8 && n0 + BN <= p.N && (n0 + BN <= p.split_n || n0 >= p.split_n)) {
+      float b[8], sc[8];
+      LoadBiasScale8(p, col, b, sc);
+#pragma unroll 1
+      for (int pass = 0; pass < BM / RB; ++pass) {
+        const float none[8] = {};
+        stage(pass);
+#pragma unroll
+        for (int k = 0; k < ITER; ++k) {
+          const int rl = r0 + k * RSTEP;
+          const int row = m0 + pass * RB + rl;
+          if (row < p.M) {
+            const float *src = tile + rl * PITCH + c8;
+            const f32x4 a0 = *reinterpret_cast<const f32x4 *>(src);
+            const f32x4 a1 = *reinterpret_cast<const f32x4 *>(src + 4);
+            float v[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              v[r] = a0[r] * sc[r];
+              v[4 + r] = a1[r] * sc[4 + r];
+            }
+            Finish8<MODE, ACT>(p, row, col, v, b, none);
+          }
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll 1
+  for (int pass = 0; pass < BM / RB; ++pass) {
+    stage(pass);
     for (int g = tid; g < RB * GPR; g += NWAVES * 64) {
       const int rl = g / GPR, c8 = (g % GPR) * 8;
       const int row = m0 + pass * RB + rl, col = n0 + c8;
