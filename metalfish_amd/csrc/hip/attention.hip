@@ -17,8 +17,11 @@
 //     to the next MFMA (the MFMA sums over K, so only the pairing of P and V
 //     slots matters), and ctx^T = V^T P^T takes them as its B operand.
 // Only V^T goes through LDS (4 KiB per head, two 8-byte reads per fragment).
-// ctx^T leaves each lane with four consecutive depths of one query: one
-// 8-byte store.  Scores, softmax statistics and accumulation stay in fp32.
+// ctx^T leaves each lane with four consecutive depths of one query; each
+// query tile's context goes through a small LDS tile so that the workgroup
+// stores its 4 heads' rows whole (256 contiguous bytes per row and plane,
+// 16 bytes per lane).  Scores, softmax statistics and accumulation stay in
+// fp32.
 //
 // Split precision: with SPLIT_IN, Q, K and V arrive as hi + lo bf16 planes,
 // P is split the same way in registers, and each product takes three MFMAs
@@ -36,6 +39,9 @@ constexpr int kHeadsPerBlock = 4;
 // V^T rows: 64 keys plus 8 of padding, so the two halves of a wave writing
 // depths d and d + 16 land on different banks.
 constexpr int kVtStride = kSq + 8;
+// Context staging tile: 16 queries x (4 heads x 32 depths) bf16 per plane,
+// rows of 16 chunks of 16 bytes, chunk c of row r stored at c ^ r.
+constexpr int kCtxCols = kHeadsPerBlock * kDepth;
 
 
 __device__ __forceinline__ f32x4 Mfma(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -50,8 +56,10 @@ __device__ __forceinline__ bf16x8 Join(u32x2 a, u32x2 b) {
 template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
 __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   constexpr int PLANES = SPLIT ? 2 : 1;
+  constexpr int OUT_PLANES = SPLIT_OUT ? 2 : 1;
   __shared__ __attribute__((aligned(16))) std::uint16_t vt_lds[kHeadsPerBlock][PLANES]
                                                                 [kDepth * kVtStride];
+  __shared__ __attribute__((aligned(16))) std::uint16_t ctx_lds[2][OUT_PLANES][16 * kCtxCols];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int heads = ap.heads;
@@ -150,7 +158,8 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   // fr + 32, fr + 48 the rest), then ctx^T = V^T P^T for the tile and its
   // store.  Only one tile's scores and probabilities are live at a time.
   const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
-  const size_t out_off = static_cast<size_t>(b) * kSq * E + h * kDepth;
+  const size_t out_off =
+      static_cast<size_t>(b) * kSq * E + (blockIdx.x % groups) * kHeadsPerBlock * kDepth;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     bf16x8 qnext, qlnext;
@@ -234,26 +243,44 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
           o[dt] = Mfma(vb, pf[u], Mfma(va, plo[u], o[dt]));
         }
       }
+    // Context of the tile into the staging buffer (lane: query fr, depths
+    // 16 dt + 4 g .. + 3 of this wave's head = half of 16-byte chunk
+    // 4 wave + 2 dt + g / 2), then one 16-byte store per plane and thread:
+    // thread t takes chunk t % 16 of query row t / 16.
+    std::uint16_t(*stage)[16 * kCtxCols] = ctx_lds[q & 1];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
-      const size_t idx = out_off + static_cast<size_t>(q * 16 + fr) * E + dt * 16 + g * 4;
+      const int chunk = (4 * wave + 2 * dt + (g >> 1)) ^ fr;
+      const int off = fr * kCtxCols + chunk * 8 + (g & 1) * 4;
       std::uint16_t hi[4];
-      std::uint32_t lw[2];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         hi[r] = f32_to_bf16(o[dt][r]);
-      *reinterpret_cast<u32x2 *>(ap.ctx + idx) =
+      *reinterpret_cast<u32x2 *>(stage[0] + off) =
           u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
                 hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
       if constexpr (SPLIT_OUT) {
+        std::uint32_t lw[2];
 #pragma unroll
         for (int r = 0; r < 4; r += 2)
           lw[r / 2] = f32_to_bf16(o[dt][r] - bf16_to_f32(hi[r])) |
                       (static_cast<std::uint32_t>(
                            f32_to_bf16(o[dt][r + 1] - bf16_to_f32(hi[r + 1])))
                        << 16);
-        *reinterpret_cast<u32x2 *>(ap.ctx_lo + idx) = u32x2{lw[0], lw[1]};
+        *reinterpret_cast<u32x2 *>(stage[1] + off) = u32x2{lw[0], lw[1]};
       }
+    }
+    // Two staging buffers: the barrier of tile q also orders every read of
+    // tile q - 1's buffer before tile q + 1 overwrites it.
+    __syncthreads();
+    {
+      const int row = threadIdx.x >> 4, chunk = threadIdx.x & 15;
+      const int src = row * kCtxCols + (chunk ^ row) * 8;
+      const size_t idx = out_off + static_cast<size_t>(q * 16 + row) * E + chunk * 8;
+#pragma unroll
+      for (int pl = 0; pl < OUT_PLANES; ++pl)
+        *reinterpret_cast<u32x4 *>((pl ? ap.ctx_lo : ap.ctx) + idx) =
+            *reinterpret_cast<const u32x4 *>(stage[pl] + src);
     }
     if (q + 1 < 4) {
       qcur = qnext;
@@ -284,13 +311,13 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::s
   const bool split = ap.qkv_lo != nullptr;
   const bool split_out = ap.ctx_lo != nullptr;
   if (ap.batch <= 0 || ap.heads <= 0 || ap.heads % kHeadsPerBlock || !ap.qkv || !ap.ctx ||
-      Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 8) ||
+      Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 16) ||
       (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
       (split && (!split_out || Misaligned(ap.qkv_lo, 16))) ||
-      (split_out && Misaligned(ap.ctx_lo, 8))) {
+      (split_out && Misaligned(ap.ctx_lo, 16))) {
     if (err)
-      *err = "attention: needs batch > 0, heads % 4 == 0, 16-byte aligned qkv, 8-byte "
-             "aligned ctx and bias, and a lo output plane whenever the input has one";
+      *err = "attention: needs batch > 0, heads % 4 == 0, 16-byte aligned qkv and ctx, "
+             "8-byte aligned bias, and a lo output plane whenever the input has one";
     return hipErrorInvalidValue;
   }
   const int grid = ap.batch * (ap.heads / kHeadsPerBlock);
