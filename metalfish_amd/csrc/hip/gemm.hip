@@ -501,32 +501,12 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     }
     return;
   }
-  if constexpr (MODE == GEMM_OUT_F32) {
-    // fp32 outputs: each lane already stores 16 bytes per row; straight out.
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = col_base + j * 16;
-      if (col >= p.N)
-        continue;
-      float b[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = row_base + i * 16;
-        if (row < p.M)
-          Epilogue4<MODE, ACT>(p, row, col, acc[i][j], b);
-      }
-    }
-    return;
-  }
-  // Staged epilogue (bf16 outputs, and the residual mode, which also reads
-  // the residual): the fp32 accumulator tile passes through LDS (reusing
-  // the operand ring, in row chunks of RB rows that fit it), then each
-  // thread applies the epilogue to eight consecutive columns of a row and
-  // stores them with 16-byte accesses: a wave writes whole 128-byte lines of
-  // consecutive rows instead of 32-byte pieces of sixteen rows.
+  // Staged epilogue (bf16 outputs, whole fp32 tiles, and the residual mode,
+  // which also reads the residual): the fp32 accumulator tile passes through
+  // LDS (reusing the operand ring, in row chunks of RB rows that fit it),
+  // then each thread applies the epilogue to eight consecutive columns of a
+  // row and stores them with 16-byte accesses: a wave writes whole 128-byte
+  // lines of consecutive rows instead of pieces of sixteen rows.
   constexpr int PITCH = BN + 4;  // floats per staged row (+4: bank spread)
   constexpr int RING_FLOATS = ST * STAGE / 2;
   constexpr int RB = RING_FLOATS >= BM * PITCH         ? BM
@@ -554,14 +534,16 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     }
     __syncthreads();
   };
-  // Whole, aligned tiles on one side of split_n, bf16 outputs: when the
-  // thread count is a multiple of the groups per row, a thread keeps one
+  // Whole, aligned tiles on one side of split_n, bf16 and fp32 outputs: when
+  // the thread count is a multiple of the groups per row, a thread keeps one
   // column group for the whole tile (bias and scale loaded once) and its
-  // rows of a chunk are ITER rows RSTEP apart.  (The residual mode keeps the
-  // loop below: requesting a chunk's residual rows ahead of the staging
-  // measured slower.)
+  // rows of a chunk are ITER rows RSTEP apart; a wave stores whole rows
+  // (fp32: two 16-byte stores per lane).  (The residual mode keeps the loop
+  // below: requesting a chunk's residual rows ahead of the staging measured
+  // slower.)
   constexpr int THREADS = NWAVES * 64;
-  if constexpr (MODE == GEMM_OUT_BF16 && THREADS % GPR == 0 && (RB * GPR) % THREADS == 0) {
+  if constexpr (MODE != GEMM_OUT_RESID_F32 && THREADS % GPR == 0 &&
+                (RB * GPR) % THREADS == 0) {
     constexpr int ITER = RB * GPR / THREADS;
     constexpr int RSTEP = THREADS / GPR;
     const int c8 = (tid % GPR) * 8, r0 = tid / GPR;
@@ -593,6 +575,27 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       }
       return;
     }
+  }
+  if constexpr (MODE == GEMM_OUT_F32) {
+    // fp32 outputs of partial or unaligned tiles: each lane stores 16 bytes
+    // per row straight from the accumulators.
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = col_base + j * 16;
+      if (col >= p.N)
+        continue;
+      float b[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = row_base + i * 16;
+        if (row < p.M)
+          Epilogue4<MODE, ACT>(p, row, col, acc[i][j], b);
+      }
+    }
+    return;
   }
 #pragma unroll 1
   for (int pass = 0; pass < BM / RB; ++pass) {
