@@ -190,6 +190,29 @@ def test_bt4_batch_256_whole_round_tiles():
         assert np.abs(wdl - small["wdl"][:hi - lo]).max() <= 1e-5
 
 
+@pytest.mark.parametrize("embedding,heads,batch", [(512, 16, 4), (2048, 64, 4), (512, 16, 40)])
+def test_wide_embedding_layernorm_groups(embedding, heads, batch):
+    """One-layer nets of embedding width 512 and 2048 (head depth 32): their
+    LayerNorm rows take the one-wave kernel with 8-element groups per lane
+    (one and four 512-element chunks), which the 256- and 1024-wide test
+    nets do not reach.  Batch 40 (2560 token rows) also runs the tiled
+    large-batch GEMMs at width 512."""
+    spec = synth.NetSpec(f"e{embedding}", embedding, 1, heads, 1024, input_ffn=512,
+                         policy_dim=embedding)
+    weights = synth.make_weights(spec, seed=3)
+    planes, legal = synth.playout_positions(batch, seed=3)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=heads), weights).evaluate_batch(planes)
+    net = backend.create_network(spec, weights, max_batch=batch, device=0)
+    gpu = net.evaluate_batch(planes)
+    net.close()
+    perr = np.abs(gpu["policy"] - ref["policy"]).max()
+    werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
+    top1 = _top1_agreement(gpu["policy"], ref["policy"], legal)
+    print(f"E={embedding} batch {batch}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} "
+          f"top1 {top1:.3f}")
+    assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
+
+
 @pytest.mark.parametrize("spec_name,n,precision", [
     ("cpu_plumbing", 16, "bf16x2"), ("cpu_plumbing", 16, "bf16x2_gemm"),
     ("bt4", 40, "bf16x2_gemm"), ("bt4", 40, "bf16")])
