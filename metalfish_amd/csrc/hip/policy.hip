@@ -30,6 +30,7 @@ __global__ __launch_bounds__(1024) void PolicyMapKernel(
     float *__restrict__ policy) {
   __shared__ float part[4][kSq * kSq];
   __shared__ float pk_term[24];
+  __shared__ float pk_wave[16][24];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int qb = wave & 3, dc = wave >> 2;
@@ -72,19 +73,44 @@ __global__ __launch_bounds__(1024) void PolicyMapKernel(
       part[dc][(qb * 16 + (lane >> 4) * 4 + r) * kSq + j * 16 + fr] = acc[j][r];
 
   // Promotion offsets: term[t][tf] = K[56+tf] . (promo[t] + promo[3]).
-  for (int d = wave; d < 24; d += 16) {
-    const int t = d / 8, tf = d % 8;
-    const size_t koff = (56 + tf) * ld + dp;
-    float s = 0.f;
-    for (int c = lane; c < dp; c += 64) {
-      float kv = bf16_to_f32(base[koff + c]);
+  // Thread c takes depth c (c, c + 1024, ...) of all 24 products, so every
+  // load is issued before any sum waits on one (a single position is
+  // latency-bound here); then one wave sum per product and a fixed-order
+  // sum over the 16 waves.
+  float term[24];
+#pragma unroll
+  for (int d = 0; d < 24; ++d)
+    term[d] = 0.f;
+  for (int c = threadIdx.x; c < dp; c += 1024) {
+    float pr[3];
+    const float p3 = promo[static_cast<size_t>(3) * dp + c];
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      pr[t] = promo[static_cast<size_t>(t) * dp + c] + p3;
+#pragma unroll
+    for (int tf = 0; tf < 8; ++tf) {
+      const size_t koff = (56 + tf) * ld + dp + c;
+      float kv = bf16_to_f32(base[koff]);
       if constexpr (SPLIT)
-        kv += bf16_to_f32(qk_lo[pos + koff + c]);
-      s += kv * (promo[static_cast<size_t>(t) * dp + c] + promo[static_cast<size_t>(3) * dp + c]);
+        kv += bf16_to_f32(qk_lo[pos + koff]);
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+        term[t * 8 + tf] += kv * pr[t];
     }
-    s = wave_sum(s);
+  }
+#pragma unroll
+  for (int d = 0; d < 24; ++d) {
+    const float w = wave_sum(term[d]);
     if (lane == 0)
-      pk_term[t * 8 + tf] = s;
+      pk_wave[wave][d] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x < 24) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w)
+      sum += pk_wave[w][threadIdx.x];
+    pk_term[threadIdx.x] = sum;
   }
   __syncthreads();
 
