@@ -138,7 +138,11 @@ int mfh_net_eval_planes(mfh_net *net, int batch, const float *planes,
 
 /* Forward pass on device-resident buffers (no host copies, no
  * synchronisation), enqueued on `stream` (a hipStream_t; NULL is the
- * default stream).  Outputs are ready when that stream reaches this point. */
+ * default stream).  Outputs are ready when that stream reaches this point.
+ * All calls on one net share its workspace, so each call's device work is
+ * ordered after the previous call's, whatever stream either ran on (the
+ * new stream waits on an event the previous call recorded); calls on
+ * different streams therefore run one after another on the device. */
 int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
                         const float *d_values, float *d_policy, float *d_wdl,
                         void *stream);

@@ -200,6 +200,12 @@ struct mfh_net {
   size_t ws_bytes = 0;
   std::map<std::string, size_t> ws_off;
 
+  // Recorded after the last work that touched the workspace, on whatever
+  // stream it ran; every call waits on it before its own work.  The
+  // workspace is shared, so calls on different streams (mfh_net_eval on the
+  // net's stream, mfh_net_eval_device on a caller's) run one after another.
+  hipEvent_t last_use = nullptr;
+
   unsigned char *pin_in = nullptr;   // masks | values | move offsets | move indices
   unsigned char *pin_out = nullptr;  // policy | value
   int last_batch = 0;
@@ -1300,6 +1306,17 @@ void DropGraphs(mfh_net *net) {
   net->graph_warm.clear();
 }
 
+// Orders this call's work on `st` after every earlier call's (BeginUse),
+// and marks where it ends (EndUse).
+int BeginUse(mfh_net *net, hipStream_t st) {
+  MFH_HIP_CHECK(hipStreamWaitEvent(st, net->last_use, 0));
+  return MFH_OK;
+}
+int EndUse(mfh_net *net, hipStream_t st) {
+  MFH_HIP_CHECK(hipEventRecord(net->last_use, st));
+  return MFH_OK;
+}
+
 // Forward through a cached HIP graph (captured on the net's capture stream,
 // launched on `st`), or eagerly while profiling, for a key's first run, or
 // when graphs are off.  A graph bakes in the batch size and the buffers.
@@ -1359,10 +1376,14 @@ int RunStaged(mfh_net *net, int batch) {
   auto *d_policy = net->S<float>("policy");
   auto *d_wdl = net->S<float>("wdl");
   MFH_HIP_CHECK(hipSetDevice(net->device));
+  int rc = BeginUse(net, net->stream);
+  if (rc != MFH_OK)
+    return rc;
   MFH_HIP_CHECK(hipMemcpyAsync(d_masks, pin_masks, n_in * 8, hipMemcpyHostToDevice, net->stream));
   MFH_HIP_CHECK(hipMemcpyAsync(d_values, pin_values, n_in * 4, hipMemcpyHostToDevice, net->stream));
-  const int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), net->stream);
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), net->stream);
   if (rc != MFH_OK) {
+    (void)EndUse(net, net->stream);
     (void)hipStreamSynchronize(net->stream);
     return rc;
   }
@@ -1376,6 +1397,7 @@ int RunStaged(mfh_net *net, int batch) {
     MFH_HIP_CHECK(hipMemcpyAsync(PinMovesLeft(net), net->S<float>("mlh"),
                                  static_cast<size_t>(batch) * 4, hipMemcpyDeviceToHost,
                                  net->stream));
+  MFH_HIP_CHECK(hipEventRecord(net->last_use, net->stream));
   MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
   net->last_batch = batch;
   return MFH_OK;
@@ -1405,6 +1427,9 @@ int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
   const unsigned char *pin = net->pin_in;
   const size_t mb = static_cast<size_t>(net->max_batch);
   MFH_HIP_CHECK(hipSetDevice(net->device));
+  int rc = BeginUse(net, net->stream);
+  if (rc != MFH_OK)
+    return rc;
   MFH_HIP_CHECK(hipMemcpyAsync(d_masks, pin, n_in * 8, hipMemcpyHostToDevice, net->stream));
   MFH_HIP_CHECK(hipMemcpyAsync(d_values, pin + mb * kPlanes * 8, n_in * 4,
                                hipMemcpyHostToDevice, net->stream));
@@ -1415,7 +1440,7 @@ int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
     MFH_HIP_CHECK(hipMemcpyAsync(d_indices, pin + PinMovesOffset(net->max_batch),
                                  static_cast<size_t>(total_moves) * 2, hipMemcpyHostToDevice,
                                  net->stream));
-  int rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), net->stream);
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), net->stream);
   if (rc == MFH_OK) {
     std::string err;
     if (mfh::LaunchPolicyPriors(d_policy, d_offsets, d_indices, batch, inv_temp, d_priors,
@@ -1423,6 +1448,7 @@ int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
       rc = SetError(MFH_ERR_HIP, "policy priors launch failed: " + err);
   }
   if (rc != MFH_OK) {
+    (void)EndUse(net, net->stream);
     (void)hipStreamSynchronize(net->stream);
     return rc;
   }
@@ -1437,6 +1463,7 @@ int RunStagedPriors(mfh_net *net, int batch, int total_moves, float inv_temp) {
     MFH_HIP_CHECK(hipMemcpyAsync(PinMovesLeft(net), net->S<float>("mlh"),
                                  static_cast<size_t>(batch) * 4, hipMemcpyDeviceToHost,
                                  net->stream));
+  MFH_HIP_CHECK(hipEventRecord(net->last_use, net->stream));
   MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
   net->last_batch = batch;
   return MFH_OK;
@@ -1534,6 +1561,14 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
   net->max_batch = desc->max_batch;
   net->arch = arch;
   net->device_name = prop.name;
+  if (net->device_name.empty()) {
+    // The marketing name comes from libdrm's amdgpu.ids table, which some
+    // installs lack: describe the device from its properties instead.
+    std::ostringstream o;
+    o << "AMD " << arch.substr(0, arch.find(':')) << " GPU, " << prop.multiProcessorCount
+      << " CUs, " << (prop.totalGlobalMem >> 30) << " GiB";
+    net->device_name = o.str();
+  }
   Blob blob;
   net->fp8 = desc->weights_dtype == MFH_WEIGHTS_FP8;
   rc = Pack(net.get(), ld, blob);
@@ -1557,6 +1592,8 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     for (hipEvent_t e : raw->fork_join)
       (void)hipEventDestroy(e);
     raw->fork_join.clear();
+    if (raw->last_use) (void)hipEventDestroy(raw->last_use);
+    raw->last_use = nullptr;
     raw->weights = raw->ws = raw->pin_in = raw->pin_out = nullptr;
     raw->stream = raw->capture_stream = raw->side = nullptr;
   };
@@ -1585,6 +1622,11 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
     cleanup();
     return SetError(MFH_ERR_HIP, "stream creation failed");
   }
+  if (hipEventCreateWithFlags(&net->last_use, hipEventDisableTiming) != hipSuccess ||
+      hipEventRecord(net->last_use, net->stream) != hipSuccess) {
+    cleanup();
+    return SetError(MFH_ERR_HIP, "event creation failed");
+  }
   for (size_t i = 0; i < 2 * (net->layers.size() + net->pol_layers.size()); ++i) {
     hipEvent_t e = nullptr;
     if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
@@ -1611,6 +1653,8 @@ void mfh_net_destroy(mfh_net *net) {
     (void)hipStreamDestroy(net->side);
   for (hipEvent_t e : net->fork_join)
     (void)hipEventDestroy(e);
+  if (net->last_use)
+    (void)hipEventDestroy(net->last_use);
   (void)CollectProfile(net);
   for (hipEvent_t e : net->event_pool)
     (void)hipEventDestroy(e);
@@ -1671,7 +1715,13 @@ int mfh_net_eval_device(mfh_net *net, int batch, const uint64_t *d_masks,
   std::lock_guard<std::mutex> lock(net->mu);
   MFH_HIP_CHECK(hipSetDevice(net->device));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = BeginUse(net, st);
+  if (rc != MFH_OK)
+    return rc;
   rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), st);
+  const int end = EndUse(net, st);
+  if (rc == MFH_OK)
+    rc = end;
   if (rc == MFH_OK)
     net->last_batch = batch;
   return rc;
@@ -1690,8 +1740,14 @@ int mfh_net_eval_device_moves_left(mfh_net *net, int batch, const uint64_t *d_ma
     return rc;
   std::lock_guard<std::mutex> lock(net->mu);
   MFH_HIP_CHECK(hipSetDevice(net->device));
-  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, d_moves_left,
-                  static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = BeginUse(net, st);
+  if (rc != MFH_OK)
+    return rc;
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, d_moves_left, st);
+  const int end = EndUse(net, st);
+  if (rc == MFH_OK)
+    rc = end;
   if (rc == MFH_OK)
     net->last_batch = batch;
   return rc;
@@ -1750,15 +1806,22 @@ int mfh_net_eval_priors_device(mfh_net *net, int batch, const uint64_t *d_masks,
   std::lock_guard<std::mutex> lock(net->mu);
   MFH_HIP_CHECK(hipSetDevice(net->device));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), st);
+  rc = BeginUse(net, st);
   if (rc != MFH_OK)
     return rc;
-  std::string err;
-  if (mfh::LaunchPolicyPriors(d_policy, d_move_offsets, d_move_indices, batch, 1.0f / softmax_temp,
-                         d_priors, st, &err) != hipSuccess)
-    return SetError(MFH_ERR_HIP, "policy priors launch failed: " + err);
-  net->last_batch = batch;
-  return MFH_OK;
+  rc = RunForward(net, batch, d_masks, d_values, d_policy, d_wdl, net->S<float>("mlh"), st);
+  if (rc == MFH_OK) {
+    std::string err;
+    if (mfh::LaunchPolicyPriors(d_policy, d_move_offsets, d_move_indices, batch,
+                                1.0f / softmax_temp, d_priors, st, &err) != hipSuccess)
+      rc = SetError(MFH_ERR_HIP, "policy priors launch failed: " + err);
+  }
+  const int end = EndUse(net, st);
+  if (rc == MFH_OK)
+    rc = end;
+  if (rc == MFH_OK)
+    net->last_batch = batch;
+  return rc;
 }
 
 int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
@@ -1821,7 +1884,7 @@ int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t byt
   if (B == 0 || bytes != size)
     return SetError(MFH_ERR_INVALID, "debug tensor size mismatch");
   MFH_HIP_CHECK(hipSetDevice(net->device));
-  MFH_HIP_CHECK(hipStreamSynchronize(net->stream));
+  MFH_HIP_CHECK(hipEventSynchronize(net->last_use));
   MFH_HIP_CHECK(hipMemcpy(out, net->ws + net->ws_off.at(ws_name), size, hipMemcpyDeviceToHost));
   return MFH_OK;
 }

@@ -118,6 +118,7 @@ void HipNetwork::RunChunk(const InputPlanes *inputs, int count, NetworkOutput *o
   // InputPlanes is a contiguous 112x64 float array, so a run of them is the
   // planes[count*112*64] layout the C ABI takes.
   const float *planes = inputs[0][0].data();
+  std::lock_guard<std::mutex> lock(mu_);
   for (int attempt = 0; attempt < 2; ++attempt) {
     const int rc = mfh_net_eval_planes(net_, count, planes, policy_.data(), value_.data(),
                                        mlh_ ? moves_.data() : nullptr);
@@ -183,6 +184,7 @@ std::vector<PriorsOutput> HipNetwork::EvaluateBatchPriors(
   std::vector<float> priors;
   for (std::size_t start = 0; start < inputs.size(); start += max_batch_) {
     const int count = static_cast<int>(std::min<std::size_t>(max_batch_, inputs.size() - start));
+    std::lock_guard<std::mutex> lock(mu_);
     masks_.resize(static_cast<std::size_t>(count) * kTotalPlanes);
     values_.resize(masks_.size());
     int rc = mfh_pack_planes(count, inputs[start][0].data(), masks_.data(), values_.data());

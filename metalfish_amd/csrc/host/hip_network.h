@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -91,6 +92,11 @@ private:
   void RunChunk(const InputPlanes *inputs, int count, NetworkOutput *outputs);
 
   mfh_net *net_ = nullptr;
+  // Held across each chunk's C call and the decode of its outputs, which
+  // live in the members below (the reference's execution_mutex_, held across
+  // run and decode, cuda_network.cpp:442-446): MCTS workers may call
+  // EvaluateBatch and EvaluateBatchPriors concurrently.
+  std::mutex mu_;
   bool graphs_ = true;
   bool wdl_ = true;
   bool mlh_ = false;
