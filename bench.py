@@ -62,8 +62,8 @@ def parse_args():
     ap.add_argument("--fp8-batch", type=int, default=1024)
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline, roofline and batch-1 latency")
-    ap.add_argument("--cpu-positions", type=int, default=16,
-                    help="positions in the CPU-baseline sample (0 skips it)")
+    ap.add_argument("--cpu-positions", type=int, default=32,
+                    help="positions in the all-cores CPU-baseline sample (0 skips it)")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 256 MiB buffer 5 times (the known-size kernel that "
@@ -83,20 +83,57 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}))
 
 
-def cpu_baseline(spec, weights, planes, n, threads):
-    """Times the CPU oracle on n positions with `threads` worker threads."""
-    import oracle
+def cpu_model():
+    """The host CPU's model string (/proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
+
+def cpu_baseline(spec, weights, planes, n, threads):
+    """Times the CPU oracle (the restated reference CPU backend) on this
+    host: positions/s on one core (2 positions), and the aggregate with one
+    worker per core over `threads` cores (n positions); also the config-1
+    net on one core.  The value reported is the aggregate."""
+    import oracle
+    from metalfish_amd import synth
+
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    threads = max(1, min(threads, affinity))
     net = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads), weights)
-    sample = planes[:n]
     t0 = time.perf_counter()
-    net.evaluate_batch(sample, threads=threads)
+    net.evaluate_batch(planes[:2], threads=1)
+    one = 2 / (time.perf_counter() - t0)
+    n = max(n, threads)
+    t0 = time.perf_counter()
+    net.evaluate_batch(planes[:n], threads=threads)
     dt = time.perf_counter() - t0
+    c1 = synth.SPECS["cpu_plumbing"]
+    c1net = oracle.OracleNet(oracle.NetFormat(body_heads=c1.heads),
+                             synth.make_weights(c1, seed=0))
+    c1planes, _ = synth.playout_positions(16, seed=0)
+    t0 = time.perf_counter()
+    c1net.evaluate_batch(c1planes, threads=1)
+    c1_rate = 16 / (time.perf_counter() - t0)
     return {"value": round(n / dt, 4), "unit": "positions/s", "cores": threads,
             "kind": "port",
             "sample": f"{n} positions of the BT4-shape net (config 2), fp32 oracle "
-                      f"(restated reference CPU backend, -O3 no FMA contraction), one "
-                      f"position per thread, {dt:.1f} s wall"}
+                      f"(restated reference CPU backend: same loop order, -O3, no FMA "
+                      f"contraction), one worker thread per core on {threads} cores, "
+                      f"{dt:.1f} s wall",
+            "one_core_positions_per_s": round(one, 4),
+            "cpu_model": cpu_model(),
+            "nproc": os.cpu_count(),
+            "affinity_cpus": affinity,
+            "config1_one_core_positions_per_s": round(c1_rate, 2)}
 
 
 def read_traffic():

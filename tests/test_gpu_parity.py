@@ -19,6 +19,7 @@ import ctypes
 import numpy as np
 import pytest
 
+import gpu_util
 import netfile
 import oracle
 from metalfish_amd import backend, synth
@@ -369,37 +370,7 @@ def test_mcts_priors_on_device(temp):
     net.close()
 
 
-class _DeviceBuffers:
-    """Device copies of numpy arrays through the HIP runtime libmfhip.so
-    itself uses (hipMalloc / hipMemcpy / hipFree via ctypes)."""
-
-    def __init__(self):
-        backend.lib()  # loads libamdhip64 as a dependency
-        self.hip = ctypes.CDLL("libamdhip64.so.7")
-        self.hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
-        self.hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                       ctypes.c_int]
-        self.hip.hipFree.argtypes = [ctypes.c_void_p]
-        self.ptrs = []
-
-    def put(self, arr):
-        arr = np.ascontiguousarray(arr)
-        p = ctypes.c_void_p()
-        assert self.hip.hipMalloc(ctypes.byref(p), max(arr.nbytes, 4)) == 0
-        self.ptrs.append(p.value)
-        if arr.nbytes:
-            assert self.hip.hipMemcpy(p.value, arr.ctypes.data, arr.nbytes, 1) == 0
-        return p.value
-
-    def get(self, ptr, like):
-        out = np.empty_like(like)
-        assert self.hip.hipMemcpy(out.ctypes.data, ptr, out.nbytes, 2) == 0
-        return out
-
-    def free(self):
-        for p in self.ptrs:
-            self.hip.hipFree(p)
-        self.ptrs = []
+_DeviceBuffers = gpu_util.DeviceBuffers
 
 
 def test_mcts_priors_device_entry_and_errors():

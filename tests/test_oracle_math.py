@@ -277,3 +277,32 @@ def test_static_pe_step_equals_zero_weight_dynamic_pe():
                          dense).evaluate_batch(planes)
     for k in ("policy", "wdl"):
         assert np.array_equal(a[k].view(np.uint32), b[k].view(np.uint32)), k
+
+
+def test_plan_rules_match_the_reference_plan_test():
+    """The expectations of the reference's own execution-plan test
+    (tests/test_mcts_module.cpp:1638-1729, on make_minimal_attention_weights_file
+    at 115-140: PE_DENSE, default activation mish, FFN activation swish,
+    smolgen default, WDL, moves-left V1), restated against the oracle's plan
+    rules: dense-stage activations, the residual scale of a two-layer body,
+    and the PE_DENSE FFN, input-embedding and attention-policy epsilons."""
+    fmt = oplan.NetFormat(ffn_activation="swish", moves_left=True)
+    act = lambda stage: oplan.dense_activation(fmt, "vanilla", "winner", stage)
+    assert act("policy.vanilla.dense2") == ""             # 1674-1677
+    assert act("policy.vanilla.output") == "mish"         # 1678-1683
+    assert act("value.winner.dense2") == "softmax"        # 1684-1686
+    assert act("moves_left.output") == "relu"             # 1687-1690
+    assert act("body.input_embedding_preprocess") == ""   # 1691-1695
+    assert act("body.input_embedding") == "mish"          # 1696-1701
+    assert act("body.encoder.0.ffn.dense1") == "swish"    # 1702-1706
+    # A two-layer body (1707-1713): residual scale 4^-0.25.
+    steps = oplan.build_plan(fmt, {"body.encoder.0.mha.q_w", "body.encoder.1.ffn.dense1_w"})
+    assert oplan.encoder_layer_count(steps) == 2
+    assert abs(oplan.residual_scale(steps, "body.encoder.1.ffn") -
+               np.float32(4.0) ** np.float32(-0.25)) < 1e-6
+    assert abs(oplan.ffn_ln_eps(fmt, "body.encoder.1.ffn_norm") - 1e-3) < 1e-9   # 1714-1718
+    assert abs(oplan.dense_ln_eps(fmt, "body.input_embedding_norm") - 1e-3) < 1e-9  # 1719-1723
+    assert abs(oplan.attention_ln_eps(fmt, "policy.vanilla.norm") - 1e-6) < 1e-12  # 1724-1729
+    # The classical value head ends in tanh (network_execution_plan.cpp:1098-1106).
+    classical = oplan.NetFormat(wdl=False)
+    assert oplan.dense_activation(classical, "vanilla", "winner", "value.winner.dense2") == "tanh"
