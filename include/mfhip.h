@@ -189,6 +189,26 @@ int mfh_net_eval_device_moves_left(mfh_net *net, int batch,
                                    float *d_policy, float *d_wdl,
                                    float *d_moves_left, void *stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  mfh_net_eval_device without the net's workspace: the
+ * forward's activations, split-K partials and smolgen bias live in the
+ * library's static 64 MiB device array (one copy per device, held until the
+ * process ends), and the call allocates nothing (no hipMalloc, no graph, no
+ * profiler events; the kernels run eagerly on `stream`).  batch must be 1 up
+ * to the largest batch below 32 whose workspace fits that array (mfh_net_info
+ * reports it; for the BT4 shape 15 in BF16X2, 19 in BF16X2_GEMM, 27 in BF16,
+ * and 31 for the 256-wide config-1 net); a larger batch is rejected with
+ * MFH_ERR_INVALID.  Outputs equal
+ * mfh_net_eval_device's bit for bit.  Every call on a device, from any net,
+ * shares that device's array, which keeps the last call's contents: calls
+ * that overlap on one device (different streams, or threads of different
+ * nets) race, so the caller orders them.  Calls on one net are serialised on
+ * the host like the other entry points. */
+int mfh_net_eval_device_noalloc(mfh_net *net, int batch,
+                                const uint64_t *d_masks, const float *d_values,
+                                float *d_policy, float *d_wdl, void *stream);
+
 /* Human-readable description (GetNetworkInfo, reference network.h:47). */
 int mfh_net_info(const mfh_net *net, char *buf, size_t len);
 

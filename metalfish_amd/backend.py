@@ -35,7 +35,7 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_weights_load", "mfh_weights_parse", "mfh_weights_describe",
            "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
            "mfh_net_eval_priors", "mfh_net_eval_priors_device",
-           "mfh_net_eval_device_moves_left")
+           "mfh_net_eval_device_moves_left", "mfh_net_eval_device_noalloc")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -114,6 +114,7 @@ def lib():
             "mfh_net_eval_priors_device": ([vp, i, vp, vp, vp, vp, ctypes.c_float, vp, vp, vp,
                                             vp], i),
             "mfh_net_eval_device_moves_left": ([vp, i, vp, vp, vp, vp, vp, vp], i),
+            "mfh_net_eval_device_noalloc": ([vp, i, vp, vp, vp, vp, vp], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)

@@ -34,6 +34,14 @@
 #include "../host/weights_file.h"
 #include "mfh_kernels.h"
 
+// Device memory of mfh_net_eval_device_noalloc: the workspace of one small
+// forward (activations, split-K partials, smolgen bias) for callers that
+// cannot allocate.  Every device the library runs on holds its own copy until
+// the process ends; host code reaches it only through the address
+// hipGetSymbolAddress gives on that device (ScratchAddress below).
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -50,6 +58,32 @@ int SetError(int code, const std::string &msg) {
       return SetError(MFH_ERR_HIP, std::string(#expr) + ": " +                 \
                                        hipGetErrorString(e_));                 \
   } while (0)
+
+// Device address of `scratch` on each device, resolved once per device with
+// that device current (mfh_net_create); null until then.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_addr[kMaxDevices] = {};
+
+int ResolveScratch(int dev) {
+  if (dev < 0 || dev >= kMaxDevices)
+    return SetError(MFH_ERR_NO_DEVICE, "device ordinal beyond the scratch address table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev])
+    return MFH_OK;
+  void *addr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !addr)
+    return SetError(MFH_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") +
+                                     hipGetErrorString(e));
+  g_scratch_addr[dev] = static_cast<unsigned char *>(addr);
+  return MFH_OK;
+}
+
+unsigned char *ScratchAddress(int dev) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return dev >= 0 && dev < kMaxDevices ? g_scratch_addr[dev] : nullptr;
+}
 
 constexpr int kSquares = 64;
 constexpr int kMaxMoves = 256;  // edges per node (reference src/mcts/search.cpp:49)
@@ -199,6 +233,12 @@ struct mfh_net {
   unsigned char *ws = nullptr;
   size_t ws_bytes = 0;
   std::map<std::string, size_t> ws_off;
+  // Workspace layout of mfh_net_eval_device_noalloc inside the scratch
+  // array, for batches up to noalloc_max_batch (0: the net does not fit).
+  std::map<std::string, size_t> noalloc_off;
+  size_t noalloc_bytes = 0;
+  int noalloc_max_batch = 0;
+  bool noalloc_call = false;  // set during that call: no profiler events
 
   // Recorded after the last work that touched the workspace, on whatever
   // stream it ran; every call waits on it before its own work.  The
@@ -660,12 +700,20 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   return MFH_OK;
 }
 
+// fp32 scratch for the split-K partials LaunchGemm may use on small batches.
+constexpr size_t kSplitKFloats = size_t(8) << 20;
+// What those partials can need at most: LaunchGemm splits K only while the
+// 64 x 64 tiles times the slices stay within 512 workgroups, so the slices
+// of one GEMM hold at most 512 * 64 * 64 floats.
+constexpr size_t kSmallSplitKFloats = size_t(512) * 64 * 64;
+// Largest batch the no-allocation entry point takes: below 2048 token rows
+// the forward runs on one stream and needs no second partials buffer.
+constexpr int kNoAllocMaxBatch = 2048 / kSquares - 1;
+
 // Split-K factor for the small-M GEMMs whose consumer sums partials
 // (smolgen dense1 -> LayerNorm, value dense1 -> value head).  It depends on K
 // only, so every position's result is bit-identical whatever the batch size
 // or the batch it shares a call with.
-// fp32 scratch for the split-K partials LaunchGemm may use on small batches.
-constexpr size_t kSplitKFloats = size_t(8) << 20;
 
 int SplitK(int k) {
   int s = 1;
@@ -674,14 +722,18 @@ int SplitK(int k) {
   return s;
 }
 
-void PlanWorkspace(mfh_net *net) {
-  const Dims &d = net->d;
-  const size_t B = static_cast<size_t>(net->max_batch);
+// Offsets of every workspace tensor for `batch` positions, with split-K
+// partial buffers of `splitk_floats` (a second one for the side stream's
+// smolgen chain when `side`); returns the total size in bytes.
+size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
+                  std::map<std::string, size_t> &ws_off) {
+  const size_t B = static_cast<size_t>(batch);
   const size_t M = B * kSquares;
   size_t off = 0;
+  ws_off.clear();
   auto add = [&](const std::string &name, size_t bytes) {
     off = AlignUp(off, 256);
-    net->ws_off[name] = off;
+    ws_off[name] = off;
     off += bytes;
   };
   // bf16 activations that feed MFMAs get a residual ("_lo") plane in split
@@ -726,17 +778,50 @@ void PlanWorkspace(mfh_net *net) {
   add("mlh", B * 4);
   // Split-K partials of small-batch GEMMs (main stream, and the smolgen
   // chain on the side stream).
-  add("splitk", kSplitKFloats * 4);
-  if (d.smolgen)
-    add("splitk_sg", kSplitKFloats * 4);
+  add("splitk", splitk_floats * 4);
+  if (side)
+    add("splitk_sg", splitk_floats * 4);
   add("policy", B * kPolicy * 4);
   add("wdl", B * 3 * 4);
   // Legal-move priors (mfh_net_eval_priors): offsets, policy indices, priors.
   add("move_offsets", (B + 1) * 4);
   add("move_indices", B * kMaxMoves * 2);
   add("priors", B * kMaxMoves * 4);
-  net->ws_bytes = AlignUp(off, 256);
+  return AlignUp(off, 256);
 }
+
+void PlanWorkspace(mfh_net *net) {
+  net->ws_bytes = PlanLayout(net->d, net->max_batch, kSplitKFloats, net->d.smolgen, net->ws_off);
+  // The no-allocation entry point's layout in the scratch array: the largest
+  // single-stream batch whose workspace fits.
+  net->noalloc_max_batch = 0;
+  for (int b = std::min(net->max_batch, kNoAllocMaxBatch); b >= 1; --b) {
+    const size_t bytes = PlanLayout(net->d, b, kSmallSplitKFloats, false, net->noalloc_off);
+    if (bytes <= kScratchBytes) {
+      net->noalloc_max_batch = b;
+      net->noalloc_bytes = bytes;
+      break;
+    }
+  }
+}
+
+// The workspace one forward uses: the net's own allocation, or the scratch
+// array (mfh_net_eval_device_noalloc).
+struct WsView {
+  unsigned char *base = nullptr;
+  const std::map<std::string, size_t> *off = nullptr;
+  size_t splitk_floats = 0;
+  template <typename T> T *S(const std::string &name) const {
+    return reinterpret_cast<T *>(base + off->at(name));
+  }
+  // Residual plane of a bf16 activation, or null in single precision.
+  std::uint16_t *Lo(const std::string &name) const {
+    auto it = off->find(name + "_lo");
+    return it == off->end() ? nullptr : reinterpret_cast<std::uint16_t *>(base + it->second);
+  }
+};
+
+WsView MainWs(const mfh_net *net) { return WsView{net->ws, &net->ws_off, kSplitKFloats}; }
 
 hipEvent_t TakeEvent(mfh_net *net) {
   if (!net->event_pool.empty()) {
@@ -758,7 +843,7 @@ struct StageTimer {
   bool on = false;
   StageTimer(mfh_net *n, hipStream_t s, const std::string &name, double flops, double bytes)
       : net(n), st(s) {
-    if (!net->profiling)
+    if (!net->profiling || net->noalloc_call)
       return;
     rec.name = name;
     rec.flops = flops;
@@ -802,8 +887,8 @@ std::string GemmKind(const mfh::GemmParams &p, const char *role) {
   return std::string(p.k_splits > 1 ? "gemm_bf16_splitk:" : "gemm_bf16:") + role;
 }
 
-int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
-            float *policy, float *wdl, float *moves_left, hipStream_t st) {
+int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
+            const float *values, float *policy, float *wdl, float *moves_left, hipStream_t st) {
   const Dims &d = net->d;
   const int M = B * kSquares;
   const int E = d.E;
@@ -822,8 +907,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   auto gemm = [&](const std::string &a, int lda, const size_t (&w)[2], int ldw, int m, int n,
                   int k, const float *bias, int act, int mode, void *C, void *C_lo, int ldc) {
     mfh::GemmParams p;
-    p.A = net->S<std::uint16_t>(a);
-    p.A_lo = net->Lo(a);
+    p.A = ws.S<std::uint16_t>(a);
+    p.A_lo = ws.Lo(a);
     p.lda = lda;
     if (net->fp8) {
       p.W8 = net->W<std::uint8_t>(w[0]);
@@ -837,8 +922,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     p.K = k;
     p.bias = bias;
     p.act = act;
-    p.partials = net->S<float>("splitk");
-    p.partials_floats = kSplitKFloats;
+    p.partials = ws.S<float>("splitk");
+    p.partials_floats = ws.splitk_floats;
     p.out_mode = mode;
     p.C = C;
     p.C_lo = C_lo;
@@ -875,32 +960,32 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     lp.gamma = g;
     lp.beta = b;
     lp.y_f32 = y32;
-    lp.y_bf16 = net->S<std::uint16_t>(y16);
-    lp.y_bf16_lo = net->Lo(y16);
+    lp.y_bf16 = ws.S<std::uint16_t>(y16);
+    lp.y_bf16_lo = ws.Lo(y16);
     return lp;
   };
 
-  auto *pe = net->S<float>("pe");
-  auto *pre = net->S<float>("pre");
-  auto *resid = net->S<float>("resid");
+  auto *pe = ws.S<float>("pe");
+  auto *pre = ws.S<float>("pre");
+  auto *resid = ws.S<float>("resid");
   // In the split precisions a LayerNorm's hi + lo output planes ("act") are
   // both the next GEMM's input and the residual of the next residual GEMM,
   // so its fp32 copy is written only where something reads it: the bf16
   // precision's residual, and the body output (debug tensor "body").
   float *res32 = d.split ? nullptr : resid;
-  auto *splitk = net->S<float>("splitk");
-  auto *sg1 = net->S<float>("sg1");
-  auto *sg2 = net->S<float>("sg2");
-  auto *val1 = net->S<float>("val1");
+  auto *splitk = ws.S<float>("splitk");
+  auto *sg1 = ws.S<float>("sg1");
+  auto *sg2 = ws.S<float>("sg2");
+  auto *val1 = ws.S<float>("val1");
 
   // Input planes, dynamic positional encoding, embedding (cpu_network.cpp:
   // 691-890), embedding LayerNorm + gates (1399-1457, 1268-1316).
   {
     StageTimer t(net, st, "input_expand", 0.0, 12.0 * B * kPlanes + 2.0 * M * d.Kin * plane_mult);
     MFH_RUN(mfh::LaunchExpandInputs(
-        masks, values, B, net->S<std::uint16_t>("emb_in"), net->Lo("emb_in"), d.Kin,
+        masks, values, B, ws.S<std::uint16_t>("emb_in"), ws.Lo("emb_in"), d.Kin,
         d.pe_map ? net->W<float>(net->static_pe) : nullptr, d.P,
-        net->S<std::uint16_t>("pos_in"), st, &err_));
+        ws.S<std::uint16_t>("pos_in"), st, &err_));
   }
   if (!d.pe_map) {
     // The PE input holds exact plane values: single precision suffices.
@@ -911,7 +996,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   }
   if (!d.pe_map) {
     StageTimer tpe(net, st, "pe_scatter", 0.0, 4.0 * B * kSquares * d.P);
-    MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, net->S<std::uint16_t>("emb_in"), net->Lo("emb_in"),
+    MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, ws.S<std::uint16_t>("emb_in"), ws.Lo("emb_in"),
                                  d.Kin, st, &err_));
   }
   MFH_RUN(run(gemm("emb_in", d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
@@ -929,8 +1014,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
     if (d.split) {
-      p.resid16 = net->S<std::uint16_t>("act");
-      p.resid16_lo = net->Lo("act");
+      p.resid16 = ws.S<std::uint16_t>("act");
+      p.resid16_lo = ws.Lo("act");
     } else {
       p.resid = resid;
     }
@@ -955,8 +1040,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     if (d.fused_ln && d.split && M >= kPanelMinRows &&
         mfh::PanelGemmShapeOk(mfh::PANEL_OUT_LN, E, k)) {
       mfh::PanelGemmParams pp;
-      pp.A = net->S<std::uint16_t>(a);
-      pp.A_lo = net->Lo(a);
+      pp.A = ws.S<std::uint16_t>(a);
+      pp.A_lo = ws.Lo(a);
       pp.lda = k;
       if (net->fp8) {
         pp.W8 = net->W<std::uint8_t>(w_off[0]);
@@ -970,8 +1055,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       pp.K = k;
       pp.bias = bias;
       pp.out_mode = mfh::PANEL_OUT_LN;
-      pp.C = net->S<std::uint16_t>("act");
-      pp.C_lo = net->Lo("act");
+      pp.C = ws.S<std::uint16_t>("act");
+      pp.C_lo = ws.Lo("act");
       pp.ldc = E;
       if (d.split) {
         pp.resid16 = pp.C;
@@ -1010,8 +1095,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       lp.parts = splits;
       lp.bias = bias;
       if (d.split) {
-        lp.resid16 = net->S<std::uint16_t>("act");
-        lp.resid16_lo = net->Lo("act");
+        lp.resid16 = ws.S<std::uint16_t>("act");
+        lp.resid16_lo = ws.Lo("act");
       } else {
         lp.resid = resid;
       }
@@ -1025,8 +1110,8 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   };
   if (d.input_ffn) {
     MFH_RUN(run(gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
-                     d.act_ffn, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"),
-                     net->Lo("hid"), d.Fi),
+                     d.act_ffn, mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("hid"),
+                     ws.Lo("hid"), d.Fi),
                 "input_ffn1"));
     const int rc = residual_ln("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
                                "input_ffn2", d.alpha, 1e-3f, net->W<float>(net->in_ln_g),
@@ -1055,18 +1140,18 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     const bool big = M >= 2048;
     hipStream_t sg_stream = big && !net->profiling ? net->side : st;
     mfh::AttentionParams ap;
-    ap.qkv = net->S<std::uint16_t>("qkv");
-    ap.qkv_lo = net->Lo("qkv");
+    ap.qkv = ws.S<std::uint16_t>("qkv");
+    ap.qkv_lo = ws.Lo("qkv");
     ap.batch = B;
     ap.heads = heads;
-    ap.ctx = net->S<std::uint16_t>("ctx");
-    ap.ctx_lo = net->Lo("ctx");
+    ap.ctx = ws.S<std::uint16_t>("ctx");
+    ap.ctx_lo = ws.Lo("ctx");
     // Dense1 on the flattened compression (split-K partials summed by the
     // LayerNorm kernel with bias and activation), dense2 (its K slices at
     // few positions summed the same way), then the shared global projection
     // into the attention bias.
     auto smolgen_chain = [&](hipStream_t on) -> int {
-      float *sk = net->S<float>(on == st ? "splitk" : "splitk_sg");
+      float *sk = ws.S<float>(on == st ? "splitk" : "splitk_sg");
       auto chain_gemm = [&](const std::string &a, int lda, const size_t (&w)[2], int ldw, int m,
                             int n, int k, const float *bias, int mode, void *C, void *C_lo,
                             int ldc) {
@@ -1079,7 +1164,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
         const size_t skip = static_cast<size_t>(3) * E;  // rows of Q | K | V
         mfh::GemmParams pc = chain_gemm("act", E, L.qkv_w, E, M, d.C, E,
                                         net->W<float>(L.qkv_b) + skip, mfh::GEMM_OUT_BF16,
-                                        net->S<std::uint16_t>("comp"), net->Lo("comp"), d.C);
+                                        ws.S<std::uint16_t>("comp"), ws.Lo("comp"), d.C);
         if (pc.W8) {
           pc.W8 += skip * E;
           pc.wscale += skip;
@@ -1118,12 +1203,12 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
       MFH_RUN(run(chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares,
                              d.G, nullptr,
                              d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
-                             net->S<void>("bias"), nullptr, kSquares * kSquares),
+                             ws.S<void>("bias"), nullptr, kSquares * kSquares),
                   "smolgen_global", on));
       return MFH_OK;
     };
     if (L.smolgen) {
-      ap.bias = net->S<void>("bias");
+      ap.bias = ws.S<void>("bias");
       ap.bias_f32 = d.split_attn ? 1 : 0;
     }
     if (L.smolgen && big) {
@@ -1139,11 +1224,11 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     }
     mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen && !big ? d.C : 0),
                               E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
-                              net->S<std::uint16_t>("qkv"), net->Lo("qkv"), 3 * E);
+                              ws.S<std::uint16_t>("qkv"), ws.Lo("qkv"), 3 * E);
     if (L.smolgen && !big) {
       pq.split_n = 3 * E;
-      pq.C2 = net->S<std::uint16_t>("comp");
-      pq.C2_lo = net->Lo("comp");
+      pq.C2 = ws.S<std::uint16_t>("comp");
+      pq.C2_lo = ws.Lo("comp");
       pq.ldc2 = d.C;
     }
     MFH_RUN(run(pq, "qkv"));
@@ -1170,7 +1255,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     if (rc != MFH_OK)
       return rc;
     MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b), d.act_ffn,
-                     mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("hid"), net->Lo("hid"), ffn),
+                     mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("hid"), ws.Lo("hid"), ffn),
                 "ffn1"));
     rc = residual_ln("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, eps_ffn,
                      net->W<float>(L.ln2_g), net->W<float>(L.ln2_b), body_out ? resid : res32);
@@ -1188,16 +1273,16 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
   // Q | K, attention policy map, value dense1 (flattened squares) and dense2.
   mfh::GemmParams ph = gemm("act", E, net->head_w, E, M, d.Dp + d.Vd, E,
                             net->W<float>(net->head_b), d.act_default, mfh::GEMM_OUT_BF16,
-                            net->S<std::uint16_t>("pol_emb"), net->Lo("pol_emb"), d.Dp);
+                            ws.S<std::uint16_t>("pol_emb"), ws.Lo("pol_emb"), d.Dp);
   ph.split_n = d.Dp;
-  ph.C2 = net->S<std::uint16_t>("val_emb");
-  ph.C2_lo = net->Lo("val_emb");
+  ph.C2 = ws.S<std::uint16_t>("val_emb");
+  ph.C2_lo = ws.Lo("val_emb");
   ph.ldc2 = d.Vd;
   MFH_RUN(run(ph, "heads"));
   if (d.mlh)
     MFH_RUN(run(gemm("act", E, net->mov_w, E, M, d.Md, E, net->W<float>(net->mov_b),
-                     d.act_default, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("mov_emb"),
-                     net->Lo("mov_emb"), d.Md),
+                     d.act_default, mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("mov_emb"),
+                     ws.Lo("mov_emb"), d.Md),
                 "moves_left"));
   if (d.PL) {
     // Policy encoder layers run on the body output before the policy
@@ -1212,18 +1297,18 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     }
     // The policy rows of the fused head weight come first.
     MFH_RUN(run(gemm("act", E, net->head_w, E, M, d.Dp, E, net->W<float>(net->head_b),
-                     d.act_default, mfh::GEMM_OUT_BF16, net->S<std::uint16_t>("pol_emb"),
-                     net->Lo("pol_emb"), d.Dp),
+                     d.act_default, mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("pol_emb"),
+                     ws.Lo("pol_emb"), d.Dp),
                 "heads"));
   }
   MFH_RUN(run(gemm("pol_emb", d.Dp, net->qk_w, d.Dp, M, 2 * d.Dp, d.Dp,
                    net->W<float>(net->qk_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
-                   net->S<std::uint16_t>("polqk"), net->Lo("polqk"), 2 * d.Dp),
+                   ws.S<std::uint16_t>("polqk"), ws.Lo("polqk"), 2 * d.Dp),
               "policy_qk"));
   {
     StageTimer t(net, st, "policy_map", 2.0 * B * kSquares * kSquares * d.Dp,
                  2.0 * plane_mult * M * 2.0 * d.Dp + 4.0 * B * kPolicy);
-    MFH_RUN(mfh::LaunchPolicyMap(net->S<std::uint16_t>("polqk"), net->Lo("polqk"), B, d.Dp,
+    MFH_RUN(mfh::LaunchPolicyMap(ws.S<std::uint16_t>("polqk"), ws.Lo("polqk"), B, d.Dp,
                                  net->W<float>(net->promo), net->W<std::int16_t>(net->gather),
                                  policy, st, &err_));
   }
@@ -1244,7 +1329,7 @@ int Forward(mfh_net *net, int B, const std::uint64_t *masks, const float *values
     // 1107-1111): ip_mov on square rows (default activation), flatten,
     // ip1_mov (default activation), ip2_mov + relu.
     const int mflat = kSquares * d.Md;
-    auto *mov1 = net->S<float>("mov1");
+    auto *mov1 = ws.S<float>("mov1");
     mfh::GemmParams pm = gemm("mov_emb", mflat, net->mov1_w, mflat, B, d.Mh, mflat, nullptr,
                               mfh::ACT_NONE, mfh::GEMM_OUT_F32, mov1, nullptr, d.Mh);
     pm.k_splits = SplitK(mflat);
@@ -1323,19 +1408,19 @@ int EndUse(mfh_net *net, hipStream_t st) {
 int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *values,
                float *policy, float *wdl, float *moves_left, hipStream_t st) {
   if (!net->graphs || net->profiling)
-    return Forward(net, B, masks, values, policy, wdl, moves_left, st);
+    return Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, st);
   const mfh_net::GraphKey key{B, masks, values, policy, wdl, moves_left};
   auto it = net->graph_execs.find(key);
   if (it == net->graph_execs.end()) {
     if (!net->graph_warm.count(key)) {
       net->graph_warm.insert(key);
-      return Forward(net, B, masks, values, policy, wdl, moves_left, st);
+      return Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, st);
     }
     if (net->graph_execs.size() >= 64)
       DropGraphs(net);
     hipGraph_t graph = nullptr;
     MFH_HIP_CHECK(hipStreamBeginCapture(net->capture_stream, hipStreamCaptureModeThreadLocal));
-    const int rc = Forward(net, B, masks, values, policy, wdl, moves_left, net->capture_stream);
+    const int rc = Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, net->capture_stream);
     const hipError_t end = hipStreamEndCapture(net->capture_stream, &graph);
     if (rc != MFH_OK || end != hipSuccess || !graph) {
       if (graph)
@@ -1343,7 +1428,7 @@ int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *val
       (void)hipGetLastError();
       // Capture is not available here: stay eager from now on.
       net->graphs = false;
-      return rc != MFH_OK ? rc : Forward(net, B, masks, values, policy, wdl, moves_left, st);
+      return rc != MFH_OK ? rc : Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, st);
     }
     hipGraphExec_t exec = nullptr;
     const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
@@ -1351,7 +1436,7 @@ int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *val
     if (inst != hipSuccess) {
       (void)hipGetLastError();
       net->graphs = false;
-      return Forward(net, B, masks, values, policy, wdl, moves_left, st);
+      return Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, st);
     }
     it = net->graph_execs.emplace(key, exec).first;
   }
@@ -1577,6 +1662,9 @@ int mfh_net_create(const mfh_net_desc *desc, const mfh_tensor *tensors, int n_te
   PlanWorkspace(net.get());
 
   MFH_HIP_CHECK(hipSetDevice(dev));
+  rc = ResolveScratch(dev);
+  if (rc != MFH_OK)
+    return rc;
   net->weight_bytes = blob.bytes.size();
   if (hipMalloc(&net->weights, net->weight_bytes) != hipSuccess)
     return SetError(MFH_ERR_OUT_OF_MEMORY, "weight upload allocation failed");
@@ -1753,6 +1841,35 @@ int mfh_net_eval_device_moves_left(mfh_net *net, int batch, const uint64_t *d_ma
   return rc;
 }
 
+int mfh_net_eval_device_noalloc(mfh_net *net, int batch, const uint64_t *d_masks,
+                                const float *d_values, float *d_policy, float *d_wdl,
+                                void *stream) {
+  if (!net)
+    return SetError(MFH_ERR_INVALID, "null net");
+  if (!d_masks || !d_values || !d_policy || !d_wdl)
+    return SetError(MFH_ERR_INVALID, "mfh_net_eval_device_noalloc: null pointer");
+  if (batch < 1 || batch > net->noalloc_max_batch) {
+    std::ostringstream o;
+    o << "mfh_net_eval_device_noalloc: batch " << batch << " outside 1.."
+      << net->noalloc_max_batch << " (the largest batch below " << kNoAllocMaxBatch + 1
+      << " whose workspace fits the " << (kScratchBytes >> 20) << " MiB scratch array)";
+    return SetError(MFH_ERR_INVALID, o.str());
+  }
+  std::lock_guard<std::mutex> lock(net->mu);
+  unsigned char *base = ScratchAddress(net->device);
+  if (!base)
+    return SetError(MFH_ERR_HIP, "scratch array address not resolved on this device");
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  // The forward writes every workspace element it reads, so nothing in the
+  // scratch array needs clearing between calls.
+  const WsView ws{base, &net->noalloc_off, kSmallSplitKFloats};
+  net->noalloc_call = true;
+  const int rc = Forward(net, ws, batch, d_masks, d_values, d_policy, d_wdl,
+                         ws.S<float>("mlh"), static_cast<hipStream_t>(stream));
+  net->noalloc_call = false;
+  return rc;
+}
+
 int mfh_net_eval_priors(mfh_net *net, int batch, const uint64_t *masks, const float *values,
                         const int32_t *move_offsets, const int16_t *move_indices,
                         float softmax_temp, float *priors, float *wdl, float *moves_left) {
@@ -1840,9 +1957,9 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
     o << ", moves left " << d.Md << "/" << d.Mh;
   o << ", activations " << ActName(d.act_default) << "/"
     << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", precision "
-    << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : "bf16") << ", weights bf16 "
-    << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
-    << net->max_batch;
+    << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : "bf16") << ", weights "
+    << (net->fp8 ? "e4m3 " : "bf16 ") << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
+    << net->max_batch << ", no-allocation batch <= " << net->noalloc_max_batch;
   const std::string s = o.str();
   std::snprintf(buf, len, "%s", s.c_str());
   return MFH_OK;
