@@ -30,6 +30,8 @@
 #include "mfh_device.h"
 #include "mfh_kernels.h"
 
+#include <mutex>
+
 namespace mfh {
 namespace {
 
@@ -305,7 +307,312 @@ bool Misaligned(const void *p, std::uintptr_t bytes) {
   return (reinterpret_cast<std::uintptr_t>(p) & (bytes - 1)) != 0;
 }
 
+// ---- Attention with the smolgen bias generated in the kernel ---------------
+//
+// bias[p][q][k] = sum_j gen[p][j] Wg[64 q + k][j] for pair p = (position,
+// head) (reference cpu_network.cpp:1164-1173) is a GEMM whose N dimension is
+// the pairs: Wg is shared by every position and head.  A workgroup of 16
+// waves takes 16 consecutive pairs of the flattened batch x heads list, so
+// one MFMA column tile covers them all: per query tile, wave w computes the
+// bias of query 16 qt + w for the 64 keys and 16 pairs (four 16-row tiles of
+// Wg rows as the A operand, the pairs' gen vectors from LDS as B), and the
+// result goes through LDS to the layout of the score tiles, where wave w
+// runs the attention of pair w.  Two bias buffers: the bias of tile qt + 1
+// is computed while other waves still run tile qt's attention, one barrier
+// per tile.
+//
+// Wg rows stream from L2 (2 MiB, shared by every workgroup and layer); each
+// lane loads 32 contiguous bytes per row and step pair, so a wave load
+// covers whole 128-byte lines: K-slots 8 g .. 8 g + 7 of the two MFMAs of a
+// step pair are elements 64 s2 + 16 g + 8 e .. + 7 (e = 0, 1) of both
+// operands (the MFMA sums over K, so only the pairing matters).
+//
+// V^T, the A operand of ctx^T = V^T P^T, is gathered into registers once
+// (eight 16-bit loads per fragment: lane (fr, g) holds depth 16 dt + fr of
+// the keys 32 u + 4 g + (j % 4) + 16 (j / 4), the same key order as the
+// probabilities it meets), so no LDS is spent on it.
+constexpr int kPairs = 16;                     // pairs (= waves) per workgroup
+constexpr int kBiasQS = kSq + 4;               // floats per staged query row
+constexpr int kBiasPS = 16 * kBiasQS + 4;      // floats per pair (bank spread)
+constexpr int kBiasFloats = kPairs * kBiasPS;  // one query tile's bias
+
+template <bool SPLIT, bool SPLIT_OUT, bool W8>
+__global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenParams ap) {
+  constexpr int PLANES = SPLIT ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float *bias_lds = reinterpret_cast<float *>(smem);  // [2][kBiasFloats]
+  std::uint16_t *gen_lds = reinterpret_cast<std::uint16_t *>(smem + 2 * kBiasFloats * 4);
+  const int G = ap.gen_width, GP = G + 8;  // gen rows padded: 16-byte bank step
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int fr = lane & 15, g = lane >> 4;
+  const int heads = ap.heads, E = heads * kDepth;
+  const int pairs = ap.batch * heads;
+  const int pair0 = blockIdx.x * kPairs;
+  // Waves past the last pair compute on a clamped pair and store nothing.
+  const bool valid = pair0 + w < pairs;
+  const int p = min(pair0 + w, pairs - 1);
+  const int b = p / heads, h = p % heads;
+  const size_t ld = static_cast<size_t>(3) * E;
+  const size_t pos = static_cast<size_t>(b) * kSq * ld;
+  const int qt_begin = blockIdx.y * ap.q_tiles, qt_end = qt_begin + ap.q_tiles;
+
+  // The 16 pairs' gen vectors (rows p * G of [B, H * G]) into LDS.
+  {
+    const int chunks = G / 8;  // 16-byte chunks per row
+    for (int c = threadIdx.x; c < PLANES * kPairs * chunks; c += 1024) {
+      const int pl = c / (kPairs * chunks), rem = c % (kPairs * chunks);
+      const int pr = rem / chunks, ch = rem % chunks;
+      const std::uint16_t *src = (pl ? ap.gen_lo : ap.gen) +
+                                 static_cast<size_t>(min(pair0 + pr, pairs - 1)) * G + ch * 8;
+      *reinterpret_cast<u32x4 *>(gen_lds + (pl * kPairs + pr) * GP + ch * 8) =
+          *reinterpret_cast<const u32x4 *>(src);
+    }
+  }
+  const std::uint16_t *qh = ap.qkv + pos;
+  const std::uint16_t *ql = SPLIT ? ap.qkv_lo + pos : ap.qkv + pos;
+  const int qcol = h * kDepth, kcol = E + h * kDepth, vcol = 2 * E + h * kDepth;
+  // V^T fragments (dt, u): slot j holds V[32 u + 4 g + (j % 4) + 16 (j / 4)][16 dt + fr].
+  bf16x8 vt[PLANES][2][2];
+#pragma unroll
+  for (int pl = 0; pl < PLANES; ++pl)
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const std::uint16_t *col = (pl ? ql : qh) + vcol + 16 * dt + fr;
+        std::uint32_t wd[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j0 = 2 * jj, j1 = 2 * jj + 1;
+          const int k0 = 32 * u + 4 * g + (j0 & 3) + 16 * (j0 >> 2);
+          const int k1 = 32 * u + 4 * g + (j1 & 3) + 16 * (j1 >> 2);
+          wd[jj] = static_cast<std::uint32_t>(col[k0 * ld]) |
+                   (static_cast<std::uint32_t>(col[k1 * ld]) << 16);
+        }
+        vt[pl][dt][u] = __builtin_bit_cast(bf16x8, u32x4{wd[0], wd[1], wd[2], wd[3]});
+      }
+  __syncthreads();  // gen vectors in LDS
+
+  // Bias of query tile qt into buffer qt & 1.
+  auto bias_phase = [&](int qt) {
+    const int qq = qt * 16 + w;
+    f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const size_t row0 = static_cast<size_t>(qq) * kSq + fr;  // Wg row of tile i: row0 + 16 i
+    for (int s2 = 0; s2 < G / 64; ++s2) {
+      const int kc = 64 * s2 + 16 * g;
+      bf16x8 bh[2], bl[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        bh[e] = *reinterpret_cast<const bf16x8 *>(gen_lds + fr * GP + kc + 8 * e);
+        if constexpr (SPLIT)
+          bl[e] = *reinterpret_cast<const bf16x8 *>(gen_lds + (kPairs + fr) * GP + kc + 8 * e);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bf16x8 a[2];
+        if constexpr (W8) {
+          const u32x4 q = *reinterpret_cast<const u32x4 *>(ap.wg8 + (row0 + 16 * i) * G + kc);
+          a[0] = Fp8x8ToBf16(u32x2{q[0], q[1]});
+          a[1] = Fp8x8ToBf16(u32x2{q[2], q[3]});
+        } else {
+          const u32x4 *src = reinterpret_cast<const u32x4 *>(ap.wg + (row0 + 16 * i) * G + kc);
+          a[0] = __builtin_bit_cast(bf16x8, src[0]);
+          a[1] = __builtin_bit_cast(bf16x8, src[1]);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          acc[i] = Mfma(a[e], bh[e], acc[i]);
+          if constexpr (SPLIT)
+            acc[i] = Mfma(a[e], bl[e], acc[i]);
+        }
+      }
+    }
+    // Lane (fr, g) holds bias rows 16 i + 4 g + r (keys) of query qq for
+    // pair fr.
+    float *dst = bias_lds + (qt & 1) * kBiasFloats + fr * kBiasPS + w * kBiasQS + 4 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 v = acc[i];
+      if constexpr (W8) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          v[r] *= ap.wg_scale[qq * kSq + 16 * i + 4 * g + r];
+      }
+      *reinterpret_cast<f32x4 *>(dst + 16 * i) = v;
+    }
+  };
+
+  const float scale = 0.17677669529663687f;  // 1 / sqrt(32)
+  const size_t out_row0 = static_cast<size_t>(b) * kSq;
+  bias_phase(qt_begin);
+  for (int qt = qt_begin; qt < qt_end; ++qt) {
+    // Bias of tile qt visible; every wave is past tile qt - 1's attention,
+    // so buffer (qt + 1) & 1 may be overwritten.
+    __syncthreads();
+    if (qt + 1 < qt_end)
+      bias_phase(qt + 1);
+    // K fragments (A operand of S^T = K Q^T: keys 16 t + fr, depths 8 g ..)
+    // and this tile's Q fragments, from L2 for each tile: registers for K
+    // would not survive the bias phase without spilling.
+    bf16x8 kf[4], kl[4], qf, qfl;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      kf[t] = *reinterpret_cast<const bf16x8 *>(qh + (t * 16 + fr) * ld + kcol + g * 8);
+      if constexpr (SPLIT)
+        kl[t] = *reinterpret_cast<const bf16x8 *>(ql + (t * 16 + fr) * ld + kcol + g * 8);
+    }
+    qf = *reinterpret_cast<const bf16x8 *>(qh + (qt * 16 + fr) * ld + qcol + g * 8);
+    if constexpr (SPLIT)
+      qfl = *reinterpret_cast<const bf16x8 *>(ql + (qt * 16 + fr) * ld + qcol + g * 8);
+    f32x4 s[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      s[t] = Mfma(kf[t], qf, f32x4{0.f, 0.f, 0.f, 0.f});
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        s[t] = Mfma(kl[t], qf, Mfma(kf[t], qfl, s[t]));
+    }
+    const float *bsrc = bias_lds + (qt & 1) * kBiasFloats + w * kBiasPS + fr * kBiasQS + 4 * g;
+    float v[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f32x4 bb = *reinterpret_cast<const f32x4 *>(bsrc + 16 * t);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        v[t][r] = s[t][r] * scale + bb[r];
+    }
+    float m = v[0][0];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        m = fmaxf(m, v[t][r]);
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v[t][r] = __expf(v[t][r] - m);
+        sum += v[t][r];
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = 1.f / sum;
+    bf16x8 pf[2], plo[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      std::uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const float p0 = v[2 * u + j / 4][j % 4] * inv;
+        const float p1 = v[2 * u + j / 4][j % 4 + 1] * inv;
+        const std::uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
+        hw[j / 2] = h0 | (static_cast<std::uint32_t>(h1) << 16);
+        if constexpr (SPLIT)
+          lw[j / 2] = f32_to_bf16(p0 - bf16_to_f32(h0)) |
+                      (static_cast<std::uint32_t>(f32_to_bf16(p1 - bf16_to_f32(h1))) << 16);
+      }
+      pf[u] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+      if constexpr (SPLIT)
+        plo[u] = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+    }
+    f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        o[dt] = Mfma(vt[0][dt][u], pf[u], o[dt]);
+        if constexpr (SPLIT)
+          o[dt] = Mfma(vt[1][dt][u], pf[u], Mfma(vt[0][dt][u], plo[u], o[dt]));
+      }
+    // Lane (fr, g): depths 16 dt + 4 g .. + 3 of query 16 qt + fr.
+    if (valid) {
+      const size_t off = (out_row0 + qt * 16 + fr) * E + h * kDepth + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        std::uint16_t hi[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          hi[r] = f32_to_bf16(o[dt][r]);
+        *reinterpret_cast<u32x2 *>(ap.ctx + off + 16 * dt) =
+            u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
+                  hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
+        if constexpr (SPLIT_OUT) {
+          std::uint32_t lw[2];
+#pragma unroll
+          for (int r = 0; r < 4; r += 2)
+            lw[r / 2] = f32_to_bf16(o[dt][r] - bf16_to_f32(hi[r])) |
+                        (static_cast<std::uint32_t>(
+                             f32_to_bf16(o[dt][r + 1] - bf16_to_f32(hi[r + 1])))
+                         << 16);
+          *reinterpret_cast<u32x2 *>(ap.ctx_lo + off + 16 * dt) = u32x2{lw[0], lw[1]};
+        }
+      }
+    }
+  }
+}
+
+template <bool SPLIT, bool SPLIT_OUT, bool W8>
+hipError_t LaunchSmolgen(const AttentionSmolgenParams &ap, dim3 grid, size_t lds,
+                         hipStream_t stream) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&AttentionSmolgenKernel<SPLIT, SPLIT_OUT, W8>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  });
+  if (attr != hipSuccess)
+    return attr;
+  hipLaunchKernelGGL((AttentionSmolgenKernel<SPLIT, SPLIT_OUT, W8>), grid, dim3(1024), lds,
+                     stream, ap);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+size_t AttentionSmolgenLds(int gen_width, bool gen_split) {
+  return static_cast<size_t>(2) * kBiasFloats * 4 +
+         static_cast<size_t>(gen_split ? 2 : 1) * kPairs * (gen_width + 8) * 2;
+}
+
+hipError_t LaunchAttentionSmolgen(const AttentionSmolgenParams &ap, hipStream_t stream,
+                                  std::string *err) {
+  const bool split = ap.qkv_lo != nullptr;
+  const bool split_out = ap.ctx_lo != nullptr;
+  const bool w8 = ap.wg8 != nullptr;
+  const size_t lds = AttentionSmolgenLds(ap.gen_width, ap.gen_lo != nullptr);
+  if (ap.batch <= 0 || ap.heads <= 0 || !ap.qkv || !ap.ctx || !ap.gen ||
+      (!ap.wg && !ap.wg8) || (ap.wg && ap.wg8) || (w8 && !ap.wg_scale) ||
+      ap.gen_width <= 0 || ap.gen_width % 64 || lds > 160 * 1024 ||
+      (ap.q_tiles != 1 && ap.q_tiles != 2 && ap.q_tiles != 4) ||
+      (split != (ap.gen_lo != nullptr)) || (split && !split_out) ||
+      Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 8) || Misaligned(ap.gen, 16) ||
+      (ap.wg && Misaligned(ap.wg, 16)) || (ap.wg8 && Misaligned(ap.wg8, 16)) ||
+      (split && (Misaligned(ap.qkv_lo, 16) || Misaligned(ap.gen_lo, 16))) ||
+      (split_out && Misaligned(ap.ctx_lo, 8))) {
+    if (err)
+      *err = "attention_smolgen: needs batch, heads > 0, gen width a multiple of 64 whose "
+             "LDS fits, q_tiles 1/2/4, one of wg / wg8 (with scales), aligned operands, and "
+             "gen / qkv / ctx lo planes together";
+    return hipErrorInvalidValue;
+  }
+  const int groups = (ap.batch * ap.heads + kPairs - 1) / kPairs;
+  const dim3 grid(groups, 4 / ap.q_tiles);
+  if (w8)
+    return split ? LaunchSmolgen<true, true, true>(ap, grid, lds, stream)
+           : split_out ? LaunchSmolgen<false, true, true>(ap, grid, lds, stream)
+                       : LaunchSmolgen<false, false, true>(ap, grid, lds, stream);
+  return split ? LaunchSmolgen<true, true, false>(ap, grid, lds, stream)
+         : split_out ? LaunchSmolgen<false, true, false>(ap, grid, lds, stream)
+                     : LaunchSmolgen<false, false, false>(ap, grid, lds, stream);
+}
 
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::string *err) {
   const bool split = ap.qkv_lo != nullptr;

@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -194,6 +195,7 @@ struct Dims {
   bool split = false;       // lo planes on dense-layer inputs (BF16X2, BF16X2_GEMM)
   bool split_attn = false;  // lo planes on attention / smolgen operands (BF16X2)
   bool fused_ln = false;    // residual GEMM + LayerNorm as one row-panel launch
+  bool fused_bias = false;  // smolgen bias generated inside the attention kernel
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -517,6 +519,13 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // PE_DENSE, 1e-5 otherwise.
   d.eps_body = d.pe_map ? 1e-6f : 1e-3f;
   d.eps_emb = d.pe_map ? 1e-5f : 1e-3f;
+  // The attention kernel generates the smolgen bias itself when its LDS
+  // stage fits (gen widths up to 256 in split precision); otherwise, or when
+  // METALFISH_HIP_SMOLGEN_BIAS=hbm asks for it, the global projection runs
+  // as a GEMM into a [B, H, 64, 64] bias tensor that attention reads.
+  const char *bias_env = std::getenv("METALFISH_HIP_SMOLGEN_BIAS");
+  d.fused_bias = d.smolgen && !(bias_env && std::string(bias_env) == "hbm") &&
+                 mfh::AttentionSmolgenLds(d.G, d.split_attn) <= 160 * 1024;
   return MFH_OK;
 }
 
@@ -766,7 +775,8 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   add16a("sg1n", B * (d.Hs ? d.Hs : 1));
   add("sg2", B * (d.HG ? d.HG : 1) * 4);
   add16a("sg2n", B * (d.HG ? d.HG : 1));
-  add("bias", d.smolgen ? B * d.H * kSquares * kSquares * (d.split_attn ? 4 : 2) : 256);
+  add("bias", d.smolgen && !d.fused_bias ? B * d.H * kSquares * kSquares * (d.split_attn ? 4 : 2)
+                                          : 256);
   add16("ctx", M * d.E);
   add16("hid", M * (hid ? hid : 1));
   add16("pol_emb", M * d.Dp);
@@ -1200,6 +1210,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       l2.bias = net->W<float>(L.sg_d2_b);
       l2.act = d.act_smolgen;
       MFH_RUN(run_ln(l2, on));
+      if (d.fused_bias)
+        return MFH_OK;  // attention projects the gen vectors itself
       MFH_RUN(run(chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares,
                              d.G, nullptr,
                              d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
@@ -1207,7 +1219,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
                   "smolgen_global", on));
       return MFH_OK;
     };
-    if (L.smolgen) {
+    if (L.smolgen && !d.fused_bias) {
       ap.bias = ws.S<void>("bias");
       ap.bias_f32 = d.split_attn ? 1 : 0;
     }
@@ -1239,7 +1251,39 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     }
     if (L.smolgen && big && sg_stream != st)
       MFH_HIP_CHECK(hipStreamWaitEvent(st, net->fork_join[2 * li + 1], 0));
-    {
+    if (L.smolgen && d.fused_bias) {
+      // Attention with the smolgen global projection in the kernel
+      // (cpu_network.cpp:1164-1218): the gen vectors ("sg2n") against the
+      // shared Wg, no bias tensor in HBM.
+      mfh::AttentionSmolgenParams sp;
+      sp.qkv = ap.qkv;
+      sp.qkv_lo = ap.qkv_lo;
+      sp.gen = ws.S<std::uint16_t>("sg2n");
+      sp.gen_lo = ws.Lo("sg2n");
+      if (net->fp8) {
+        sp.wg8 = net->W<std::uint8_t>(net->global_w[0]);
+        sp.wg_scale = net->W<float>(net->global_w[1]);
+      } else {
+        sp.wg = net->W<std::uint16_t>(net->global_w[0]);
+      }
+      sp.gen_width = d.G;
+      sp.batch = B;
+      sp.heads = heads;
+      // Enough workgroups for the 256 CUs: one per 16 (position, head)
+      // pairs and all four query tiles at large batches; the query tiles
+      // split over 2 or 4 workgroups below that.
+      const int groups = (B * heads + 15) / 16;
+      sp.q_tiles = groups >= 256 ? 4 : groups >= 128 ? 2 : 1;
+      sp.ctx = ap.ctx;
+      sp.ctx_lo = ap.ctx_lo;
+      const double pairs = static_cast<double>(B) * heads;
+      const double flops =
+          pairs * 2.0 * (2.0 * kSquares * kSquares * 32) + pairs * 2.0 * kSquares * kSquares * d.G;
+      const double bytes = 2.0 * (d.split_attn ? 2.0 : 1.0) * 3.0 * M * E +
+                           2.0 * plane_mult * M * E + 2.0 * (d.split_attn ? 2.0 : 1.0) * pairs * d.G;
+      StageTimer t(net, st, "attention", flops, bytes);
+      MFH_RUN(mfh::LaunchAttentionSmolgen(sp, st, &err_));
+    } else {
       const double heads_total = static_cast<double>(B) * heads;
       const double flops = heads_total * 2.0 * (2.0 * kSquares * kSquares * 32);
       const double bytes = 2.0 * (d.split_attn ? 2.0 : 1.0) * 3.0 * M * E +
@@ -1950,7 +1994,8 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
     << "): attention body E=" << d.E << " L=" << d.L << " H=" << d.H << " FFN=" << d.F
     << " PE=" << d.P << (d.gates ? " gates" : "") << (d.input_ffn ? " input-ffn" : "");
   if (d.smolgen)
-    o << " smolgen C=" << d.C << "/" << d.Hs << "/" << d.G;
+    o << " smolgen C=" << d.C << "/" << d.Hs << "/" << d.G
+      << (d.fused_bias ? " (bias in attention)" : " (bias tensor)");
   o << ", policy attention Dp=" << d.Dp << ", value " << (d.wdl ? "wdl" : "scalar") << " "
     << d.Vd << "/" << d.Vh;
   if (d.mlh)

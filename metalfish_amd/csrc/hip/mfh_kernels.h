@@ -207,6 +207,33 @@ struct AttentionParams {
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream,
                            std::string *err);
 
+// The same attention for smolgen nets with the per-head bias generated in
+// the kernel (reference cpu_network.cpp:1164-1218): for (position b, head
+// h), bias[q][k] = sum_j gen[b][h*G + j] * Wg[q*64 + k][j], where gen is
+// the smolgen dense2 output after its LayerNorm ([B, H*G] bf16, gen_lo its
+// residual plane or null) and Wg the shared global projection [4096, G]
+// (bf16, or e4m3 codes wg8 with row scales wg_scale).  A workgroup takes 16
+// (position, head) pairs and q_tiles of the 4 query tiles; G % 64 == 0.
+struct AttentionSmolgenParams {
+  const std::uint16_t *qkv = nullptr;
+  const std::uint16_t *qkv_lo = nullptr;
+  const std::uint16_t *gen = nullptr;
+  const std::uint16_t *gen_lo = nullptr;
+  const std::uint16_t *wg = nullptr;
+  const std::uint8_t *wg8 = nullptr;
+  const float *wg_scale = nullptr;
+  int gen_width = 0;  // G
+  int batch = 0, heads = 0;
+  int q_tiles = 4;    // query tiles per workgroup: 1, 2 or 4
+  std::uint16_t *ctx = nullptr;
+  std::uint16_t *ctx_lo = nullptr;
+};
+hipError_t LaunchAttentionSmolgen(const AttentionSmolgenParams &ap, hipStream_t stream,
+                                  std::string *err);
+// Dynamic LDS bytes the kernel needs for a gen width (and whether gen has a
+// lo plane); the launcher checks it against the device limit.
+size_t AttentionSmolgenLds(int gen_width, bool gen_split);
+
 // Attention policy map: raw[q,k] = Q_q.K_k / sqrt(Dp), the 8x24 promotion
 // logits, and the 1858-entry gather (cpu_network.cpp:892-1025).
 // qk [B*64, 2*Dp] bf16 (Q | K; qk_lo residual plane or null), promo [4, Dp]

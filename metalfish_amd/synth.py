@@ -89,6 +89,12 @@ SPECS = {
     # channels, embedding input 112 + 64) in place of the dynamic one.
     "cpu_plumbing_pe_map": NetSpec("cpu_plumbing_pe_map", 256, 2, 8, 512, pe_channels=64,
                                    input_ffn=512, policy_dim=256, pe_map=True),
+    # Test net: config 1 with smolgen (16 compressed channels -> 64 hidden ->
+    # 8 heads x 64 gen): 8 heads per position, so the attention kernel's
+    # groups of 16 (position, head) pairs span two positions.
+    "cpu_plumbing_smolgen": NetSpec("cpu_plumbing_smolgen", 256, 2, 8, 512, input_ffn=512,
+                                    smolgen_compress=16, smolgen_hidden=64, smolgen_gen=64,
+                                    policy_dim=256),
     # Test net: config 1 with one encoder layer (8 heads) in the policy head.
     "cpu_plumbing_pol_enc": NetSpec("cpu_plumbing_pol_enc", 256, 2, 8, 512, input_ffn=512,
                                     policy_dim=256, policy_encoders=1, policy_heads=8),
