@@ -197,7 +197,7 @@ int mfh_net_eval_device_moves_left(mfh_net *net, int batch,
  * process ends), and the call allocates nothing (no hipMalloc, no graph, no
  * profiler events; the kernels run eagerly on `stream`).  batch must be 1 up
  * to the largest batch below 32 whose workspace fits that array (mfh_net_info
- * reports it; for the BT4 shape 18 in BF16X2, 21 in BF16X2_GEMM, 31 in BF16,
+ * reports it; for the BT4 shape 15 in BF16X2, 19 in BF16X2_GEMM, 27 in BF16,
  * and 31 for the 256-wide config-1 net); a larger batch is rejected with
  * MFH_ERR_INVALID.  Outputs equal
  * mfh_net_eval_device's bit for bit.  Every call on a device, from any net,

@@ -336,13 +336,14 @@ constexpr int kBiasQS = kSq + 4;               // floats per staged query row
 constexpr int kBiasPS = 16 * kBiasQS + 4;      // floats per pair (bank spread)
 constexpr int kBiasFloats = kPairs * kBiasPS;  // one query tile's bias
 
-template <bool SPLIT, bool SPLIT_OUT, bool W8>
+template <int G, bool SPLIT, bool SPLIT_OUT, bool W8>
 __global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenParams ap) {
   constexpr int PLANES = SPLIT ? 2 : 1;
+  constexpr int GP = G + 8;  // gen rows padded: 16-byte bank step
+  constexpr int STEPS = G / 64;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float *bias_lds = reinterpret_cast<float *>(smem);  // [2][kBiasFloats]
   std::uint16_t *gen_lds = reinterpret_cast<std::uint16_t *>(smem + 2 * kBiasFloats * 4);
-  const int G = ap.gen_width, GP = G + 8;  // gen rows padded: 16-byte bank step
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int fr = lane & 15, g = lane >> 4;
   const int heads = ap.heads, E = heads * kDepth;
@@ -401,7 +402,27 @@ __global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenP
     for (int i = 0; i < 4; ++i)
       acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     const size_t row0 = static_cast<size_t>(qq) * kSq + fr;  // Wg row of tile i: row0 + 16 i
-    for (int s2 = 0; s2 < G / 64; ++s2) {
+    // Wg fragments of step pair s2 for the four row tiles (32 bytes per lane
+    // and row; e4m3: 16 codes), requested one step pair ahead of their MFMAs.
+    auto load_a = [&](int s2, u32x4 (&raw)[4][2]) {
+      const int kc = 64 * s2 + 16 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (W8) {
+          raw[i][0] = *reinterpret_cast<const u32x4 *>(ap.wg8 + (row0 + 16 * i) * G + kc);
+        } else {
+          const u32x4 *src = reinterpret_cast<const u32x4 *>(ap.wg + (row0 + 16 * i) * G + kc);
+          raw[i][0] = src[0];
+          raw[i][1] = src[1];
+        }
+      }
+    };
+    u32x4 cur[4][2], nxt[4][2];
+    load_a(0, cur);
+#pragma unroll
+    for (int s2 = 0; s2 < STEPS; ++s2) {
+      if (s2 + 1 < STEPS)
+        load_a(s2 + 1, nxt);
       const int kc = 64 * s2 + 16 * g;
       bf16x8 bh[2], bl[2];
 #pragma unroll
@@ -414,19 +435,24 @@ __global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenP
       for (int i = 0; i < 4; ++i) {
         bf16x8 a[2];
         if constexpr (W8) {
-          const u32x4 q = *reinterpret_cast<const u32x4 *>(ap.wg8 + (row0 + 16 * i) * G + kc);
-          a[0] = Fp8x8ToBf16(u32x2{q[0], q[1]});
-          a[1] = Fp8x8ToBf16(u32x2{q[2], q[3]});
+          a[0] = Fp8x8ToBf16(u32x2{cur[i][0][0], cur[i][0][1]});
+          a[1] = Fp8x8ToBf16(u32x2{cur[i][0][2], cur[i][0][3]});
         } else {
-          const u32x4 *src = reinterpret_cast<const u32x4 *>(ap.wg + (row0 + 16 * i) * G + kc);
-          a[0] = __builtin_bit_cast(bf16x8, src[0]);
-          a[1] = __builtin_bit_cast(bf16x8, src[1]);
+          a[0] = __builtin_bit_cast(bf16x8, cur[i][0]);
+          a[1] = __builtin_bit_cast(bf16x8, cur[i][1]);
         }
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           acc[i] = Mfma(a[e], bh[e], acc[i]);
           if constexpr (SPLIT)
             acc[i] = Mfma(a[e], bl[e], acc[i]);
+        }
+      }
+      if (s2 + 1 < STEPS) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          cur[i][0] = nxt[i][0];
+          cur[i][1] = nxt[i][1];
         }
       }
     }
@@ -558,21 +584,32 @@ __global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenP
   }
 }
 
-template <bool SPLIT, bool SPLIT_OUT, bool W8>
-hipError_t LaunchSmolgen(const AttentionSmolgenParams &ap, dim3 grid, size_t lds,
-                         hipStream_t stream) {
+template <int G, bool SPLIT, bool SPLIT_OUT, bool W8>
+hipError_t LaunchSmolgenG(const AttentionSmolgenParams &ap, dim3 grid, size_t lds,
+                          hipStream_t stream) {
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
     attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&AttentionSmolgenKernel<SPLIT, SPLIT_OUT, W8>),
+        reinterpret_cast<const void *>(&AttentionSmolgenKernel<G, SPLIT, SPLIT_OUT, W8>),
         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   });
   if (attr != hipSuccess)
     return attr;
-  hipLaunchKernelGGL((AttentionSmolgenKernel<SPLIT, SPLIT_OUT, W8>), grid, dim3(1024), lds,
+  hipLaunchKernelGGL((AttentionSmolgenKernel<G, SPLIT, SPLIT_OUT, W8>), grid, dim3(1024), lds,
                      stream, ap);
   return hipGetLastError();
+}
+
+// Gen widths of Lc0-style smolgen nets: 64, 128, 256.
+template <bool SPLIT, bool SPLIT_OUT, bool W8>
+hipError_t LaunchSmolgen(const AttentionSmolgenParams &ap, dim3 grid, size_t lds,
+                         hipStream_t stream) {
+  switch (ap.gen_width) {
+  case 64: return LaunchSmolgenG<64, SPLIT, SPLIT_OUT, W8>(ap, grid, lds, stream);
+  case 128: return LaunchSmolgenG<128, SPLIT, SPLIT_OUT, W8>(ap, grid, lds, stream);
+  default: return LaunchSmolgenG<256, SPLIT, SPLIT_OUT, W8>(ap, grid, lds, stream);
+  }
 }
 
 }  // namespace
@@ -590,7 +627,8 @@ hipError_t LaunchAttentionSmolgen(const AttentionSmolgenParams &ap, hipStream_t 
   const size_t lds = AttentionSmolgenLds(ap.gen_width, ap.gen_lo != nullptr);
   if (ap.batch <= 0 || ap.heads <= 0 || !ap.qkv || !ap.ctx || !ap.gen ||
       (!ap.wg && !ap.wg8) || (ap.wg && ap.wg8) || (w8 && !ap.wg_scale) ||
-      ap.gen_width <= 0 || ap.gen_width % 64 || lds > 160 * 1024 ||
+      (ap.gen_width != 64 && ap.gen_width != 128 && ap.gen_width != 256) ||
+      lds > 160 * 1024 ||
       (ap.q_tiles != 1 && ap.q_tiles != 2 && ap.q_tiles != 4) ||
       (split != (ap.gen_lo != nullptr)) || (split && !split_out) ||
       Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 8) || Misaligned(ap.gen, 16) ||
@@ -598,8 +636,8 @@ hipError_t LaunchAttentionSmolgen(const AttentionSmolgenParams &ap, hipStream_t 
       (split && (Misaligned(ap.qkv_lo, 16) || Misaligned(ap.gen_lo, 16))) ||
       (split_out && Misaligned(ap.ctx_lo, 8))) {
     if (err)
-      *err = "attention_smolgen: needs batch, heads > 0, gen width a multiple of 64 whose "
-             "LDS fits, q_tiles 1/2/4, one of wg / wg8 (with scales), aligned operands, and "
+      *err = "attention_smolgen: needs batch, heads > 0, gen width 64, 128 or 256, "
+             "q_tiles 1/2/4, one of wg / wg8 (with scales), aligned operands, and "
              "gen / qkv / ctx lo planes together";
     return hipErrorInvalidValue;
   }

@@ -519,12 +519,15 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // PE_DENSE, 1e-5 otherwise.
   d.eps_body = d.pe_map ? 1e-6f : 1e-3f;
   d.eps_emb = d.pe_map ? 1e-5f : 1e-3f;
-  // The attention kernel generates the smolgen bias itself when its LDS
-  // stage fits (gen widths up to 256 in split precision); otherwise, or when
-  // METALFISH_HIP_SMOLGEN_BIAS=hbm asks for it, the global projection runs
-  // as a GEMM into a [B, H, 64, 64] bias tensor that attention reads.
+  // Smolgen bias: by default the global projection runs as a GEMM into a
+  // [B, H, 64, 64] bias tensor that attention reads (measured faster on
+  // MI355X at every batch size: the in-kernel form streams the whole global
+  // projection matrix from L2 for every 16 (position, head) pairs).  With
+  // METALFISH_HIP_SMOLGEN_BIAS=attention the attention kernel generates the
+  // bias itself (gen widths 64, 128 or 256) and no bias tensor exists.
   const char *bias_env = std::getenv("METALFISH_HIP_SMOLGEN_BIAS");
-  d.fused_bias = d.smolgen && !(bias_env && std::string(bias_env) == "hbm") &&
+  d.fused_bias = d.smolgen && bias_env && std::string(bias_env) == "attention" &&
+                 (d.G == 64 || d.G == 128 || d.G == 256) &&
                  mfh::AttentionSmolgenLds(d.G, d.split_attn) <= 160 * 1024;
   return MFH_OK;
 }

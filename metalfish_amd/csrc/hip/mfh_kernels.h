@@ -213,7 +213,7 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream,
 // the smolgen dense2 output after its LayerNorm ([B, H*G] bf16, gen_lo its
 // residual plane or null) and Wg the shared global projection [4096, G]
 // (bf16, or e4m3 codes wg8 with row scales wg_scale).  A workgroup takes 16
-// (position, head) pairs and q_tiles of the 4 query tiles; G % 64 == 0.
+// (position, head) pairs and q_tiles of the 4 query tiles; G is 64, 128 or 256.
 struct AttentionSmolgenParams {
   const std::uint16_t *qkv = nullptr;
   const std::uint16_t *qkv_lo = nullptr;

@@ -215,20 +215,20 @@ def test_single_bf16_whole_round_tiles_against_fp64(m, n, k):
 
 @pytest.mark.parametrize("batch", [1, 64, 256])
 def test_smolgen_bias_in_attention_against_bias_tensor(bt4, batch, monkeypatch):
-    """The attention kernel that generates the smolgen bias itself (query
-    tiles split over 4, 2 and 1 workgroups per 16 pairs at batches 1, 64 and
-    256) against the global-projection GEMM + bias tensor path
-    (METALFISH_HIP_SMOLGEN_BIAS=hbm): both meet the gates against the oracle
-    and agree to fp32 summation-order noise (the bias is the same fp32 sum
-    in a different order)."""
+    """The attention kernel that generates the smolgen bias itself
+    (METALFISH_HIP_SMOLGEN_BIAS=attention; query tiles split over 4, 2 and 1
+    workgroups per 16 pairs at batches 1, 64 and 256) against the default
+    global-projection GEMM + bias tensor path: both meet the gates against
+    the oracle and agree to fp32 summation-order noise (the bias is the same
+    fp32 sum in a different order)."""
     B = batch
     s = np.arange(B)
     ref = {"policy": bt4["ref"]["policy"][s], "wdl": bt4["ref"]["wdl"][s]}
     legal = bt4["legal"][s]
     out = {}
     for mode in ("fused", "hbm"):
-        if mode == "hbm":
-            monkeypatch.setenv("METALFISH_HIP_SMOLGEN_BIAS", "hbm")
+        if mode == "fused":
+            monkeypatch.setenv("METALFISH_HIP_SMOLGEN_BIAS", "attention")
         else:
             monkeypatch.delenv("METALFISH_HIP_SMOLGEN_BIAS", raising=False)
         net = backend.create_network(bt4["spec"], bt4["weights"], max_batch=B, device=0)

@@ -515,26 +515,32 @@ def test_policy_encoder_layers(precision, batch, tmp_path):
             assert np.array_equal(got[k].view(np.uint32), out[k].view(np.uint32)), k
 
 
+@pytest.mark.parametrize("bias", ["attention", "tensor"])
 @pytest.mark.parametrize("precision,batch", [("bf16x2", 5), ("bf16x2_gemm", 5), ("bf16", 5),
                                              ("bf16x2", 40)])
-def test_smolgen_groups_spanning_positions(precision, batch):
-    """A smolgen net with 8 heads: the attention kernel's groups of 16
-    (position, head) pairs span two positions, and at batch 5 the last group
-    holds 8 pairs (its other waves compute and store nothing); gen width 64.
-    Against the oracle; batch 40 is the large-batch path (smolgen chain on
-    the second stream)."""
+def test_smolgen_groups_spanning_positions(precision, batch, bias, monkeypatch):
+    """A smolgen net with 8 heads and gen width 64, with the bias generated
+    in the attention kernel (METALFISH_HIP_SMOLGEN_BIAS=attention: its groups
+    of 16 (position, head) pairs span two positions, and at batch 5 the last
+    group holds 8 pairs whose other waves compute and store nothing) and
+    through the default bias tensor.  Against the oracle; batch 40 is the
+    large-batch path (smolgen chain on the second stream)."""
+    if bias == "attention":
+        monkeypatch.setenv("METALFISH_HIP_SMOLGEN_BIAS", "attention")
+    else:
+        monkeypatch.delenv("METALFISH_HIP_SMOLGEN_BIAS", raising=False)
     spec = synth.SPECS["cpu_plumbing_smolgen"]
     weights = synth.make_weights(spec, seed=7)
     planes, legal = synth.playout_positions(batch, seed=13)
     ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads),
                            weights).evaluate_batch(planes)
     net = backend.create_network(spec, weights, max_batch=batch, precision=precision)
-    assert "bias in attention" in net.info()
+    assert ("bias in attention" in net.info()) == (bias == "attention")
     out = net.evaluate_batch(planes)
     net.close()
     perr = np.abs(out["policy"] - ref["policy"]).max()
     werr = np.abs(out["wdl"] - ref["wdl"]).max()
-    print(f"smolgen H=8 {precision} batch {batch}: policy {perr:.3e} wdl {werr:.3e}")
+    print(f"smolgen H=8 {precision} batch {batch} bias {bias}: policy {perr:.3e} wdl {werr:.3e}")
     assert perr <= _policy_tol(precision) and werr <= WDL_TOL
     if precision == "bf16x2":
         assert perr <= 1e-3 and _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
