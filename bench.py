@@ -18,8 +18,9 @@ Prints one JSON line.  Besides the contract fields it carries:
                     backend) timed on a bounded sample on this host's cores;
   small_batch    -- config 3: p50 / p99 latency, positions/s and weight-stream
                     bandwidth at batches 1, 8, 32, 64;
-  encoder_layer  -- config 4: one encoder layer's time and MFMA utilisation at
-                    batches 256 and 1024 (bf16 activations);
+  encoder_layer  -- config 4: one encoder layer run alone on bf16 N(0, 1)
+                    inputs at batches 256 and 1024: its time, MFMA
+                    utilisation, and each kernel's time and TFLOP/s;
   precisions     -- batch-256 throughput of the other activation precisions;
   fp8_weights    -- config 5: e4m3 weights with per-row scales at batch 1024,
                     and batch-1 latency with the halved weight bytes;
@@ -44,8 +45,6 @@ GFLOP_PER_POSITION = 16.33  # BT4 shape, GEMM + attention + smolgen products
 LAYER_GFLOP_PER_POSITION = 1.033
 METRIC = "NN positions/sec at batch 256 (BT4-shape bf16, 1 GPU)"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_bf16_traffic.txt")
-BODY_ROLES = ("qkv", "out", "ffn1", "ffn2", "smolgen_dense1", "smolgen_dense2",
-              "smolgen_global")
 
 
 def parse_args():
@@ -379,27 +378,53 @@ def main():
                 "device_forward_plus_priors_ms": round(fwd_priors_ms, 4)}
     run.close()
 
-    # Config 4: one encoder layer at the BT4 shape, bf16 activations.
+    # Config 4: one encoder layer alone at the BT4 shape (its GEMMs, smolgen
+    # and attention), bf16 activations with inputs x ~ N(0, 1), through
+    # mfh_debug_encoder_layer: per-layer time from events around the runs,
+    # per-kernel times from the stage profiler.
     layer = {}
     if not args.no_extras:
         lbs = [int(x) for x in args.layer_batches.split(",") if x]
-        lrun = Runner(backend, torch, np, spec, weights, masks, values, max(lbs), "bf16", stream)
+        lnet = backend.create_network(spec, weights, max_batch=max(lbs), device=0,
+                                      precision="bf16")
+        rng = np.random.default_rng(args.seed)
         for b in lbs:
-            lrun.time_steps(b, 2, 3)
-            p = lrun.profile(b, 3)
-            body = gemm_totals(p, BODY_ROLES)
-            attn = p.get("attention", {"ms": 0.0})["ms"]
-            per_layer_ms = (body["ms"] + attn) / 3 / spec.layers
+            x = rng.standard_normal((b * 64, spec.embedding), dtype=np.float32)
+            u = x.view(np.uint32)
+            xb = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+            lnet.encoder_layer_ms(b, 0, 2, xb)
+            per_layer_ms = lnet.encoder_layer_ms(b, 0, 5, xb)
+            lnet.profile_reset()
+            lnet.set_profiling(True)
+            lnet.encoder_layer_ms(b, 0, 3, xb)
+            p = lnet.profile()
+            lnet.set_profiling(False)
+            roles = {}
+            for k, v in sorted(p.items(), key=lambda kv: -kv[1]["ms"]):
+                name = k.split(":", 1)[1] if ":" in k else k
+                r = roles.setdefault(name, {"ms": 0.0, "flops": 0.0})
+                r["ms"] += v["ms"] / 3
+                r["flops"] += v["flops"] / 3
+            role_out = {}
+            for name, r in roles.items():
+                e = {"ms": round(r["ms"], 4)}
+                if r["flops"] and r["ms"]:
+                    tf = r["flops"] / (r["ms"] * 1e-3) / 1e12
+                    e["tflops"] = round(tf, 1)
+                    e["mfma_util_pct"] = round(100.0 * tf / PEAK_BF16_TFLOPS, 1)
+                role_out[name] = e
             enc = gemm_totals(p, ("qkv", "out", "ffn1", "ffn2"))
             enc_tf = enc["flops"] / (enc["ms"] * 1e-3) / 1e12 if enc["ms"] else 0.0
             layer[str(b)] = {
+                "input": "bf16 x ~ N(0, 1), layer 0 of the BT4-shape net, bf16 precision",
                 "layer_ms": round(per_layer_ms, 4),
                 "layer_gflop": round(LAYER_GFLOP_PER_POSITION * b, 1),
                 "layer_mfma_util_pct": round(100.0 * LAYER_GFLOP_PER_POSITION * b * 1e9 /
                                              (per_layer_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 1),
                 "encoder_gemm_tflops": round(enc_tf, 1),
-                "encoder_gemm_mfma_util_pct": round(100.0 * enc_tf / PEAK_BF16_TFLOPS, 1)}
-        lrun.close()
+                "encoder_gemm_mfma_util_pct": round(100.0 * enc_tf / PEAK_BF16_TFLOPS, 1),
+                "kernels": role_out}
+        lnet.close()
 
     # The other activation precisions at the headline batch.
     precisions = {}

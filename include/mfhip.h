@@ -361,6 +361,16 @@ int mfh_debug_panel_gemm(int M, int N, int K, const uint16_t *A,
                          const float *gamma, const float *beta,
                          uint16_t *out_hi, uint16_t *out_lo, float *out_f32);
 
+/* One body encoder layer alone (cpu_network.cpp:1027-1266 and 1318-1457;
+ * the isolated encoder-layer microbenchmark): writes x (bf16 bits
+ * [batch*64, E]; x_lo its lo plane, required in the split precisions) into
+ * the residual stream, runs layer `layer` `iterations` times on the net's
+ * stream (each run on the previous run's output) and returns the average
+ * milliseconds per run.  With profiling on, mfh_net_profile reports the
+ * layer's kernels. */
+int mfh_debug_encoder_layer(mfh_net *net, int batch, int layer, int iterations,
+                            const uint16_t *x, const uint16_t *x_lo, float *ms);
+
 /* Copies a named workspace tensor left by the last eval call to host
  * memory: "body" (fp32 [B*64,E], encoder output; with no encoder layers
  * the input-embedding output) or "policy_qk" (bf16 [B*64,2Dp], the hi plane

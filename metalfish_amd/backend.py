@@ -35,7 +35,8 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_weights_load", "mfh_weights_parse", "mfh_weights_describe",
            "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
            "mfh_net_eval_priors", "mfh_net_eval_priors_device",
-           "mfh_net_eval_device_moves_left", "mfh_net_eval_device_noalloc")
+           "mfh_net_eval_device_moves_left", "mfh_net_eval_device_noalloc",
+           "mfh_debug_encoder_layer")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -115,6 +116,7 @@ def lib():
                                             vp], i),
             "mfh_net_eval_device_moves_left": ([vp, i, vp, vp, vp, vp, vp, vp], i),
             "mfh_net_eval_device_noalloc": ([vp, i, vp, vp, vp, vp, vp], i),
+            "mfh_debug_encoder_layer": ([vp, i, i, i, vp, vp, ctypes.POINTER(ctypes.c_float)], i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -302,6 +304,19 @@ class HipNetwork:
         """Device-resident forward (pointers are device addresses)."""
         _check(lib().mfh_net_eval_device(self._h, batch, d_masks, d_values, d_policy, d_wdl,
                                          stream), "mfh_net_eval_device")
+
+    def encoder_layer_ms(self, batch, layer, iterations, x_bits, x_lo_bits=None):
+        """Runs body encoder layer `layer` alone `iterations` times on the
+        residual stream x (bf16 bits [batch*64, E], x_lo_bits its lo plane in
+        the split precisions) and returns milliseconds per run
+        (mfh_debug_encoder_layer)."""
+        x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+        lo = None if x_lo_bits is None else np.ascontiguousarray(x_lo_bits, dtype=np.uint16)
+        ms = ctypes.c_float()
+        _check(lib().mfh_debug_encoder_layer(self._h, batch, layer, iterations, _ptr(x),
+                                             None if lo is None else _ptr(lo), ctypes.byref(ms)),
+               "mfh_debug_encoder_layer")
+        return ms.value
 
     def set_graphs(self, enabled: bool):
         """Graph capture/replay of the forward (on by default)."""

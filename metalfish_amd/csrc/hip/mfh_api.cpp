@@ -900,8 +900,13 @@ std::string GemmKind(const mfh::GemmParams &p, const char *role) {
   return std::string(p.k_splits > 1 ? "gemm_bf16_splitk:" : "gemm_bf16:") + role;
 }
 
+// The forward pass.  only_layer >= 0 runs body encoder layer only_layer
+// alone on the residual stream already in the workspace (the encoder-layer
+// microbenchmark), nothing before or after it.
 int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
-            const float *values, float *policy, float *wdl, float *moves_left, hipStream_t st) {
+            const float *values, float *policy, float *wdl, float *moves_left, hipStream_t st,
+            int only_layer = -1) {
+  const bool full = only_layer < 0;
   const Dims &d = net->d;
   const int M = B * kSquares;
   const int E = d.E;
@@ -993,34 +998,37 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
 
   // Input planes, dynamic positional encoding, embedding (cpu_network.cpp:
   // 691-890), embedding LayerNorm + gates (1399-1457, 1268-1316).
-  {
-    StageTimer t(net, st, "input_expand", 0.0, 12.0 * B * kPlanes + 2.0 * M * d.Kin * plane_mult);
-    MFH_RUN(mfh::LaunchExpandInputs(
-        masks, values, B, ws.S<std::uint16_t>("emb_in"), ws.Lo("emb_in"), d.Kin,
-        d.pe_map ? net->W<float>(net->static_pe) : nullptr, d.P,
-        ws.S<std::uint16_t>("pos_in"), st, &err_));
-  }
-  if (!d.pe_map) {
-    // The PE input holds exact plane values: single precision suffices.
-    mfh::GemmParams p = gemm("pos_in", kSquares * 12, net->pre_w, kSquares * 12, B,
-                             kSquares * d.P, kSquares * 12, net->W<float>(net->pre_b),
-                             mfh::ACT_NONE, mfh::GEMM_OUT_F32, pe, nullptr, kSquares * d.P);
-    MFH_RUN(run(p, "pe"));
-  }
-  if (!d.pe_map) {
-    StageTimer tpe(net, st, "pe_scatter", 0.0, 4.0 * B * kSquares * d.P);
-    MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, ws.S<std::uint16_t>("emb_in"), ws.Lo("emb_in"),
-                                 d.Kin, st, &err_));
-  }
-  MFH_RUN(run(gemm("emb_in", d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
-                   d.act_default, mfh::GEMM_OUT_F32, pre, nullptr, E),
-                  "embedding"));
-  {
-    mfh::LayerNormParams lp = ln(pre, M, E, d.eps_emb, net->W<float>(net->emb_ln_g),
-                                 net->W<float>(net->emb_ln_b), res32, "act");
-    lp.mult_gate = net->mult_gate ? net->W<float>(net->mult_gate) : nullptr;
-    lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;
-    MFH_RUN(run_ln(lp));
+  if (full) {
+    {
+      StageTimer t(net, st, "input_expand", 0.0,
+                   12.0 * B * kPlanes + 2.0 * M * d.Kin * plane_mult);
+      MFH_RUN(mfh::LaunchExpandInputs(
+          masks, values, B, ws.S<std::uint16_t>("emb_in"), ws.Lo("emb_in"), d.Kin,
+          d.pe_map ? net->W<float>(net->static_pe) : nullptr, d.P,
+          ws.S<std::uint16_t>("pos_in"), st, &err_));
+    }
+    if (!d.pe_map) {
+      // The PE input holds exact plane values: single precision suffices.
+      mfh::GemmParams p = gemm("pos_in", kSquares * 12, net->pre_w, kSquares * 12, B,
+                               kSquares * d.P, kSquares * 12, net->W<float>(net->pre_b),
+                               mfh::ACT_NONE, mfh::GEMM_OUT_F32, pe, nullptr, kSquares * d.P);
+      MFH_RUN(run(p, "pe"));
+    }
+    if (!d.pe_map) {
+      StageTimer tpe(net, st, "pe_scatter", 0.0, 4.0 * B * kSquares * d.P);
+      MFH_RUN(mfh::LaunchScatterPe(pe, B, d.P, ws.S<std::uint16_t>("emb_in"), ws.Lo("emb_in"),
+                                   d.Kin, st, &err_));
+    }
+    MFH_RUN(run(gemm("emb_in", d.Kin, net->emb_w, d.Kin, M, E, d.Kin, net->W<float>(net->emb_b),
+                     d.act_default, mfh::GEMM_OUT_F32, pre, nullptr, E),
+                    "embedding"));
+    {
+      mfh::LayerNormParams lp = ln(pre, M, E, d.eps_emb, net->W<float>(net->emb_ln_g),
+                                   net->W<float>(net->emb_ln_b), res32, "act");
+      lp.mult_gate = net->mult_gate ? net->W<float>(net->mult_gate) : nullptr;
+      lp.add_gate = net->add_gate ? net->W<float>(net->add_gate) : nullptr;
+      MFH_RUN(run_ln(lp));
+    }
   }
   auto residual_gemm = [&](const std::string &a, int k, const size_t (&w_off)[2],
                            const float *bias, const char *role, float alpha) {
@@ -1121,7 +1129,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     MFH_RUN(run_ln(ln(pre, M, E, eps, g, b, y32, "act")));
     return MFH_OK;
   };
-  if (d.input_ffn) {
+  if (full && d.input_ffn) {
     MFH_RUN(run(gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
                      d.act_ffn, mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("hid"),
                      ws.Lo("hid"), d.Fi),
@@ -1308,6 +1316,11 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
                      net->W<float>(L.ln2_g), net->W<float>(L.ln2_b), body_out ? resid : res32);
     return rc;
   };
+  if (!full) {
+    layer_index = only_layer;
+    return encoder_layer(net->layers[only_layer], d.H, d.F, d.eps_body, d.eps_body, d.alpha,
+                         false);
+  }
   for (const Layer &L : net->layers) {
     const int rc = encoder_layer(L, d.H, d.F, d.eps_body, d.eps_body, d.alpha,
                                  &L == &net->layers.back());
@@ -2052,6 +2065,54 @@ int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t byt
   MFH_HIP_CHECK(hipEventSynchronize(net->last_use));
   MFH_HIP_CHECK(hipMemcpy(out, net->ws + net->ws_off.at(ws_name), size, hipMemcpyDeviceToHost));
   return MFH_OK;
+}
+
+int mfh_debug_encoder_layer(mfh_net *net, int batch, int layer, int iterations,
+                            const uint16_t *x, const uint16_t *x_lo, float *ms) {
+  int rc = CheckBatch(net, batch);
+  if (rc != MFH_OK)
+    return rc;
+  if (layer < 0 || layer >= static_cast<int>(net->layers.size()) || iterations < 1 || !x ||
+      !ms || (net->d.split && !x_lo))
+    return SetError(MFH_ERR_INVALID, "mfh_debug_encoder_layer: bad arguments");
+  std::lock_guard<std::mutex> lock(net->mu);
+  MFH_HIP_CHECK(hipSetDevice(net->device));
+  const WsView ws = MainWs(net);
+  const size_t n = static_cast<size_t>(batch) * kSquares * net->d.E;
+  hipStream_t st = net->stream;
+  rc = BeginUse(net, st);
+  if (rc != MFH_OK)
+    return rc;
+  // The layer's input: the residual stream's bf16 planes and, in single
+  // precision, its fp32 copy.
+  MFH_HIP_CHECK(hipMemcpy(ws.S<std::uint16_t>("act"), x, n * 2, hipMemcpyHostToDevice));
+  if (net->d.split) {
+    MFH_HIP_CHECK(hipMemcpy(ws.Lo("act"), x_lo, n * 2, hipMemcpyHostToDevice));
+  } else {
+    std::vector<float> x32(n);
+    for (size_t i = 0; i < n; ++i) {
+      const std::uint32_t u = static_cast<std::uint32_t>(x[i]) << 16;
+      std::memcpy(&x32[i], &u, 4);
+    }
+    MFH_HIP_CHECK(hipMemcpy(ws.S<float>("resid"), x32.data(), n * 4, hipMemcpyHostToDevice));
+  }
+  hipEvent_t a = nullptr, z = nullptr;
+  MFH_HIP_CHECK(hipEventCreate(&a));
+  MFH_HIP_CHECK(hipEventCreate(&z));
+  (void)hipEventRecord(a, st);
+  for (int i = 0; i < iterations && rc == MFH_OK; ++i)
+    rc = Forward(net, ws, batch, nullptr, nullptr, nullptr, nullptr, nullptr, st, layer);
+  (void)hipEventRecord(z, st);
+  (void)EndUse(net, st);
+  const hipError_t sync = hipEventSynchronize(z);
+  float elapsed = 0.f;
+  if (rc == MFH_OK && sync == hipSuccess && hipEventElapsedTime(&elapsed, a, z) == hipSuccess)
+    *ms = elapsed / static_cast<float>(iterations);
+  else if (rc == MFH_OK)
+    rc = SetError(MFH_ERR_HIP, "mfh_debug_encoder_layer: timing failed");
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(z);
+  return rc;
 }
 
 int mfh_net_set_graphs(mfh_net *net, int enabled) {

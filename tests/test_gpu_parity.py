@@ -546,6 +546,43 @@ def test_smolgen_groups_spanning_positions(precision, batch, bias, monkeypatch):
         assert perr <= 1e-3 and _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
 
 
+@pytest.mark.parametrize("default_act,ffn_act,smolgen_act,wdl", [
+    ("mish", "relu_2", "swish", True),    # the legacy smolgen nets' FFN (loader.cpp:115-116)
+    ("relu", "tanh", "tanh", False),      # classical value head: tanh output
+    ("mish", "sigmoid", "sigmoid", True),
+    ("relu", "selu", "relu", True),
+])
+def test_activation_functions(default_act, ffn_act, smolgen_act, wdl):
+    """Every activation of the reference (cpu_network.cpp:302-323) on the
+    device, each against the oracle in a smolgen net: relu^2, tanh, sigmoid
+    and selu as FFN and smolgen activations, relu as the default activation
+    (embedding, policy and value denses), and the classical value head,
+    whose output is tanh (network_execution_plan.cpp:1098-1106)."""
+    import dataclasses
+    spec = dataclasses.replace(synth.SPECS["cpu_plumbing_smolgen"], name="act_test",
+                               default_activation=default_act, ffn_activation=ffn_act,
+                               smolgen_activation=smolgen_act, wdl=wdl)
+    weights = synth.make_weights(spec, seed=17)
+    planes, legal = synth.playout_positions(16, seed=19)
+    fmt = oracle.NetFormat(body_heads=spec.heads, wdl=wdl, default_activation=default_act,
+                           ffn_activation=ffn_act, smolgen_activation=smolgen_act)
+    ref = oracle.OracleNet(fmt, weights).evaluate_batch(planes)
+    net = backend.create_network(spec, weights, max_batch=16)
+    info = net.info()
+    assert f"activations {default_act}/{smolgen_act}/{ffn_act}" in info, info
+    out = net.evaluate_batch(planes)
+    net.close()
+    perr = np.abs(out["policy"] - ref["policy"]).max()
+    verr = np.abs(out["value"] - ref["value"]).max()
+    werr = np.abs(out["wdl"] - ref["wdl"]).max()
+    top1 = _top1_agreement(out["policy"], ref["policy"], legal)
+    print(f"{default_act}/{ffn_act}/{smolgen_act} wdl={wdl}: policy {perr:.3e} value {verr:.3e} "
+          f"wdl {werr:.3e} top1 {top1:.3f}")
+    assert perr <= 1e-3 and verr <= 1e-4 and werr <= 1e-4 and top1 >= 0.995
+    if not wdl:
+        assert np.all(np.abs(out["value"]) <= 1.0)  # tanh range
+
+
 def test_concurrent_callers_share_one_net():
     """Several threads evaluating on one net at once (MCTS workers calling
     the backend concurrently, reference search.cpp:433 and
@@ -575,6 +612,27 @@ def test_concurrent_callers_share_one_net():
     net.close()
     assert not any(t.is_alive() for t in threads)
     assert not bad, bad
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x2"])
+def test_encoder_layer_microbench_entry(precision):
+    """mfh_debug_encoder_layer (the isolated encoder-layer benchmark) runs a
+    body layer alone on a given residual stream and returns a time; bad
+    layer indices and missing lo planes are rejected."""
+    spec = synth.SPECS["cpu_plumbing"]
+    net = backend.create_network(spec, synth.make_weights(spec, seed=2), max_batch=8,
+                                 precision=precision)
+    rng = np.random.default_rng(3)
+    x = _bf16_bits(rng.standard_normal((8 * 64, spec.embedding)).astype(np.float32))
+    lo = np.zeros_like(x) if precision != "bf16" else None
+    ms = net.encoder_layer_ms(8, 1, 3, x, lo)
+    assert 0.0 < ms < 50.0
+    with pytest.raises(RuntimeError, match="bad arguments"):
+        net.encoder_layer_ms(8, spec.layers, 1, x, lo)
+    if precision != "bf16":
+        with pytest.raises(RuntimeError, match="bad arguments"):
+            net.encoder_layer_ms(8, 0, 1, x, None)
+    net.close()
 
 
 def test_bad_batch_rejected():
