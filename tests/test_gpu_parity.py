@@ -151,7 +151,9 @@ def test_bt4_net_parity_16_positions(precision):
 @pytest.mark.parametrize("precision", ["bf16x2", "bf16"])
 def test_bt4_large_batch_tiles(precision):
     """40 positions = 2560 token rows: the dense layers take the large-M tile
-    configurations (the ones the batch-256 benchmark runs)."""
+    configurations: 128 x 128 split tiles for Q|K|V (480 tiles), and the
+    64 x 64 tiles that split precision uses below one 128 x 128 tile per CU
+    for the out-projection, FFN1 and FFN2 (160 / 240 / 160 tiles)."""
     gpu, ref, legal = _compare("bt4", 40, check_packed=False, precision=precision)
     perr = np.abs(gpu["policy"] - ref["policy"]).max()
     werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
