@@ -344,6 +344,29 @@ int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A,
                         const uint16_t *W, const float *bias, int act,
                         float *C);
 
+/* Few-row GEMM (the kernel of the batch-1 encoder layers, reference
+ * cpu_network.cpp:822-890 with the LayerNorm of 424-460 applied to its
+ * input) on host arrays, for tests.  The activation operand is A [M,K] bf16
+ * bits (A_lo: optional lo plane), or, with x set, the LayerNorm of fp32 rows
+ * x [ceil(M / rows_per_src), rows_per_src * K]: row r reads segment
+ * r % rows_per_src of source row r / rows_per_src, normalised over the whole
+ * source row with gamma / beta of that width and eps (ln_split adds the
+ * normalised value's bf16 lo plane to the product; y_hi / y_lo / y32, when
+ * set with rows_per_src == 1, receive the normalised rows [M,K]).  W [N,K]
+ * bf16 bits.  out_mode 0: out = act(A.W^T + bias) as bf16 bits (+ out_lo);
+ * 1: fp32 act(A.W^T + bias); 2: fp32 resid + alpha (A.W^T + bias) with
+ * resid32 or resid_hi + resid_lo.  stats (fp32 modes, optional): per
+ * workgroup part p and row m the sum and sum of squares of the outputs at
+ * stats[2 (p M + m)], *parts parts.  No counterpart in the reference. */
+int mfh_debug_skinny_gemm(int M, int N, int K, const uint16_t *A,
+                          const uint16_t *A_lo, const float *x, int rows_per_src,
+                          float eps, const float *gamma, const float *beta,
+                          int ln_split, const uint16_t *W, const float *bias,
+                          int act, int out_mode, const float *resid32,
+                          const uint16_t *resid_hi, const uint16_t *resid_lo,
+                          float alpha, void *out, uint16_t *out_lo, float *stats,
+                          int *parts, uint16_t *y_hi, uint16_t *y_lo, float *y32);
+
 /* Row-panel GEMM (the kernel behind the batch >= 128 residual + LayerNorm
  * steps, reference cpu_network.cpp:1256-1259 / 1318-1397 then 1399-1457) on
  * host arrays, for tests.  A [M,K] bf16 bits (A_lo: optional split-precision

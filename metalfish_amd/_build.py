@@ -21,7 +21,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 
-HIP_SOURCES = ["hip/gemm.hip", "hip/panel_gemm.hip", "hip/attention.hip", "hip/rowops.hip",
+HIP_SOURCES = ["hip/gemm.hip", "hip/panel_gemm.hip", "hip/skinny_gemm.hip", "hip/attention.hip", "hip/rowops.hip",
                "hip/policy.hip",
                "hip/mfh_api.cpp", "host/policy_tables.cpp"]
 # Host-only parts of libmfhip.so (no device code), compiled with g++.

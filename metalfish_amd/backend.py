@@ -36,7 +36,7 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
            "mfh_net_eval_priors", "mfh_net_eval_priors_device",
            "mfh_net_eval_device_moves_left", "mfh_net_eval_device_noalloc",
-           "mfh_debug_encoder_layer")
+           "mfh_debug_encoder_layer", "mfh_debug_skinny_gemm")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -100,6 +100,9 @@ def lib():
             "mfh_debug_gemm_bf16": ([i, i, i, vp, vp, vp, i, vp], i),
             "mfh_debug_panel_gemm": ([i, i, i, vp, vp, vp, vp, vp, vp, i, i, vp, vp, vp,
                                       ctypes.c_float, ctypes.c_float, vp, vp, vp, vp, vp], i),
+            "mfh_debug_skinny_gemm": ([i, i, i, vp, vp, vp, i, ctypes.c_float, vp, vp, i, vp, vp,
+                                       i, i, vp, vp, vp, ctypes.c_float, vp, vp, vp,
+                                       ctypes.POINTER(i), vp, vp, vp], i),
             "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
             "mfh_debug_quantize_fp8": ([i, i, vp, vp, vp], i),
             "mfh_weights_load": ([ctypes.c_char_p, ctypes.POINTER(vp)], i),
@@ -413,6 +416,47 @@ def panel_gemm(a_bits, w_bits=None, a_lo_bits=None, w8_codes=None, wscale=None, 
         _ptr(keep[3]), _ptr(keep[4]), float(ln.get("alpha", 1.0)), float(ln.get("eps", 1e-3)),
         _ptr(keep[5]), _ptr(keep[6]), _ptr(hi), _ptr(lo), _ptr(y32)), "mfh_debug_panel_gemm")
     return (hi, lo, y32) if layernorm is not None else (hi, lo)
+
+
+def skinny_gemm(w_bits, a_bits=None, a_lo_bits=None, ln=None, bias=None, act="none",
+                out_mode="bf16", resid=None, alpha=1.0, want_lo=False):
+    """Few-row GEMM through mfh_debug_skinny_gemm (a test hook).  The A
+    operand is the bf16 planes ``a_bits`` (+ ``a_lo_bits``), or ``ln`` =
+    dict(x, gamma, beta, eps, rows, rows_per_src=1, split=True): the
+    LayerNorm of fp32 source rows x.  ``out_mode`` "bf16" returns (hi, lo);
+    "f32" and "resid" (``resid`` = fp32 array or (hi, lo) bit planes) return
+    (out, stats [parts, M, 2]); with ``ln`` the normalised rows (hi, lo, fp32)
+    come last."""
+    u16 = lambda x: None if x is None else np.ascontiguousarray(x, dtype=np.uint16)
+    f32 = lambda x: None if x is None else np.ascontiguousarray(x, dtype=np.float32)
+    w_bits = u16(w_bits)
+    n, k = w_bits.shape
+    a_bits, a_lo_bits = u16(a_bits), u16(a_lo_bits)
+    m = a_bits.shape[0] if a_bits is not None else int(ln["rows"])
+    mode = {"bf16": 0, "f32": 1, "resid": 2}[out_mode]
+    out = np.zeros((m, n), np.uint16 if mode == 0 else np.float32)
+    out_lo = np.zeros((m, n), np.uint16) if mode == 0 and want_lo else None
+    stats = np.zeros((max(1, (n + 15) // 16), m, 2), np.float32) if mode else None
+    parts = ctypes.c_int(0)
+    ln = ln or {}
+    rps = int(ln.get("rows_per_src", 1))
+    y = [np.zeros((m, k), t) for t in (np.uint16, np.uint16, np.float32)] if ln and rps == 1 \
+        else [None, None, None]
+    r32 = rh = rl = None
+    if mode == 2:
+        if isinstance(resid, tuple):
+            rh, rl = u16(resid[0]), u16(resid[1])
+        else:
+            r32 = f32(resid)
+    keep = [f32(ln.get("x")), f32(ln.get("gamma")), f32(ln.get("beta")), f32(bias)]
+    _check(lib().mfh_debug_skinny_gemm(
+        m, n, k, _ptr(a_bits), _ptr(a_lo_bits), _ptr(keep[0]), rps, float(ln.get("eps", 1e-3)),
+        _ptr(keep[1]), _ptr(keep[2]), 1 if ln.get("split", True) else 0, _ptr(w_bits),
+        _ptr(keep[3]), ACTIVATION[act], mode, _ptr(r32), _ptr(rh), _ptr(rl), float(alpha),
+        _ptr(out), _ptr(out_lo), _ptr(stats), ctypes.byref(parts), _ptr(y[0]), _ptr(y[1]),
+        _ptr(y[2])), "mfh_debug_skinny_gemm")
+    res = (out, out_lo) if mode == 0 else (out, stats[:parts.value])
+    return res + (tuple(y),) if ln and rps == 1 else res
 
 
 def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",

@@ -196,6 +196,7 @@ struct Dims {
   bool split_attn = false;  // lo planes on attention / smolgen operands (BF16X2)
   bool fused_ln = false;    // residual GEMM + LayerNorm as one row-panel launch
   bool fused_bias = false;  // smolgen bias generated inside the attention kernel
+  bool skinny = true;       // few-row GEMMs for single-position forwards
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -529,6 +530,10 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   d.fused_bias = d.smolgen && bias_env && std::string(bias_env) == "attention" &&
                  (d.G == 64 || d.G == 128 || d.G == 256) &&
                  mfh::AttentionSmolgenLds(d.G, d.split_attn) <= 160 * 1024;
+  // Single-position forward with few-row GEMMs and deferred LayerNorms (on
+  // unless METALFISH_HIP_SKINNY=0, which keeps the split-K path at batch 1).
+  const char *skinny_env = std::getenv("METALFISH_HIP_SKINNY");
+  d.skinny = !(skinny_env && skinny_env[0] == '0');
   return MFH_OK;
 }
 
@@ -789,6 +794,10 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   add16("mov_emb", M * (d.Md ? d.Md : 1));
   add("mov1", (d.mlh ? SplitK(kSquares * d.Md) : 1) * B * (d.Mh ? d.Mh : 1) * 4);
   add("mlh", B * 4);
+  // Row statistics of the single-position smolgen chain's deferred
+  // LayerNorms (partial sums per workgroup): dense1 and dense2 outputs.
+  add("lnst_s1", std::max<size_t>(256, 8 * size_t(mfh::SkinnyGemmParts(d.Hs ? d.Hs : 4))));
+  add("lnst_s2", std::max<size_t>(256, 8 * size_t(mfh::SkinnyGemmParts(d.HG ? d.HG : 4))));
   // Split-K partials of small-batch GEMMs (main stream, and the smolgen
   // chain on the side stream).
   add("splitk", splitk_floats * 4);
@@ -824,6 +833,7 @@ struct WsView {
   unsigned char *base = nullptr;
   const std::map<std::string, size_t> *off = nullptr;
   size_t splitk_floats = 0;
+
   template <typename T> T *S(const std::string &name) const {
     return reinterpret_cast<T *>(base + off->at(name));
   }
@@ -1141,6 +1151,80 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       return rc;
   }
 
+  // Single position (M <= 64 token rows, bf16 weights): the smolgen chain
+  // runs as three few-row GEMM launches instead of six (split-K GEMMs with
+  // their LayerNorm and reduce launches).  dense1 writes its activated rows
+  // with their partial row statistics, dense2 applies dense1's LayerNorm as
+  // it loads them, and the global projection applies dense2's (each of its
+  // rows one head's gen-wide segment of the position's row).
+  const bool few_row_smolgen =
+      d.smolgen && d.skinny && M <= mfh::kSkinnyMaxRows && B * d.H <= mfh::kSkinnyMaxRows &&
+      !net->fp8 && !d.fused_bias && d.HG <= 8192 &&
+      mfh::SkinnyShapeOk(B, d.Hs, kSquares * d.C) && mfh::SkinnyShapeOk(B, d.HG, d.Hs) &&
+      mfh::SkinnyShapeOk(B * d.H, kSquares * kSquares, d.G);
+  auto run_sk = [&](const mfh::SkinnyParams &p, const char *role) {
+    const double flops = 2.0 * p.M * p.N * p.K;
+    const double bytes = 2.0 * p.N * p.K + 4.0 * p.M * p.K + 4.0 * p.M * p.N;
+    StageTimer t(net, st, std::string("gemm_bf16:") + role, flops, bytes);
+    return mfh::LaunchSkinnyGemm(p, st, &err_);
+  };
+  auto smolgen_few_row = [&](const Layer &L) -> int {
+    auto base = [&](const size_t (&w)[2], int m, int n, int k, const float *bias, int act,
+                    int mode, void *C, int ldc) {
+      mfh::SkinnyParams p;
+      p.W = net->W<std::uint16_t>(w[0]);
+      p.ldw = k;
+      p.M = m;
+      p.N = n;
+      p.K = k;
+      p.bias = bias;
+      p.act = act;
+      p.out_mode = mode;
+      p.C = C;
+      p.ldc = ldc;
+      return p;
+    };
+    const int flat = kSquares * d.C;
+    mfh::SkinnyParams p1 = base(L.sg_d1_w, B, d.Hs, flat, net->W<float>(L.sg_d1_b),
+                                d.act_smolgen, mfh::SKINNY_OUT_F32, ws.S<float>("sg1"), d.Hs);
+    p1.a16 = ws.S<std::uint16_t>("comp");
+    p1.a16_lo = ws.Lo("comp");
+    p1.lda = flat;
+    p1.stats_out = ws.S<float>("lnst_s1");
+    MFH_RUN(run_sk(p1, "smolgen_dense1"));
+    mfh::SkinnyParams p2 = base(L.sg_d2_w, B, d.HG, d.Hs, net->W<float>(L.sg_d2_b),
+                                d.act_smolgen, mfh::SKINNY_OUT_F32, ws.S<float>("sg2"), d.HG);
+    p2.x = ws.S<float>("sg1");
+    p2.ldx = d.Hs;
+    p2.ln_stats = ws.S<float>("lnst_s1");
+    p2.ln_parts = mfh::SkinnyGemmParts(d.Hs);
+    p2.ln_rows = B;
+    p2.ln_width = d.Hs;
+    p2.ln_eps = 1e-3f;
+    p2.gamma = net->W<float>(L.sg_ln1_g);
+    p2.beta = net->W<float>(L.sg_ln1_b);
+    p2.ln_split = d.split_attn;
+    p2.stats_out = ws.S<float>("lnst_s2");
+    MFH_RUN(run_sk(p2, "smolgen_dense2"));
+    mfh::SkinnyParams pg =
+        base(net->global_w, B * d.H, kSquares * kSquares, d.G, nullptr, mfh::ACT_NONE,
+             d.split_attn ? mfh::SKINNY_OUT_F32 : mfh::SKINNY_OUT_BF16, ws.S<void>("bias"),
+             kSquares * kSquares);
+    pg.x = ws.S<float>("sg2");
+    pg.ldx = d.HG;
+    pg.rows_per_src = d.H;
+    pg.ln_stats = ws.S<float>("lnst_s2");
+    pg.ln_parts = mfh::SkinnyGemmParts(d.HG);
+    pg.ln_rows = B;
+    pg.ln_width = d.HG;
+    pg.ln_eps = 1e-3f;
+    pg.gamma = net->W<float>(L.sg_ln2_g);
+    pg.beta = net->W<float>(L.sg_ln2_b);
+    pg.ln_split = d.split_attn;
+    MFH_RUN(run_sk(pg, "smolgen_global"));
+    return MFH_OK;
+  };
+
   int layer_index = 0;  // encoder layers run so far (their fork / join events)
   // One encoder layer (cpu_network.cpp:1027-1266, 1318-1457) on resid/act:
   // `heads` attention heads, FFN width `ffn`, LayerNorm epsilons after the
@@ -1172,6 +1256,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // few positions summed the same way), then the shared global projection
     // into the attention bias.
     auto smolgen_chain = [&](hipStream_t on) -> int {
+      if (few_row_smolgen)
+        return smolgen_few_row(L);
       float *sk = ws.S<float>(on == st ? "splitk" : "splitk_sg");
       auto chain_gemm = [&](const std::string &a, int lda, const size_t (&w)[2], int ldw, int m,
                             int n, int k, const float *bias, int mode, void *C, void *C_lo,
@@ -1321,6 +1407,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     return encoder_layer(net->layers[only_layer], d.H, d.F, d.eps_body, d.eps_body, d.alpha,
                          false);
   }
+
   for (const Layer &L : net->layers) {
     const int rc = encoder_layer(L, d.H, d.F, d.eps_body, d.eps_body, d.alpha,
                                  &L == &net->layers.back());
@@ -2382,6 +2469,105 @@ struct DebugBuffers {
     return static_cast<T *>(d);
   }
 };
+
+int mfh_debug_skinny_gemm(int M, int N, int K, const uint16_t *A, const uint16_t *A_lo,
+                          const float *x, int rows_per_src, float eps, const float *gamma,
+                          const float *beta, int ln_split, const uint16_t *W, const float *bias,
+                          int act, int out_mode, const float *resid32, const uint16_t *resid_hi,
+                          const uint16_t *resid_lo, float alpha, void *out, uint16_t *out_lo,
+                          float *stats, int *parts, uint16_t *y_hi, uint16_t *y_lo,
+                          float *y32) {
+  if (M <= 0 || N <= 0 || K <= 0 || (!A && !x) || !W || !out || out_mode < 0 || out_mode > 2 ||
+      rows_per_src < 1)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_skinny_gemm: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  const size_t nw = static_cast<size_t>(N) * K, nc = static_cast<size_t>(M) * N;
+  const int src_rows = (M + rows_per_src - 1) / rows_per_src;
+  const int width = rows_per_src * K;
+  try {
+    DebugBuffers buf;
+    mfh::SkinnyParams p;
+    std::vector<float> st;
+    if (x) {
+      // One statistics part per source row, summed on the host.
+      st.resize(2 * static_cast<size_t>(src_rows));
+      for (int r = 0; r < src_rows; ++r) {
+        float s = 0.f, ss = 0.f;
+        for (int c = 0; c < width; ++c) {
+          const float v = x[static_cast<size_t>(r) * width + c];
+          s += v;
+          ss += v * v;
+        }
+        st[2 * r] = s;
+        st[2 * r + 1] = ss;
+      }
+      p.x = buf.Put(x, static_cast<size_t>(src_rows) * width);
+      p.ldx = width;
+      p.rows_per_src = rows_per_src;
+      p.ln_stats = buf.Put(st.data(), st.size());
+      p.ln_parts = 1;
+      p.ln_rows = src_rows;
+      p.ln_width = width;
+      p.ln_eps = eps;
+      p.gamma = buf.Put(gamma, width);
+      p.beta = buf.Put(beta, width);
+      p.ln_split = ln_split != 0;
+      p.y16 = y_hi ? buf.Put<std::uint16_t>(nullptr, static_cast<size_t>(M) * K, false) : nullptr;
+      p.y16_lo = y_lo ? buf.Put<std::uint16_t>(nullptr, static_cast<size_t>(M) * K, false)
+                      : nullptr;
+      p.y32 = y32 ? buf.Put<float>(nullptr, static_cast<size_t>(M) * K, false) : nullptr;
+      p.ldy = K;
+    } else {
+      p.a16 = buf.Put(A, static_cast<size_t>(M) * K);
+      p.a16_lo = buf.Put(A_lo, static_cast<size_t>(M) * K);
+      p.lda = K;
+    }
+    p.W = buf.Put(W, nw);
+    p.ldw = K;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.bias = buf.Put(bias, N);
+    p.act = ActFromProto(act, mfh::ACT_RELU);
+    if (act == MFH_ACTIVATION_NONE || act == MFH_ACTIVATION_DEFAULT)
+      p.act = mfh::ACT_NONE;
+    p.out_mode = out_mode;
+    const size_t out_bytes = out_mode == mfh::SKINNY_OUT_BF16 ? 2 : 4;
+    p.C = buf.Put<unsigned char>(nullptr, nc * out_bytes, false);
+    p.C_lo = out_lo ? buf.Put<std::uint16_t>(nullptr, nc, false) : nullptr;
+    p.ldc = N;
+    if (out_mode == mfh::SKINNY_OUT_RESID) {
+      p.resid = buf.Put(resid32, nc);
+      p.resid16 = buf.Put(resid_hi, nc);
+      p.resid16_lo = buf.Put(resid_lo, nc);
+      p.ldr = N;
+      p.alpha = alpha;
+    }
+    const int np = mfh::SkinnyGemmParts(N);
+    if (parts)
+      *parts = np;
+    if (stats && out_mode != mfh::SKINNY_OUT_BF16)
+      p.stats_out = buf.Put<float>(nullptr, 2 * static_cast<size_t>(np) * M, false);
+    std::string err;
+    if (mfh::LaunchSkinnyGemm(p, nullptr, &err) != hipSuccess)
+      return SetError(MFH_ERR_INVALID, err);
+    const size_t ny = static_cast<size_t>(M) * K;
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(out, p.C, nc * out_bytes, hipMemcpyDeviceToHost) != hipSuccess ||
+        (p.C_lo && hipMemcpy(out_lo, p.C_lo, nc * 2, hipMemcpyDeviceToHost) != hipSuccess) ||
+        (p.stats_out && hipMemcpy(stats, p.stats_out, 8 * static_cast<size_t>(np) * M,
+                                  hipMemcpyDeviceToHost) != hipSuccess) ||
+        (p.y16 && hipMemcpy(y_hi, p.y16, ny * 2, hipMemcpyDeviceToHost) != hipSuccess) ||
+        (p.y16_lo && hipMemcpy(y_lo, p.y16_lo, ny * 2, hipMemcpyDeviceToHost) != hipSuccess) ||
+        (p.y32 && hipMemcpy(y32, p.y32, ny * 4, hipMemcpyDeviceToHost) != hipSuccess))
+      return SetError(MFH_ERR_HIP, "skinny gemm execution failed");
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_HIP, e.what());
+  }
+  return MFH_OK;
+}
 
 int mfh_debug_panel_gemm(int M, int N, int K, const uint16_t *A, const uint16_t *A_lo,
                          const uint16_t *W, const uint8_t *W8, const float *wscale,

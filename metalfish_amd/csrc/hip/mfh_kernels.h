@@ -134,6 +134,81 @@ struct PanelGemmParams {
 bool PanelGemmShapeOk(int out_mode, int N, int K);
 hipError_t LaunchPanelGemm(const PanelGemmParams &p, hipStream_t stream, std::string *err);
 
+// Few-row GEMM (M <= 64, the single-position smolgen chain): C = A . W^T with
+// the whole K per workgroup, so no split-K partials and no reduce launch.  A
+// workgroup of 16 waves owns 16 * NT output columns for all M rows; its
+// waves split the M rows into 16-row tiles and K into equal parts, load
+// their fragments straight from global memory into registers, and sum the
+// K parts through LDS in a fixed order.
+//   A operand: the bf16 planes a16 (+ a16_lo), or, with `x` set, the
+//   LayerNorm of fp32 rows computed on the fly:
+//     A[r][k] = (x[s][c0 + k] - mean_s) * inv_std_s * gamma[c0 + k]
+//               + beta[c0 + k],  s = r / rows_per_src,
+//               c0 = (r % rows_per_src) * K,
+//   with mean / variance from ln_parts partial (sum, sum of squares) pairs
+//   per source row (ln_stats[part * ln_rows + s], as written by stats_out)
+//   over ln_width columns: var = E[x^2] - mean^2 clamped at 0, inv_std =
+//   1 / sqrt(var + eps) (reference cpu_network.cpp:424-460).  ln_split adds
+//   the bf16 lo plane of the normalised value to the product.  With y16 set
+//   the normalised rows are also stored (hi to y16, lo to y16_lo, fp32 to
+//   y32, stride ldy; rows_per_src must be 1), each 64-wide K block by one
+//   workgroup.
+//   Outputs (row m, columns n .. n + 3 per lane):
+//     SKINNY_OUT_BF16   act(acc + bias) -> bf16 hi (+ lo) planes, columns at
+//                       or past split_n to C2 / C2_lo (ldc2)
+//     SKINNY_OUT_F32    act(acc + bias) -> fp32
+//     SKINNY_OUT_RESID  resid + alpha * (acc + bias) -> fp32, the residual
+//                       fp32 `resid` or the planes resid16 + resid16_lo
+//   stats_out (fp32 modes): per workgroup and row, the sum and sum of squares
+//   of the stored values over its columns, at stats_out[2 * (blockIdx * M +
+//   m)], for a later LayerNorm of these rows.
+// Constraints (checked by LaunchSkinnyGemm): SkinnyShapeOk(M, N, K)
+// (1 <= M <= 64, N % 4 == 0, K % 64 == 0 with the K parts dividing K / 64),
+// 16-byte aligned operands, lda / ldw / ldy % 8 == 0, ldx % 4 == 0.
+enum SkinnyOut : int { SKINNY_OUT_BF16 = 0, SKINNY_OUT_F32 = 1, SKINNY_OUT_RESID = 2 };
+constexpr int kSkinnyMaxRows = 64;
+struct SkinnyParams {
+  const std::uint16_t *a16 = nullptr;
+  const std::uint16_t *a16_lo = nullptr;
+  int lda = 0;
+  const float *x = nullptr;
+  int ldx = 0;
+  int rows_per_src = 1;
+  const float *ln_stats = nullptr;
+  int ln_parts = 0, ln_rows = 0, ln_width = 0;
+  float ln_eps = 1e-5f;
+  const float *gamma = nullptr, *beta = nullptr;
+  bool ln_split = false;
+  std::uint16_t *y16 = nullptr;
+  std::uint16_t *y16_lo = nullptr;
+  float *y32 = nullptr;
+  int ldy = 0;
+  const std::uint16_t *W = nullptr;
+  int ldw = 0;
+  int M = 0, N = 0, K = 0;
+  int out_mode = SKINNY_OUT_BF16;
+  const float *bias = nullptr;
+  int act = -1;
+  void *C = nullptr;
+  std::uint16_t *C_lo = nullptr;
+  int ldc = 0;
+  int split_n = 1 << 30;
+  void *C2 = nullptr;
+  std::uint16_t *C2_lo = nullptr;
+  int ldc2 = 0;
+  const float *resid = nullptr;
+  const std::uint16_t *resid16 = nullptr;
+  const std::uint16_t *resid16_lo = nullptr;
+  int ldr = 0;
+  float alpha = 1.0f;
+  float *stats_out = nullptr;
+};
+// Workgroups LaunchSkinnyGemm uses for N columns (the ln_parts of a
+// LayerNorm that reads its stats_out).
+int SkinnyGemmParts(int N);
+bool SkinnyShapeOk(int M, int N, int K);
+hipError_t LaunchSkinnyGemm(const SkinnyParams &p, hipStream_t stream, std::string *err);
+
 // Packed planes -> embedding input rows and the dynamic-PE input.
 //   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values; with static_pe
 //   ([64][pe_ch] fp32, PE_MAP nets) cols 112..111+pe_ch the square's table

@@ -295,6 +295,48 @@ def test_bt4_small_batch_parity(batch):
     assert _top1_agreement(pol, ref["policy"][:n], legal[:n]) == 1.0
 
 
+@pytest.mark.parametrize("spec_name,precision", [
+    ("bt4", "bf16x2"), ("bt4", "bf16x2_gemm"), ("bt4", "bf16"),
+    ("cpu_plumbing_smolgen", "bf16x2"), ("cpu_plumbing_smolgen", "bf16")])
+def test_single_position_few_row_path(spec_name, precision, monkeypatch):
+    """At batch 1 the smolgen chain runs as three few-row GEMM launches, each
+    of its LayerNorms applied by the GEMM that reads its output (the global
+    projection normalises each position's whole gen row and reads one head's
+    segment).  Position by position against the oracle, and against the
+    split-K chain with separate LayerNorm launches (METALFISH_HIP_SKINNY=0):
+    the two differ only in fp32 summation order."""
+    spec = synth.SPECS[spec_name]
+    seed = 0 if spec_name == "bt4" else 7
+    weights, planes, legal, ref = _reference(spec_name, 16, seed, 0)
+    n = 3
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("METALFISH_HIP_SKINNY", mode)
+        net = backend.create_network(spec, weights, max_batch=1, device=0, precision=precision)
+        res = [net.evaluate(planes[i]) for i in range(n)]
+        net.close()
+        outs[mode] = {k: np.stack([r[k] for r in res]) for k in ("policy", "wdl")}
+    few, splitk = outs["1"], outs["0"]
+    for name, o in (("few-row", few), ("split-K", splitk)):
+        assert np.isfinite(o["policy"]).all() and np.isfinite(o["wdl"]).all(), name
+    perr = np.abs(few["policy"] - ref["policy"][:n]).max()
+    werr = np.abs(few["wdl"] - ref["wdl"][:n]).max()
+    pdiff = np.abs(few["policy"] - splitk["policy"]).max()
+    wdiff = np.abs(few["wdl"] - splitk["wdl"]).max()
+    print(f"{spec_name} {precision} batch 1 few-row: policy {perr:.3e} wdl {werr:.3e} "
+          f"(vs split-K path: {pdiff:.3e} / {wdiff:.3e})")
+    assert perr <= _policy_tol(precision) and werr <= WDL_TOL
+    if precision != "bf16x2":
+        # Single-bf16 operands (attention in bf16x2_gemm, everything in
+        # bf16): one rounding of an activation can move with the summation
+        # order, and the split-K path itself sits this far from the oracle.
+        assert pdiff <= 2e-2 and wdiff <= 5e-3
+    else:
+        assert perr <= 1e-3 and werr <= 1e-4
+        assert pdiff <= 1e-4 and wdiff <= 1e-5
+        assert _top1_agreement(few["policy"], ref["policy"][:n], legal[:n]) == 1.0
+
+
 def test_graph_replay_matches_eager():
     """The forward replayed from a captured HIP graph gives the eager bits,
     on every replay, with eager work on the same net in between."""
