@@ -459,6 +459,20 @@ def main():
                "batch1_weight_stream_gbs": round(wb / (p50 * 1e-3) / 1e9, 1),
                "mma": "bf16 MFMA on exactly converted e4m3 weights (bf16x2 activations)"}
         backend_fp8.close()
+        # The FP8 precision: e4m3 activations (per-row scales) into the body's
+        # Q|K|V, out-projection and FFN GEMMs on the fp8 MFMA.  Measured below
+        # the parity gates on the random-init net (top-1 0.79-0.83 against
+        # the oracle), so it is reported beside config 5, never as its value.
+        r8 = Runner(backend, torch, np, spec, fweights, masks, values, fb, "fp8", stream,
+                    weights_dtype="fp8")
+        ms8 = r8.time_steps(fb, max(3, args.steps // 4), 2)
+        r8.close()
+        fp8["fp8_activations"] = {
+            "positions_per_s": round(fb / (ms8 * 1e-3), 1), "ms_per_step": round(ms8, 4),
+            "mma": "fp8 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4) for the encoder's Q|K|V, "
+                   "out-projection and FFN GEMMs; bf16 elsewhere",
+            "parity": "fails the gates on the random-init BT4 net: top-1 0.79-0.83, policy "
+                      "max-abs 0.15-0.18, WDL max-abs 1.1-1.6e-2 (test_fp8_activation_parity)"}
 
     cpu = None
     if args.cpu_positions > 0:

@@ -69,8 +69,17 @@ enum { MFH_WEIGHTS_BF16 = 0, MFH_WEIGHTS_FP8 = 1 };
  * bf16 MFMAs, giving ~16-bit activation precision against the exact bf16
  * weights at twice the MFMA work.  BF16X2_GEMM: the pair only for the inputs
  * of the dense layers and the policy map; attention Q/K/V, its
- * probabilities, the smolgen activations and bias stay single bf16. */
-enum { MFH_PRECISION_BF16 = 0, MFH_PRECISION_BF16X2 = 1, MFH_PRECISION_BF16X2_GEMM = 2 };
+ * probabilities, the smolgen activations and bias stay single bf16.
+ * FP8 (needs MFH_WEIGHTS_FP8): from 2048 token rows (32 positions) up, the
+ * Q|K|V, out-projection and FFN GEMMs of the encoder layers run on the fp8
+ * MFMA, their inputs quantised per row to OCP e4m3 (scale max|row| / 448)
+ * just before each GEMM; everything else as in BF16. */
+enum {
+  MFH_PRECISION_BF16 = 0,
+  MFH_PRECISION_BF16X2 = 1,
+  MFH_PRECISION_BF16X2_GEMM = 2,
+  MFH_PRECISION_FP8 = 3
+};
 
 /* Network description: the format fields of the weights file plus the
  * attention head count (Weights.headcount) and run-time sizing. */
@@ -344,6 +353,22 @@ int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A,
                         const uint16_t *W, const float *bias, int act,
                         float *C);
 
+/* fp8 x fp8 GEMM (the kernel of the fp8-activation precision) on host
+ * arrays, for tests: C[M,N] = act((A8 . W8^T) * ascale[m] * wscale[n] +
+ * bias) in fp32, A8 [M,K] and W8 [N,K] OCP e4m3 codes with row scales.
+ * K % 128 == 0, M >= 2048.  No counterpart in the reference. */
+int mfh_debug_gemm_fp8(int M, int N, int K, const uint8_t *A8, const float *ascale,
+                       const uint8_t *W8, const float *wscale, const float *bias,
+                       int act, float *C);
+
+/* The device row quantiser of the fp8-activation precision on host arrays,
+ * for tests: rows of bf16 bits x (+ lo plane x_lo) as OCP e4m3 codes with
+ * scale = max|row| / 448 per row, the arithmetic of mfh_debug_quantize_fp8.
+ * No counterpart in the reference. */
+int mfh_debug_quantize_rows_e4m3(int rows, int cols, const uint16_t *x,
+                                 const uint16_t *x_lo, uint8_t *codes,
+                                 float *scales);
+
 /* Few-row GEMM (the kernel of the batch-1 encoder layers, reference
  * cpu_network.cpp:822-890 with the LayerNorm of 424-460 applied to its
  * input) on host arrays, for tests.  The activation operand is A [M,K] bf16
@@ -394,11 +419,17 @@ int mfh_debug_panel_gemm(int M, int N, int K, const uint16_t *A,
 int mfh_debug_encoder_layer(mfh_net *net, int batch, int layer, int iterations,
                             const uint16_t *x, const uint16_t *x_lo, float *ms);
 
-/* Copies a named workspace tensor left by the last eval call to host
- * memory: "body" (fp32 [B*64,E], encoder output; with no encoder layers
- * the input-embedding output) or "policy_qk" (bf16 [B*64,2Dp], the hi plane
- * in split precision).  bytes must equal the tensor's size for the last
- * batch. */
+/* Copies a named workspace tensor left by the last eval call (or
+ * mfh_debug_encoder_layer run) to host memory: "body" (fp32 [B*64,E],
+ * encoder output; with no encoder layers the input-embedding output),
+ * "policy_qk" (bf16 [B*64,2Dp]), the last encoder layer's "act" (bf16
+ * [B*64,E], its output), "qkv" (bf16 [B*64,3E]), "ctx" (bf16 [B*64,E],
+ * attention output), "hid" (bf16 [B*64,F], FFN hidden rows) and "pre"
+ * (fp32 [B*64,E], the FFN residual sum before its LayerNorm); bf16 tensors
+ * are the hi plane in split precision.  In the FP8 precision also
+ * "act_e4m3" / "ctx_e4m3" / "hid_e4m3" (u8 codes, the FFN1, out-projection
+ * and FFN2 inputs) with "act_scale" / "ctx_scale" / "hid_scale" (fp32 per
+ * row).  bytes must equal the tensor's size for the last batch. */
 int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out,
                          uint64_t bytes);
 

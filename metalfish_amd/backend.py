@@ -20,7 +20,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libmfhip.so")
 
 MFH_OK = 0
-PRECISION = {"bf16": 0, "bf16x2": 1, "bf16x2_gemm": 2}
+PRECISION = {"bf16": 0, "bf16x2": 1, "bf16x2_gemm": 2, "fp8": 3}
 WEIGHTS = {"bf16": 0, "fp8": 1}
 ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid": 5,
               "selu": 6, "swish": 7, "relu_2": 8}
@@ -36,7 +36,8 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_weights_tensors", "mfh_weights_tensor_dims", "mfh_weights_free",
            "mfh_net_eval_priors", "mfh_net_eval_priors_device",
            "mfh_net_eval_device_moves_left", "mfh_net_eval_device_noalloc",
-           "mfh_debug_encoder_layer", "mfh_debug_skinny_gemm")
+           "mfh_debug_encoder_layer", "mfh_debug_skinny_gemm", "mfh_debug_gemm_fp8",
+           "mfh_debug_quantize_rows_e4m3")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -103,6 +104,8 @@ def lib():
             "mfh_debug_skinny_gemm": ([i, i, i, vp, vp, vp, i, ctypes.c_float, vp, vp, i, vp, vp,
                                        i, i, vp, vp, vp, ctypes.c_float, vp, vp, vp,
                                        ctypes.POINTER(i), vp, vp, vp], i),
+            "mfh_debug_gemm_fp8": ([i, i, i, vp, vp, vp, vp, vp, i, vp], i),
+            "mfh_debug_quantize_rows_e4m3": ([i, i, vp, vp, vp, vp], i),
             "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
             "mfh_debug_quantize_fp8": ([i, i, vp, vp, vp], i),
             "mfh_weights_load": ([ctypes.c_char_p, ctypes.POINTER(vp)], i),
@@ -378,6 +381,34 @@ def quantize_fp8(w):
     _check(lib().mfh_debug_quantize_fp8(rows, cols, _ptr(w), _ptr(codes), _ptr(scale)),
            "mfh_debug_quantize_fp8")
     return codes, scale
+
+
+def gemm_fp8(a_codes, ascale, w_codes, wscale, bias=None, act="none"):
+    """fp8 x fp8 GEMM through mfh_debug_gemm_fp8 (a test hook): fp32
+    act((A8.W8^T) * ascale[m] * wscale[n] + bias)."""
+    a = np.ascontiguousarray(a_codes, dtype=np.uint8)
+    w = np.ascontiguousarray(w_codes, dtype=np.uint8)
+    sa = np.ascontiguousarray(ascale, dtype=np.float32)
+    sw = np.ascontiguousarray(wscale, dtype=np.float32)
+    m, k = a.shape
+    n = w.shape[0]
+    out = np.zeros((m, n), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(lib().mfh_debug_gemm_fp8(m, n, k, _ptr(a), _ptr(sa), _ptr(w), _ptr(sw), _ptr(b),
+                                    ACTIVATION[act], _ptr(out)), "mfh_debug_gemm_fp8")
+    return out
+
+
+def quantize_rows_e4m3(x_bits, x_lo_bits=None):
+    """The device row quantiser (a test hook): (codes uint8, scales fp32)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    lo = None if x_lo_bits is None else np.ascontiguousarray(x_lo_bits, dtype=np.uint16)
+    rows, cols = x.shape
+    codes = np.zeros((rows, cols), np.uint8)
+    scales = np.zeros(rows, np.float32)
+    _check(lib().mfh_debug_quantize_rows_e4m3(rows, cols, _ptr(x), _ptr(lo), _ptr(codes),
+                                              _ptr(scales)), "mfh_debug_quantize_rows_e4m3")
+    return codes, scales
 
 
 def gemm_bf16(a_bits, w_bits, bias=None, act="none"):

@@ -286,7 +286,7 @@ __device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col,
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8>
+          bool W8, bool F8 = false>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -298,6 +298,11 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int STAGE = (A_ROWS + W_ROWS) * BK;    // bf16 elements per stage
   constexpr int LOADS = (A_ROWS + W_ROWS) * BK * 2 / 1024;
   static_assert(!W8 || ST == 2, "fp8 weights use the two-stage loop");
+  // F8: both operands are e4m3 bytes staged like bf16 rows of BK = 64
+  // (128-byte rows): one v_mfma_f32_16x16x128_f8f6f4 per fragment pair and
+  // K step.  The launcher passes the byte operands with K and the leading
+  // dimensions halved.
+  static_assert(!F8 || (BK == 64 && !SPLIT && !W8), "fp8 activations: BK = 64 bytes pairs");
   static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
   static_assert(LOADS % NWAVES == 0, "stage loads must split evenly over waves");
   constexpr int LPW = LOADS / NWAVES;
@@ -426,6 +431,33 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
                 *reinterpret_cast<const u32x2 *>(wsrc[j] + (kt + 1) * BK + kk * 32);
       }
     }
+    if constexpr (F8) {
+      // Lane (r, c) of a fragment holds bytes 32 c .. 32 c + 31 of row r's
+      // 128-byte K step: 16-byte chunks 2 c and 2 c + 1.
+      i32x8 af[TM], bw[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * WTN + j * 16 + fr;
+        const u32x4 c0 = *reinterpret_cast<const u32x4 *>(sw + Swz<BK>(row, 2 * fc));
+        const u32x4 c1 = *reinterpret_cast<const u32x4 *>(sw + Swz<BK>(row, 2 * fc + 1));
+        bw[j] = i32x8{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
+                      (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WTM + i * 16 + fr;
+        const u32x4 c0 = *reinterpret_cast<const u32x4 *>(sa + Swz<BK>(row, 2 * fc));
+        const u32x4 c1 = *reinterpret_cast<const u32x4 *>(sa + Swz<BK>(row, 2 * fc + 1));
+        af[i] = i32x8{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
+                      (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bw[j], af[i], acc[i][j], 0,
+                                                                      0, 0, 0, 0, 0);
+    } else {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       bf16x8 af[TM], bw[TN];
@@ -459,6 +491,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
                 __builtin_amdgcn_mfma_f32_16x16x32_bf16(bw[j], af[i], acc[i][j], 0, 0, 0);
       }
     }
+    }  // F8 / bf16 fragments
     if constexpr (W8) {
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
@@ -468,6 +501,18 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     }
   }
 
+  // fp8 activations: each row's quantisation scale (the weight row scale
+  // follows in the epilogue).
+  if (p.ascale) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm * WTM + i * 16 + (lane & 15);
+      const float rs = p.ascale[row < p.M ? row : p.M - 1];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] *= rs;
+    }
+  }
   // Transposed accumulator layout: lane holds output row m_base + lane % 16
   // of its tile, columns n_base + 4 * (lane / 16) + r, r = 0..3.
   const int row_base = m0 + wm * WTM + (lane & 15);
@@ -644,11 +689,11 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8 = false>
+          bool W8 = false, bool F8 = false>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   constexpr int A_ROWS = SPLIT ? 2 * BM : BM;
   constexpr size_t kLds = static_cast<size_t>(ST) * (A_ROWS + (W8 ? 0 : BN)) * BK * 2;
-  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8>;
+  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&]() {
@@ -687,21 +732,21 @@ hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_
 
 // Epilogue dispatch: the activations the network uses (none, mish) get
 // dedicated instances, anything else the runtime switch.
-template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8, bool F8 = false>
 hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
   if (p.k_splits > 1 || (p.out_mode == GEMM_OUT_F32 && p.act == ACT_NONE))
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8, F8>(p, stream);
   if (p.out_mode == GEMM_OUT_RESID_F32)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8, F8>(p, stream);
   if (p.out_mode == GEMM_OUT_F32)
     return p.act == ACT_MISH
-               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8>(p, stream)
-               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8>(p, stream);
+               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8, F8>(p, stream)
+               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8, F8>(p, stream);
   if (p.act == ACT_NONE)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8, F8>(p, stream);
   if (p.act == ACT_MISH)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8>(p, stream);
-  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8, F8>(p, stream);
+  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8, F8>(p, stream);
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
@@ -739,6 +784,24 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     return hipErrorInvalidValue;
   };
   GemmParams p = p_in;
+  const bool f8 = p.A8 != nullptr;
+  if (f8) {
+    // fp8 activations x fp8 weights: the byte operands go through the bf16
+    // data path as 16-bit units (K and leading dimensions halved); the F8
+    // kernels run one fp8 MFMA per 128-byte K step.
+    if (p.A || p.A_lo || !p.W8 || p.W || !p.wscale || !p.ascale || p.k_splits != 1 ||
+        p.K % 128 || p.lda % 16 || p.ldw % 16 || p.lda < p.K || p.ldw < p.K ||
+        !Aligned(p.A8, 16) || !Aligned(p.W8, 16) || p.M < 2048)
+      return fail("fp8 activations need A8 + ascale with W8 + wscale, K % 128 == 0, "
+                  "lda / ldw % 16 == 0, 16-byte aligned operands and M >= 2048");
+    p.A = reinterpret_cast<const std::uint16_t *>(p.A8);
+    p.lda /= 2;
+    p.W = reinterpret_cast<const std::uint16_t *>(p.W8);
+    p.W8 = nullptr;
+    p.ldw /= 2;
+    p.K /= 2;
+    p.partials = nullptr;
+  }
   if (p.M <= 0 || p.N <= 0 || p.K <= 0)
     return fail("non-positive shape");
   if (p.K % 32)
@@ -837,6 +900,9 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   // a partial last round) and FFN1 (384).  bf16 weights only (the fp8 path
   // keeps two stages).
   const long big_tiles = static_cast<long>((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (f8)
+    return big_tiles % 256 == 0 ? LaunchW<256, 256, 64, 2, 4, 2, false, false, true>(p, stream)
+                                : LaunchW<128, 128, 64, 2, 2, 4, false, false, true>(p, stream);
   if (large && !p.W8 && p.k_splits == 1 && big_tiles % 256 == 0)
     return split ? LaunchW<256, 256, 32, 3, 4, 2, true, false>(p, stream)
                  : LaunchW<256, 256, 32, 4, 4, 2, false, false>(p, stream);

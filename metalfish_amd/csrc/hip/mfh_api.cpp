@@ -197,6 +197,7 @@ struct Dims {
   bool fused_ln = false;    // residual GEMM + LayerNorm as one row-panel launch
   bool fused_bias = false;  // smolgen bias generated inside the attention kernel
   bool skinny = true;       // few-row GEMMs for single-position forwards
+  bool fp8_act = false;     // e4m3 activations on the fp8 MFMA (FP8 precision)
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -411,9 +412,12 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   if (desc.weights_dtype != MFH_WEIGHTS_BF16 && desc.weights_dtype != MFH_WEIGHTS_FP8)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
   if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2 &&
-      desc.precision != MFH_PRECISION_BF16X2_GEMM)
+      desc.precision != MFH_PRECISION_BF16X2_GEMM && desc.precision != MFH_PRECISION_FP8)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported precision mode");
-  d.split = desc.precision != MFH_PRECISION_BF16;
+  if (desc.precision == MFH_PRECISION_FP8 && desc.weights_dtype != MFH_WEIGHTS_FP8)
+    return SetError(MFH_ERR_UNSUPPORTED, "the FP8 precision needs FP8 (e4m3) weights");
+  d.fp8_act = desc.precision == MFH_PRECISION_FP8;
+  d.split = desc.precision == MFH_PRECISION_BF16X2 || desc.precision == MFH_PRECISION_BF16X2_GEMM;
   d.split_attn = desc.precision == MFH_PRECISION_BF16X2;
   // Measured at the BT4 shape: the panel wins with e4m3 weights (half the
   // weight bytes to stream), the tiled GEMM + LayerNorm kernel with bf16.
@@ -794,6 +798,15 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   add16("mov_emb", M * (d.Md ? d.Md : 1));
   add("mov1", (d.mlh ? SplitK(kSquares * d.Md) : 1) * B * (d.Mh ? d.Mh : 1) * 4);
   add("mlh", B * 4);
+  // e4m3 copies of the body GEMM inputs with their row scales (FP8).
+  if (d.fp8_act) {
+    add("act8", M * d.E);
+    add("sc_act", M * 4);
+    add("ctx8", M * d.E);
+    add("sc_ctx", M * 4);
+    add("hid8", M * (hid ? hid : 1));
+    add("sc_hid", M * 4);
+  }
   // Row statistics of the single-position smolgen chain's deferred
   // LayerNorms (partial sums per workgroup): dense1 and dense2 outputs.
   add("lnst_s1", std::max<size_t>(256, 8 * size_t(mfh::SkinnyGemmParts(d.Hs ? d.Hs : 4))));
@@ -931,6 +944,12 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     if (e_ != hipSuccess)                                                      \
       return fail(e_);                                                         \
   } while (0)
+#define MFH_RC(expr)                                                           \
+  do {                                                                         \
+    const int rc_ = (expr);                                                    \
+    if (rc_ != MFH_OK)                                                         \
+      return rc_;                                                              \
+  } while (0)
   // GEMM with A from workspace tensor `a` (its residual plane when split).
   auto gemm = [&](const std::string &a, int lda, const size_t (&w)[2], int ldw, int m, int n,
                   int k, const float *bias, int act, int mode, void *C, void *C_lo, int ldc) {
@@ -1040,10 +1059,27 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       MFH_RUN(run_ln(lp));
     }
   }
+  // FP8 precision: rows of workspace tensor `a` -> e4m3 codes "<a>8" and
+  // their scales "sc_<a>", and a GEMM switched onto them.
+  auto quant = [&](const std::string &a, int cols) -> int {
+    StageTimer t(net, st, "quantize_e4m3", 0.0, 2.0 * M * cols + 1.0 * M * cols + 4.0 * M);
+    MFH_RUN(mfh::LaunchQuantizeRowsE4m3(ws.S<std::uint16_t>(a), ws.Lo(a), cols, M, cols,
+                                        ws.S<std::uint8_t>(a + "8"), cols,
+                                        ws.S<float>("sc_" + a), st, &err_));
+    return MFH_OK;
+  };
+  auto use_fp8 = [&](mfh::GemmParams &p, const std::string &a) {
+    p.A8 = ws.S<std::uint8_t>(a + "8");
+    p.ascale = ws.S<float>("sc_" + a);
+    p.A = nullptr;
+    p.A_lo = nullptr;
+  };
   auto residual_gemm = [&](const std::string &a, int k, const size_t (&w_off)[2],
-                           const float *bias, const char *role, float alpha) {
+                           const float *bias, const char *role, float alpha, bool f8 = false) {
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
+    if (f8)
+      use_fp8(p, a);
     if (d.split) {
       p.resid16 = ws.S<std::uint16_t>("act");
       p.resid16_lo = ws.Lo("act");
@@ -1062,7 +1098,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // pre-LayerNorm rows to `pre` for the LayerNorm kernel.
   auto residual_ln = [&](const std::string &a, int k, const size_t (&w_off)[2],
                          const float *bias, const char *role, float alpha, float eps,
-                         const float *g, const float *b, float *y32) -> int {
+                         const float *g, const float *b, float *y32, bool f8 = false) -> int {
     // fused_layernorm (default with fp8 weights).  The panel streams each
     // weight row from L2 for only 64 activation rows, which needs every
     // weight fragment to feed two MFMAs (split activations); with bf16
@@ -1110,8 +1146,10 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     }
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
-    const int splits = mfh::GemmAutoSplits(p);
-    if (splits > 1) {
+    const int splits = f8 ? 1 : mfh::GemmAutoSplits(p);
+    if (f8) {
+      MFH_RC(quant(a, k));
+    } else if (splits > 1) {
       // Few positions: the K slices' raw partials go straight to the
       // LayerNorm kernel, which sums them in slice order with the bias and
       // the residual (no separate reduce launch).
@@ -1135,7 +1173,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       MFH_RUN(run_ln(lp));
       return MFH_OK;
     }
-    MFH_RUN(residual_gemm(a, k, w_off, bias, role, alpha));
+    MFH_RUN(residual_gemm(a, k, w_off, bias, role, alpha, f8));
     MFH_RUN(run_ln(ln(pre, M, E, eps, g, b, y32, "act")));
     return MFH_OK;
   };
@@ -1243,6 +1281,9 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // stream so each launch is timed alone.
     const int li = layer_index++;
     const bool big = M >= 2048;
+    // FP8 precision from 2048 rows: Q|K|V, out-projection and FFN GEMMs on
+    // per-row e4m3 copies of their inputs (the smolgen chain stays bf16).
+    const bool f8 = d.fp8_act && big;
     hipStream_t sg_stream = big && !net->profiling ? net->side : st;
     mfh::AttentionParams ap;
     ap.qkv = ws.S<std::uint16_t>("qkv");
@@ -1340,6 +1381,10 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       pq.C2_lo = ws.Lo("comp");
       pq.ldc2 = d.C;
     }
+    if (f8) {
+      MFH_RC(quant("act", E));
+      use_fp8(pq, "act");
+    }
     MFH_RUN(run(pq, "qkv"));
     if (L.smolgen && !big) {
       const int rc = smolgen_chain(st);
@@ -1392,14 +1437,20 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
     }
     int rc = residual_ln("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha, eps_attn,
-                         net->W<float>(L.ln1_g), net->W<float>(L.ln1_b), res32);
+                         net->W<float>(L.ln1_g), net->W<float>(L.ln1_b), res32, f8);
     if (rc != MFH_OK)
       return rc;
-    MFH_RUN(run(gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b), d.act_ffn,
-                     mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("hid"), ws.Lo("hid"), ffn),
-                "ffn1"));
+    mfh::GemmParams pf = gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b),
+                              d.act_ffn, mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("hid"),
+                              ws.Lo("hid"), ffn);
+    if (f8) {
+      MFH_RC(quant("act", E));
+      use_fp8(pf, "act");
+    }
+    MFH_RUN(run(pf, "ffn1"));
     rc = residual_ln("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, eps_ffn,
-                     net->W<float>(L.ln2_g), net->W<float>(L.ln2_b), body_out ? resid : res32);
+                     net->W<float>(L.ln2_g), net->W<float>(L.ln2_b), body_out ? resid : res32,
+                     f8);
     return rc;
   };
   if (!full) {
@@ -1488,6 +1539,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
                                  &err_));
   }
 #undef MFH_RUN
+#undef MFH_RC
   return MFH_OK;
 }
 
@@ -2105,7 +2157,8 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
     o << ", moves left " << d.Md << "/" << d.Mh;
   o << ", activations " << ActName(d.act_default) << "/"
     << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", precision "
-    << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : "bf16") << ", weights "
+    << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : d.fp8_act ? "fp8" : "bf16")
+    << ", weights "
     << (net->fp8 ? "e4m3 " : "bf16 ") << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
     << net->max_batch << ", no-allocation batch <= " << net->noalloc_max_batch;
   const std::string s = o.str();
@@ -2143,6 +2196,24 @@ int mfh_net_debug_tensor(mfh_net *net, const char *name, void *out, uint64_t byt
   } else if (n == "policy_qk") {
     ws_name = "polqk";
     size = B * kSquares * 2 * d.Dp * 2;
+  } else if (n == "act" || n == "ctx") {
+    ws_name = n == "act" ? "act" : "ctx";
+    size = B * kSquares * d.E * 2;
+  } else if (n == "qkv") {
+    ws_name = "qkv";
+    size = B * kSquares * 3 * d.E * 2;
+  } else if (n == "hid") {
+    ws_name = "hid";
+    size = B * kSquares * d.F * 2;
+  } else if (n == "pre") {
+    ws_name = "pre";
+    size = B * kSquares * d.E * 4;
+  } else if (d.fp8_act && (n == "act_e4m3" || n == "ctx_e4m3" || n == "hid_e4m3")) {
+    ws_name = n == "act_e4m3" ? "act8" : n == "ctx_e4m3" ? "ctx8" : "hid8";
+    size = B * kSquares * (n == "hid_e4m3" ? d.F : d.E);
+  } else if (d.fp8_act && (n == "act_scale" || n == "ctx_scale" || n == "hid_scale")) {
+    ws_name = n == "act_scale" ? "sc_act" : n == "ctx_scale" ? "sc_ctx" : "sc_hid";
+    size = B * kSquares * 4;
   } else {
     return SetError(MFH_ERR_INVALID, "unknown debug tensor " + n);
   }
@@ -2199,6 +2270,8 @@ int mfh_debug_encoder_layer(mfh_net *net, int batch, int layer, int iterations,
     rc = SetError(MFH_ERR_HIP, "mfh_debug_encoder_layer: timing failed");
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(z);
+  if (rc == MFH_OK)
+    net->last_batch = batch;
   return rc;
 }
 
@@ -2469,6 +2542,75 @@ struct DebugBuffers {
     return static_cast<T *>(d);
   }
 };
+
+int mfh_debug_gemm_fp8(int M, int N, int K, const uint8_t *A8, const float *ascale,
+                       const uint8_t *W8, const float *wscale, const float *bias, int act,
+                       float *C) {
+  if (M <= 0 || N <= 0 || K <= 0 || !A8 || !ascale || !W8 || !wscale || !C)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_gemm_fp8: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  const size_t na = static_cast<size_t>(M) * K, nw = static_cast<size_t>(N) * K,
+               nc = static_cast<size_t>(M) * N;
+  try {
+    DebugBuffers buf;
+    mfh::GemmParams p;
+    p.A8 = buf.Put(A8, na);
+    p.ascale = buf.Put(ascale, M);
+    p.lda = K;
+    p.W8 = buf.Put(W8, nw);
+    p.wscale = buf.Put(wscale, N);
+    p.ldw = K;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.bias = buf.Put(bias, N);
+    p.act = ActFromProto(act, mfh::ACT_RELU);
+    if (act == MFH_ACTIVATION_NONE || act == MFH_ACTIVATION_DEFAULT)
+      p.act = mfh::ACT_NONE;
+    p.out_mode = mfh::GEMM_OUT_F32;
+    p.C = buf.Put<float>(nullptr, nc, false);
+    p.ldc = N;
+    std::string err;
+    if (mfh::LaunchGemm(p, nullptr, &err) != hipSuccess)
+      return SetError(MFH_ERR_INVALID, err);
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(C, p.C, nc * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      return SetError(MFH_ERR_HIP, "fp8 gemm execution failed");
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_HIP, e.what());
+  }
+  return MFH_OK;
+}
+
+int mfh_debug_quantize_rows_e4m3(int rows, int cols, const uint16_t *x, const uint16_t *x_lo,
+                                 uint8_t *codes, float *scales) {
+  if (rows <= 0 || cols <= 0 || !x || !codes || !scales)
+    return SetError(MFH_ERR_INVALID, "mfh_debug_quantize_rows_e4m3: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  const size_t n = static_cast<size_t>(rows) * cols;
+  try {
+    DebugBuffers buf;
+    const std::uint16_t *dx = buf.Put(x, n);
+    const std::uint16_t *dl = buf.Put(x_lo, n);
+    std::uint8_t *dq = buf.Put<std::uint8_t>(nullptr, n, false);
+    float *ds = buf.Put<float>(nullptr, rows, false);
+    std::string err;
+    if (mfh::LaunchQuantizeRowsE4m3(dx, dl, cols, rows, cols, dq, cols, ds, nullptr, &err) !=
+        hipSuccess)
+      return SetError(MFH_ERR_INVALID, err);
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(codes, dq, n, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(scales, ds, static_cast<size_t>(rows) * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      return SetError(MFH_ERR_HIP, "row quantisation failed");
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_HIP, e.what());
+  }
+  return MFH_OK;
+}
 
 int mfh_debug_skinny_gemm(int M, int N, int K, const uint16_t *A, const uint16_t *A_lo,
                           const float *x, int rows_per_src, float eps, const float *gamma,

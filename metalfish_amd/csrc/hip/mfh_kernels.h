@@ -74,6 +74,12 @@ struct GemmParams {
   // K for small problems (partials summed by a second kernel).
   float *partials = nullptr;
   size_t partials_floats = 0;
+  // fp8 activations: A8 holds e4m3 codes [M][lda] of the rows A / ascale[m]
+  // (the weights then are W8 with their row scales); the product runs on the
+  // fp8 MFMA and output row m is scaled by ascale[m] * wscale[n].  K % 128
+  // == 0, lda % 16 == 0, M >= 2048 rows.
+  const std::uint8_t *A8 = nullptr;
+  const float *ascale = nullptr;
   // Set by LaunchGemm: every output row start allows 4-column vector stores
   // (vec), and 8-column groups allow 16-byte accesses everywhere (vec8).
   bool vec = false;
@@ -208,6 +214,14 @@ struct SkinnyParams {
 int SkinnyGemmParts(int N);
 bool SkinnyShapeOk(int M, int N, int K);
 hipError_t LaunchSkinnyGemm(const SkinnyParams &p, hipStream_t stream, std::string *err);
+
+// Rows of bf16 activations (x, plus the lo plane x_lo when given; stride
+// ldx) as OCP e4m3 codes q (stride ldq) with one fp32 scale per row:
+// scale = max|row| / 448 (1 for a zero row), q = e4m3(x / scale) rounded to
+// nearest even.  16 <= cols <= 2048, cols % 16 == 0, 16-byte aligned rows.
+hipError_t LaunchQuantizeRowsE4m3(const std::uint16_t *x, const std::uint16_t *x_lo, int ldx,
+                                  int rows, int cols, std::uint8_t *q, int ldq, float *scale,
+                                  hipStream_t stream, std::string *err);
 
 // Packed planes -> embedding input rows and the dynamic-PE input.
 //   emb_in [B*64, emb_ld] bf16: cols 0..111 plane values; with static_pe

@@ -250,6 +250,68 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
   }
 }
 
+// Rows of bf16 activations (hi, plus the lo plane when given) as OCP e4m3
+// codes with one fp32 scale per row: scale = max|row| / 448 (1 for a zero
+// row), code = e4m3(x / scale) rounded to nearest even, the quotient
+// clamped to +-448 first (the host weight quantiser's arithmetic).  One wave
+// per row; lane l holds columns 16 (l + 64 g) .. + 15 for g < 2.
+__global__ __launch_bounds__(256) void QuantizeRowsE4m3Kernel(
+    const std::uint16_t *__restrict__ x, const std::uint16_t *__restrict__ x_lo, int ldx,
+    int rows, int cols, std::uint8_t *__restrict__ q, int ldq, float *__restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows)
+    return;
+  float v[2][16];
+  float mx = 0.f;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int c = 16 * (lane + 64 * g);
+    if (c < cols) {
+      const size_t off = static_cast<size_t>(row) * ldx + c;
+      const u32x4 h0 = *reinterpret_cast<const u32x4 *>(x + off);
+      const u32x4 h1 = *reinterpret_cast<const u32x4 *>(x + off + 8);
+      u32x4 l0 = u32x4{0u, 0u, 0u, 0u}, l1 = l0;
+      if (x_lo) {
+        l0 = *reinterpret_cast<const u32x4 *>(x_lo + off);
+        l1 = *reinterpret_cast<const u32x4 *>(x_lo + off + 8);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const unsigned hw = (e < 4 ? h0 : h1)[(e & 3)], lw = (e < 4 ? l0 : l1)[(e & 3)];
+        v[g][2 * e] = __uint_as_float(hw << 16) + __uint_as_float(lw << 16);
+        v[g][2 * e + 1] = __uint_as_float(hw & 0xFFFF0000u) + __uint_as_float(lw & 0xFFFF0000u);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        mx = fmaxf(mx, fabsf(v[g][e]));
+    }
+  }
+  mx = wave_max(mx);
+  const float s = mx > 0.f ? mx / 448.0f : 1.0f;
+  if (lane == 0)
+    scale[row] = s;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int c = 16 * (lane + 64 * g);
+    if (c < cols) {
+      unsigned w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          t[e] = fminf(fmaxf(v[g][4 * k + e] / s, -448.0f), 448.0f);
+        int packed = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0, false);
+        packed = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], packed, true);
+        w[k] = static_cast<unsigned>(packed);
+      }
+      *reinterpret_cast<u32x4 *>(q + static_cast<size_t>(row) * ldq + c) =
+          u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
 // One wave per position: dense2 (vh -> 3 or 1) then softmax or tanh
 // (reference network_execution_plan.cpp:1098-1106, cpu_network.cpp:336-351).
 __global__ __launch_bounds__(256) void ValueHeadKernel(
@@ -424,6 +486,22 @@ hipError_t LaunchValueHead(const float *hidden, int parts, const float *b1, int 
   }
   hipLaunchKernelGGL(ValueHeadKernel, dim3((batch + 3) / 4), dim3(256), 0, stream, hidden,
                      parts, b1, act, batch, vh, w2, b2, mode, out);
+  return hipGetLastError();
+}
+
+hipError_t LaunchQuantizeRowsE4m3(const std::uint16_t *x, const std::uint16_t *x_lo, int ldx,
+                                  int rows, int cols, std::uint8_t *q, int ldq, float *scale,
+                                  hipStream_t stream, std::string *err) {
+  if (!x || !q || !scale || rows < 1 || cols < 16 || cols % 16 || cols > 2048 || ldx < cols ||
+      ldx % 8 || ldq < cols || ldq % 16 || (reinterpret_cast<std::uintptr_t>(x) & 15) ||
+      (x_lo && (reinterpret_cast<std::uintptr_t>(x_lo) & 15)) ||
+      (reinterpret_cast<std::uintptr_t>(q) & 15)) {
+    if (err)
+      *err = "quantize rows: 16 <= cols <= 2048, cols % 16 == 0, 16-byte aligned rows";
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(QuantizeRowsE4m3Kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, x, x_lo,
+                     ldx, rows, cols, q, ldq, scale);
   return hipGetLastError();
 }
 

@@ -65,7 +65,7 @@ def test_row_quantisation_library_matches_numpy():
     assert np.allclose(deq3, deq, rtol=2 ** -22, atol=0)
 
 
-def _fp8_parity(spec_name, n, seed=0, batch=None):
+def _fp8_parity(spec_name, n, seed=0, batch=None, precision="bf16x2"):
     """Parity of an fp8 net on n positions against the oracle; with `batch`,
     the positions fill a batch of that size cyclically (large batches take
     the row-panel GEMMs) and every copy is compared."""
@@ -77,7 +77,8 @@ def _fp8_parity(spec_name, n, seed=0, batch=None):
     ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads), weights).evaluate_batch(planes)
     batch = batch or n
     idx = np.arange(batch) % n
-    net = backend.create_network(spec, weights, max_batch=batch, device=0, weights_dtype="fp8")
+    net = backend.create_network(spec, weights, max_batch=batch, device=0, weights_dtype="fp8",
+                                 precision=precision)
     gpu = net.evaluate_batch(planes[idx])
     net.close()
     planes, legal = planes[idx], legal[idx]
@@ -88,7 +89,7 @@ def _fp8_parity(spec_name, n, seed=0, batch=None):
     agree = np.mean([legal[i][legal[i] >= 0][np.argmax(gpu["policy"][i, legal[i][legal[i] >= 0]])] ==
                      legal[i][legal[i] >= 0][np.argmax(ref["policy"][i, legal[i][legal[i] >= 0]])]
                      for i in range(n)])
-    print(f"fp8 {spec_name} x{n}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {agree:.3f}")
+    print(f"fp8 {precision} {spec_name} x{n}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {agree:.3f}")
     return perr, werr, agree
 
 
@@ -103,3 +104,128 @@ def test_fp8_weight_parity(spec_name, n, batch):
         pytest.fail("GPU tests need an MI355X; none visible")
     perr, werr, agree = _fp8_parity(spec_name, n, batch=batch)
     assert perr <= 1e-3 and werr <= 1e-4 and agree == 1.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,batch", [(40, None), (40, 128), (8, None)])
+def test_fp8_activation_parity(n, batch):
+    """The FP8 precision (e4m3 activations into the body's Q|K|V, out-
+    projection and FFN GEMMs from 2048 token rows) against the oracle on the
+    same dequantised weights.
+
+    It does not meet the parity gates (top-1 >= 99.5 %, policy max-abs
+    <= 2e-2, WDL <= 5e-3): on the random-init BT4 net it measured top-1
+    0.825 / 0.789, policy max-abs 0.15 / 0.18 and WDL max-abs 1.6e-2 /
+    1.1e-2 at 40 positions / a batch of 128, while each fp8 GEMM matches
+    fp64 of its codes (test_fp8_precision_layer_integration): the loss is
+    the 3-bit mantissa of the activations compounding over 15 layers.  The
+    bounds below only catch regressions.  8 positions (512 rows) stay on the
+    bf16 GEMMs and keep the gates."""
+    if backend.device_count() < 1:
+        pytest.fail("GPU tests need an MI355X; none visible")
+    perr, werr, agree = _fp8_parity("bt4", n, batch=batch, precision="fp8")
+    if n * 64 < 2048 and (batch or n) * 64 < 2048:
+        assert perr <= 2e-2 and werr <= 5e-3 and agree == 1.0
+    else:
+        assert perr <= 0.3 and werr <= 0.04 and agree >= 0.7
+
+
+def test_fp8_precision_needs_fp8_weights():
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=0)
+    with pytest.raises(RuntimeError, match="FP8 precision needs FP8"):
+        backend.create_network(spec, weights, max_batch=4, device=-1, precision="fp8")
+
+
+def _e4m3_decode(codes):
+    v = synth.e4m3_values().astype(np.float64)
+    return v[np.asarray(codes)]
+
+
+def _bits_f64(b):
+    return (np.asarray(b).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _to_bits(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _ln(x, g, b, eps):
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * g + b
+
+
+@pytest.mark.gpu
+def test_fp8_precision_layer_integration():
+    """One BT4 encoder layer in the FP8 precision at 32 positions (2048 token
+    rows), step by step against fp64 on the host: each e4m3 GEMM input is
+    the row quantisation of the tensor it stands for (bit for bit), and each
+    GEMM output is the product of those codes with the layer's weights
+    (Q|K|V, out-projection through the first LayerNorm, FFN1 with Mish,
+    FFN2's residual sum, the second LayerNorm)."""
+    if backend.device_count() < 1:
+        pytest.fail("GPU tests need an MI355X; none visible")
+    spec = synth.SPECS["bt4"]
+    w = synth.make_weights(spec, seed=5, fp8=True)
+    b, e, f = 32, spec.embedding, spec.ffn
+    m = b * 64
+    net = backend.create_network(spec, w, max_batch=b, device=0, weights_dtype="fp8",
+                                 precision="fp8")
+    rng = np.random.default_rng(11)
+    x_bits = _to_bits(rng.standard_normal((m, e)))
+    net.encoder_layer_ms(b, 0, 1, x_bits)
+    get = net.debug_tensor
+    qkv = _bits_f64(get("qkv", (m, 3 * e), np.uint16))
+    ctx_bits = get("ctx", (m, e), np.uint16)
+    hid_bits = get("hid", (m, f), np.uint16)
+    pre = get("pre", (m, e), np.float32).astype(np.float64)
+    body = get("body", (m, e), np.float32).astype(np.float64)
+    act8, act_s = get("act_e4m3", (m, e), np.uint8), get("act_scale", (m,), np.float32)
+    ctx8, ctx_s = get("ctx_e4m3", (m, e), np.uint8), get("ctx_scale", (m,), np.float32)
+    hid8, hid_s = get("hid_e4m3", (m, f), np.uint8), get("hid_scale", (m,), np.float32)
+    net.close()
+
+    p = "body.encoder.0."
+    W = lambda n: w[p + n].astype(np.float64)
+    alpha = float(np.float32(2.0 * spec.layers) ** np.float32(-0.25))
+    eps = 1e-6 if spec.pe_map else 1e-3
+    x = _bits_f64(x_bits)
+
+    def deq(codes, s):
+        return _e4m3_decode(codes) * s.astype(np.float64)[:, None]
+
+    def near_bf16(got, ref):
+        # bf16 rounding of the output (2^-9 relative) plus the fp8 MFMA's
+        # summation error (1e-4 of the largest output).
+        return np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-4 * np.abs(ref).max())
+
+    # Q|K|V from the quantised layer input.
+    xq, xs = backend.quantize_fp8(x.astype(np.float32))
+    wqkv = np.concatenate([W("mha.q_w"), W("mha.k_w"), W("mha.v_w")])
+    bqkv = np.concatenate([W("mha.q_b"), W("mha.k_b"), W("mha.v_b")])
+    ref_qkv = deq(xq, xs) @ wqkv.T + bqkv
+    assert near_bf16(qkv, ref_qkv), np.abs(qkv - ref_qkv).max()
+    # Out-projection input: the attention output, quantised bit for bit.
+    cq, cs = backend.quantize_fp8(_bits_f64(ctx_bits).astype(np.float32))
+    assert np.array_equal(ctx8, cq) and np.array_equal(ctx_s.view(np.uint32), cs.view(np.uint32))
+    resid1 = _ln(x + alpha * (deq(ctx8, ctx_s) @ W("mha.dense_w").T + W("mha.dense_b")),
+                 W("ln1_gammas"), W("ln1_betas"), eps)
+    # FFN1 input: the first LayerNorm's bf16 rows, quantised (a host row
+    # that rounds to other bf16 values than the device's fp32 LayerNorm can
+    # differ in a few codes).
+    aq, _ = backend.quantize_fp8(_bits_f64(_to_bits(resid1)).astype(np.float32))
+    agree = np.mean(act8 == aq)
+    print(f"FFN1 input codes equal to the host's: {agree:.6f}")
+    assert agree >= 0.999
+    lin1 = deq(act8, act_s) @ W("ffn.dense1_w").T + W("ffn.dense1_b")
+    ref_hid = lin1 * np.tanh(np.log1p(np.exp(lin1)))
+    assert near_bf16(_bits_f64(hid_bits), ref_hid), np.abs(_bits_f64(hid_bits) - ref_hid).max()
+    hq, hs = backend.quantize_fp8(_bits_f64(hid_bits).astype(np.float32))
+    assert np.array_equal(hid8, hq) and np.array_equal(hid_s.view(np.uint32), hs.view(np.uint32))
+    ref_pre = resid1 + alpha * (deq(hid8, hid_s) @ W("ffn.dense2_w").T + W("ffn.dense2_b"))
+    perr = np.abs(pre - ref_pre).max()
+    berr = np.abs(body - _ln(pre, W("ln2_gammas"), W("ln2_betas"), eps)).max()
+    print(f"FFN2 residual sum max-abs {perr:.2e}, LayerNorm {berr:.2e}")
+    assert perr <= 1e-4 * np.abs(ref_pre).max() and berr <= 1e-4
