@@ -672,8 +672,7 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
   const float *src = part + static_cast<size_t>(row) * p.N + col;
   f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
   if (p.vec && col + 3 < p.N) {
-    for (int s = 0; s < splits; ++s)
-      a += *reinterpret_cast<const f32x4 *>(src + s * plane);
+    a = sum_parts4(src, plane, splits);
   } else {
     for (int s = 0; s < splits; ++s)
 #pragma unroll

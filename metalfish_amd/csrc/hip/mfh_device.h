@@ -88,6 +88,45 @@ __device__ __forceinline__ bf16x8 Fp8x8ToBf16(u32x2 q) {
 // direct global->LDS load builtin takes.
 #define MFH_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))
 
+// Sum of the split-K partials x[0], x[stride], ..., x[(parts - 1) * stride]
+// added in that order (a fixed order, whatever the launch shape), with the
+// loads of each run of B parts issued together: partials written by
+// workgroups on other XCDs come from HBM, and one dependent load per part
+// would serialise those misses.
+template <int B = 16>
+__device__ __forceinline__ f32x4 sum_parts4(const float *x, size_t stride, int parts) {
+  f32x4 a = *reinterpret_cast<const f32x4 *>(x);
+  for (int k0 = 1; k0 < parts; k0 += B) {
+    f32x4 v[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (k0 + j < parts)
+        v[j] = *reinterpret_cast<const f32x4 *>(x + (k0 + j) * stride);
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (k0 + j < parts)
+        a += v[j];
+  }
+  return a;
+}
+
+template <int B = 16>
+__device__ __forceinline__ float sum_parts1(const float *x, size_t stride, int parts) {
+  float a = x[0];
+  for (int k0 = 1; k0 < parts; k0 += B) {
+    float v[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (k0 + j < parts)
+        v[j] = x[(k0 + j) * stride];
+#pragma unroll
+    for (int j = 0; j < B; ++j)
+      if (k0 + j < parts)
+        a += v[j];
+  }
+  return a;
+}
+
 // Wave-wide (64 lanes) reductions.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

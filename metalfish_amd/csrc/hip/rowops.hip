@@ -130,10 +130,9 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
       const int c = c0 + 4 * q;
       f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
       if (active && c0 < width) {
-        x = *reinterpret_cast<const f32x4 *>(lp.x + row_off + c);
-#pragma unroll 4
-        for (int part = 1; part < lp.parts; ++part)
-          x += *reinterpret_cast<const f32x4 *>(lp.x + part * plane + row_off + c);
+        // Rows that sum many parts take 256+ threads (few positions): their
+        // part loads go out 16 at a time; one-wave rows keep the registers.
+        x = sum_parts4<T >= 256 ? 16 : 4>(lp.x + row_off + c, plane, lp.parts);
         if (lp.bias)
           x += *reinterpret_cast<const f32x4 *>(lp.bias + c);
         if (lp.resid) {
@@ -327,9 +326,7 @@ __global__ __launch_bounds__(256) void ValueHeadKernel(
   float acc[3] = {0.f, 0.f, 0.f};
   const size_t plane = static_cast<size_t>(batch) * vh;
   for (int c = lane; c < vh; c += 64) {
-    float v = h[c];
-    for (int part = 1; part < parts; ++part)
-      v += h[part * plane + c];
+    float v = sum_parts1(h + c, plane, parts);
     if (b1)
       v += b1[c];
     v = activate(v, act);
