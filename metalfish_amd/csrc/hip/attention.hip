@@ -3,7 +3,9 @@
 // restating reference src/nn/cpu/cpu_network.cpp:1175-1254.
 //
 // One wave owns one (position, head); a workgroup holds 4 heads of one
-// position.  The wave computes the transposed scores S^T = K Q^T with
+// position and 4, 2 or 1 of its 4 query tiles (each tile's softmax is its
+// own, so the split changes no result; at small batches it spreads the work
+// over more workgroups and shortens each wave's chain).  The wave computes the transposed scores S^T = K Q^T with
 // v_mfma_f32_16x16x32_bf16 (the MFMA's K dimension is exactly the head
 // depth), K and Q fragments coming straight from HBM as 16-byte loads.  In
 // that layout a lane holds, for one query, four consecutive keys of every
@@ -68,6 +70,8 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   const int groups = heads / kHeadsPerBlock;
   const int b = blockIdx.x / groups;
   const int h = (blockIdx.x % groups) * kHeadsPerBlock + wave;
+  const int qn = ap.q_tiles;              // query tiles of this workgroup
+  const int q0 = blockIdx.y * qn;         // its first one
   const int E = heads * kDepth;
   const size_t ld = static_cast<size_t>(3) * E;
   const size_t pos = static_cast<size_t>(b) * kSq * ld;
@@ -136,8 +140,8 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   };
   bf16x8 qcur, qlcur;
   float bcur[4][4];
-  load_q(0, qcur, qlcur);
-  load_bias(0, bcur);
+  load_q(q0, qcur, qlcur);
+  load_bias(q0, bcur);
 
   // V^T into LDS, one packed dword (two keys) per depth.  Each wave reads
   // only its own head's V^T.
@@ -163,10 +167,13 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   const size_t out_off =
       static_cast<size_t>(b) * kSq * E + (blockIdx.x % groups) * kHeadsPerBlock * kDepth;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int qi = 0; qi < 4; ++qi) {
+    if (qi >= qn)
+      break;
+    const int q = q0 + qi;
     bf16x8 qnext, qlnext;
     float bnext[4][4];
-    if (q + 1 < 4) {
+    if (qi + 1 < qn) {
       load_q(q + 1, qnext, qlnext);
       load_bias(q + 1, bnext);
     }
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     // 16 dt + 4 g .. + 3 of this wave's head = half of 16-byte chunk
     // 4 wave + 2 dt + g / 2), then one 16-byte store per plane and thread:
     // thread t takes chunk t % 16 of query row t / 16.
-    std::uint16_t(*stage)[16 * kCtxCols] = ctx_lds[q & 1];
+    std::uint16_t(*stage)[16 * kCtxCols] = ctx_lds[qi & 1];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       const int chunk = (4 * wave + 2 * dt + (g >> 1)) ^ fr;
@@ -272,8 +279,8 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
         *reinterpret_cast<u32x2 *>(stage[1] + off) = u32x2{lw[0], lw[1]};
       }
     }
-    // Two staging buffers: the barrier of tile q also orders every read of
-    // tile q - 1's buffer before tile q + 1 overwrites it.
+    // Two staging buffers: the barrier of a tile also orders every read of
+    // the previous tile's buffer before the next tile overwrites it.
     __syncthreads();
     {
       const int row = threadIdx.x >> 4, chunk = threadIdx.x & 15;
@@ -284,7 +291,7 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
         *reinterpret_cast<u32x4 *>((pl ? ap.ctx_lo : ap.ctx) + idx) =
             *reinterpret_cast<const u32x4 *>(stage[pl] + src);
     }
-    if (q + 1 < 4) {
+    if (qi + 1 < qn) {
       qcur = qnext;
       qlcur = qlnext;
 #pragma unroll
@@ -298,8 +305,8 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
 
 template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
 hipError_t Launch(const AttentionParams &ap, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((AttentionKernel<SPLIT, SPLIT_OUT, BIAS_F32>), dim3(grid), dim3(256), 0,
-                     stream, ap);
+  hipLaunchKernelGGL((AttentionKernel<SPLIT, SPLIT_OUT, BIAS_F32>),
+                     dim3(grid, 4 / ap.q_tiles), dim3(256), 0, stream, ap);
   return hipGetLastError();
 }
 
@@ -665,15 +672,25 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::s
              "8-byte aligned bias, and a lo output plane whenever the input has one";
     return hipErrorInvalidValue;
   }
+  if (ap.q_tiles != 0 && ap.q_tiles != 1 && ap.q_tiles != 2 && ap.q_tiles != 4) {
+    if (err)
+      *err = "attention: q_tiles must be 0 (by batch), 1, 2 or 4";
+    return hipErrorInvalidValue;
+  }
   const int grid = ap.batch * (ap.heads / kHeadsPerBlock);
+  AttentionParams a = ap;
+  // By batch: whole heads from 256 workgroups up (one round of the CUs),
+  // below that the query tiles split over up to four workgroups.
+  if (a.q_tiles == 0)
+    a.q_tiles = grid >= 256 ? 4 : grid >= 128 ? 2 : 1;
   if (split)
-    return ap.bias_f32 ? Launch<true, true, true>(ap, grid, stream)
-                       : Launch<true, true, false>(ap, grid, stream);
+    return a.bias_f32 ? Launch<true, true, true>(a, grid, stream)
+                      : Launch<true, true, false>(a, grid, stream);
   if (split_out)
-    return ap.bias_f32 ? Launch<false, true, true>(ap, grid, stream)
-                       : Launch<false, true, false>(ap, grid, stream);
-  return ap.bias_f32 ? Launch<false, false, true>(ap, grid, stream)
-                     : Launch<false, false, false>(ap, grid, stream);
+    return a.bias_f32 ? Launch<false, true, true>(a, grid, stream)
+                      : Launch<false, true, false>(a, grid, stream);
+  return a.bias_f32 ? Launch<false, false, true>(a, grid, stream)
+                    : Launch<false, false, false>(a, grid, stream);
 }
 
 }  // namespace mfh

@@ -750,8 +750,8 @@ hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
 hipError_t Launch(const GemmParams &p, hipStream_t stream) {
-  if (p.W8)
-    return LaunchW<BM, BN, BK, ST, WM, WN, SPLIT, true>(p, stream);
+  if (p.W8)  // fp8 weights: two stages (their fragments bypass LDS)
+    return LaunchW<BM, BN, BK, 2, WM, WN, SPLIT, true>(p, stream);
   return LaunchW<BM, BN, BK, ST, WM, WN, SPLIT, false>(p, stream);
 }
 
@@ -922,9 +922,20 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
                  : Launch<128, 128, 64, 2, 2, 2, false>(p, stream);
   }
-  if (kslice % 64 == 0)
+  // 64 x 64 tiles over the whole K (Q|K|V at 6-31 positions, the
+  // out-projection and FFN at 16-31, the smolgen dense2 and global
+  // projection at some batches): from 256 rows up a three-stage ring keeps
+  // two K steps in flight (batch 16 forward 2.30 -> 2.05 ms, batch 8 1.75
+  // -> 1.68, batch 256 +0.9 %); at 128 rows (smolgen dense2 at batch 128,
+  // beside the Q|K|V GEMM on the other stream) it was 1.7 % slower, and four
+  // stages (one workgroup per CU) were slower at every batch.
+  if (kslice % 64 == 0) {
+    if (p.M >= 256)
+      return split ? Launch<64, 64, 64, 3, 2, 2, true>(p, stream)
+                   : Launch<64, 64, 64, 3, 2, 2, false>(p, stream);
     return split ? Launch<64, 64, 64, 2, 2, 2, true>(p, stream)
                  : Launch<64, 64, 64, 2, 2, 2, false>(p, stream);
+  }
   return split ? Launch<64, 64, 32, 2, 2, 2, true>(p, stream)
                : Launch<64, 64, 32, 2, 2, 2, false>(p, stream);
 }

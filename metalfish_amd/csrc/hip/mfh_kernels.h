@@ -292,6 +292,9 @@ struct AttentionParams {
   int batch = 0, heads = 0;
   std::uint16_t *ctx = nullptr;
   std::uint16_t *ctx_lo = nullptr;
+  // Query tiles (of 4) per workgroup: 4, 2 or 1 (the rest over grid.y), or
+  // 0 to choose by batch (fewer per workgroup when there are few of them).
+  int q_tiles = 0;
 };
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream,
                            std::string *err);
