@@ -130,9 +130,11 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
       const int c = c0 + 4 * q;
       f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
       if (active && c0 < width) {
-        // Rows that sum many parts take 256+ threads (few positions): their
-        // part loads go out 16 at a time; one-wave rows keep the registers.
-        x = sum_parts4<T >= 256 ? 16 : 4>(lp.x + row_off + c, plane, lp.parts);
+        // Part loads go out 16 at a time in the variants that sum split-K
+        // parts (256+ threads per row, or one wave with at most two
+        // 4-element groups per lane), 4 at a time otherwise.
+        x = sum_parts4<(T >= 256 || (G == 4 && NV <= 2)) ? 16 : 4>(lp.x + row_off + c, plane,
+                                                                    lp.parts);
         if (lp.bias)
           x += *reinterpret_cast<const f32x4 *>(lp.bias + c);
         if (lp.resid) {
