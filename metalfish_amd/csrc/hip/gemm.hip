@@ -915,6 +915,22 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   if (large && kslice % 64 == 0) {
     if (split && tiles128 < 256)
       return Launch<64, 64, 64, 2, 2, 2, true>(p, stream);
+    if (kslice <= 1024 && split && !p.W8) {
+      // 256 x 128 tiles (eight 64 x 64 waves, two 40 KiB stages, two
+      // workgroups per CU) read 12 LDS fragments per 32 MFMAs, 128 x 128
+      // tiles 10 per 16; a 256 x 128 tile costs ~1.8 times a 128 x 128
+      // one, so it is taken when its rounds of 256 workgroups cost less and
+      // it fills at least one round.  Below one round (FFN1 at batches 48
+      // and 64, the out-projection at 96) it was 1-5 % slower, except for
+      // Q|K|V at 2048 rows (batch 32), where its 192 tiles leave CUs to the
+      // smolgen chain running beside it, the longer branch there.
+      // Measured forward: batch 32 2.72 -> 2.61 ms, 96 5.32 -> 5.26, 128
+      // 6.72 -> 6.66, 256 11.30 -> 11.16; 48 and 64 unchanged.
+      const long t256 = static_cast<long>((p.M + 255) / 256) * ((p.N + 127) / 128);
+      if ((t256 >= 256 || p.M <= 2048) &&
+          9 * ((t256 + 255) / 256) < 5 * ((tiles128 + 255) / 256))
+        return LaunchW<256, 128, 32, 2, 4, 2, true, false>(p, stream);
+    }
     if (kslice <= 1024)
       return split ? Launch<128, 128, 32, 2, 2, 4, true>(p, stream)
              : p.W8 ? Launch<256, 128, 32, 2, 4, 2, false>(p, stream)
