@@ -7,7 +7,7 @@
  * (mfhip.h) and the CPU oracle.  The reference has no counterpart for the net
  * generator (it loads trained .pb files, reference src/nn/loader.cpp:156-179);
  * the position encoder follows NN::EncodePositionForNN
- * (reference src/nn/encoder.cpp:249-475) for INPUT_CLASSICAL_112_PLANE.
+ * (reference src/nn/encoder.cpp:249-475) for every input format.
  */
 #ifndef MFH_SYNTH_H
 #define MFH_SYNTH_H
@@ -54,6 +54,27 @@ int mfs_playout_batch(uint64_t seed, int first_game, int count, int min_plies,
  * written to legal[] (policy indices, side-to-move frame) or -1 on error. */
 int mfs_encode_game(const char *fen, const char *moves, float *planes,
                     int16_t *legal, int legal_cap);
+
+/* The same for any input format of a network file (net.proto InputFormat:
+ * 1 classical, 2 castling plane, 3 canonical, 4 canonical hectoplies, 132
+ * canonical hectoplies armageddon, 5 canonical v2, 133 canonical v2
+ * armageddon), fill_empty_history 0 NO / 1 FEN_ONLY / 2 ALWAYS, and
+ * history_planes earlier positions at most (8 used).  The legal moves'
+ * policy indices take the transform the encoder chose, written to
+ * *transform_out when given (reference src/mcts/evaluator.cpp:152-160,
+ * 194-200).  planes may be null.  Returns the legal-move count or -1. */
+int mfs_encode_game_format(const char *fen, const char *moves, int input_format,
+                           int fill_empty_history, int history_planes, float *planes,
+                           int16_t *legal, int legal_cap, int *transform_out);
+
+/* Policy index of the move from -> to (side-to-move frame; promo 0 or one
+ * of 'q','r','b','n') under an input transform, or -1 (reference
+ * NN::MoveToNNIndex, src/nn/policy_map.cpp:316-360). */
+int mfs_move_to_index(int from, int to, char promo, int transform);
+
+/* Move of a policy index under an input transform (reference
+ * NN::IndexToNNMove, policy_map.cpp:362-410); -1 for a bad index. */
+int mfs_index_to_move(int index, int transform, int *from, int *to, char *promo);
 
 /* Legal-move tree size of `fen` at `depth`; -1 if the FEN is invalid. */
 int64_t mfs_perft(const char *fen, int depth);

@@ -569,6 +569,50 @@ namespace {
 // Byte-order reversal flips the board vertically (rank r -> 7 - r).
 inline Bitboard ReverseBytes(Bitboard b) { return __builtin_bswap64(b); }
 
+// Bit reversal within each byte flips the board horizontally (file f ->
+// 7 - f).
+inline Bitboard ReverseBitsInBytes(Bitboard v) {
+  v = ((v >> 1) & 0x5555555555555555ULL) | ((v & 0x5555555555555555ULL) << 1);
+  v = ((v >> 2) & 0x3333333333333333ULL) | ((v & 0x3333333333333333ULL) << 2);
+  return ((v >> 4) & 0x0F0F0F0F0F0F0F0FULL) | ((v & 0x0F0F0F0F0F0F0F0FULL) << 4);
+}
+
+// Reflection in the a8-h1 diagonal: square (rank r, file f) -> (rank 7 - f,
+// file 7 - r), as three block swaps of 1, 2 and 4 squares (the reference's
+// TransposeBitsInBytes, encoder.cpp:47-55, does the same).
+inline Bitboard TransposeAntiDiagonal(Bitboard v) {
+  v = ((v & 0xAA00AA00AA00AA00ULL) >> 9) | ((v & 0x0055005500550055ULL) << 9) |
+      (v & 0x55AA55AA55AA55AAULL);
+  v = ((v & 0xCCCC0000CCCC0000ULL) >> 18) | ((v & 0x0000333300003333ULL) << 18) |
+      (v & 0x3333CCCC3333CCCCULL);
+  return ((v & 0xF0F0F0F000000000ULL) >> 36) | ((v & 0x000000000F0F0F0FULL) << 36) |
+         (v & 0x0F0F0F0FF0F0F0F0ULL);
+}
+
+// Flip, then mirror, then transpose (reference encoder.cpp:57-73).
+Bitboard ApplyTransform(Bitboard b, int transform) {
+  if (b == 0 || b == ~0ULL)
+    return b;
+  if (transform & kFlipTransform)
+    b = ReverseBitsInBytes(b);
+  if (transform & kMirrorTransform)
+    b = ReverseBytes(b);
+  if (transform & kTransposeTransform)
+    b = TransposeAntiDiagonal(b);
+  return b;
+}
+
+// -1 / 0 / 1 as `board` (after the flip / mirror of `transform`) is below,
+// equal to or above its transpose (reference encoder.cpp:75-92).
+int CompareTransposing(Bitboard board, int transform) {
+  if (transform & kFlipTransform)
+    board = ReverseBitsInBytes(board);
+  if (transform & kMirrorTransform)
+    board = ReverseBytes(board);
+  const Bitboard alt = TransposeAntiDiagonal(board);
+  return board < alt ? -1 : board > alt ? 1 : 0;
+}
+
 void SetBits(float *plane, Bitboard b) {
   while (b)
     plane[PopLsb(b)] = 1.0f;
@@ -579,30 +623,142 @@ void Fill(float *plane, float v) {
 }
 }  // namespace
 
-void EncodeClassical112(const std::vector<State> &history, float *planes) {
+bool IsCanonicalFormat(int f) {
+  return f == INPUT_112_WITH_CANONICALIZATION || f == INPUT_112_WITH_CANONICALIZATION_HECTOPLIES ||
+         f == INPUT_112_WITH_CANONICALIZATION_HECTOPLIES_ARMAGEDDON ||
+         f == INPUT_112_WITH_CANONICALIZATION_V2 ||
+         f == INPUT_112_WITH_CANONICALIZATION_V2_ARMAGEDDON;
+}
+
+bool IsHectopliesFormat(int f) {
+  return f == INPUT_112_WITH_CANONICALIZATION_HECTOPLIES ||
+         f == INPUT_112_WITH_CANONICALIZATION_HECTOPLIES_ARMAGEDDON ||
+         f == INPUT_112_WITH_CANONICALIZATION_V2 ||
+         f == INPUT_112_WITH_CANONICALIZATION_V2_ARMAGEDDON;
+}
+
+bool IsCanonicalArmageddonFormat(int f) {
+  return f == INPUT_112_WITH_CANONICALIZATION_HECTOPLIES_ARMAGEDDON ||
+         f == INPUT_112_WITH_CANONICALIZATION_V2_ARMAGEDDON;
+}
+
+// No transform while any castling right remains.  Otherwise the side to
+// move's king goes to files e-h (flip); without pawns also to ranks 1-4
+// (mirror) and below the a8-h1 diagonal (transpose), a king on that
+// diagonal breaking the tie by comparing whole-board, own, king, queen,
+// rook, knight and bishop bitboards with their transposes.  The king and
+// the tie-break boards are taken in board coordinates, not flipped for
+// black to move, as the reference takes them.
+int ChooseTransform(const State &s) {
+  if (s.castling != 0)
+    return 0;
+  const int us = s.stm;
+  Bitboard king = s.Pieces(us, KING);
+  int t = 0;
+  if (king & 0x0F0F0F0F0F0F0F0FULL) {
+    t |= kFlipTransform;
+    king = ReverseBitsInBytes(king);
+  }
+  if (s.by_type[PAWN] != 0)
+    return t;
+  if (king & 0xFFFFFFFF00000000ULL) {
+    t |= kMirrorTransform;
+    king = ReverseBytes(king);
+  }
+  if (king & 0xE0C08000ULL)
+    return t | kTransposeTransform;
+  if (king & 0x10204080ULL) {
+    const Bitboard boards[7] = {s.Pieces(), s.by_color[us], s.by_type[KING], s.by_type[QUEEN],
+                                s.by_type[ROOK], s.by_type[KNIGHT], s.by_type[BISHOP]};
+    for (Bitboard b : boards) {
+      const int c = CompareTransposing(b, t);
+      if (c < 0)
+        return t;
+      if (c > 0)
+        return t | kTransposeTransform;
+    }
+  }
+  return t;
+}
+
+int EncodePositionForNN(const std::vector<State> &history, int fmt, int history_planes,
+                        int fill, float *planes) {
   std::memset(planes, 0, sizeof(float) * 112 * 64);
   if (history.empty())
-    return;
+    return 0;
   const State &cur = history.back();
   const int us = cur.stm, them = us ^ 1;
+  const bool canonical = IsCanonicalFormat(fmt);
+  const bool skip_non_repeats = fmt == INPUT_112_WITH_CANONICALIZATION_V2 ||
+                                fmt == INPUT_112_WITH_CANONICALIZATION_V2_ARMAGEDDON;
+  const int transform = canonical ? ChooseTransform(cur) : 0;
+  const int our_oo = us == WHITE ? WHITE_OO : BLACK_OO;
+  const int our_ooo = us == WHITE ? WHITE_OOO : BLACK_OOO;
+  const int their_oo = us == WHITE ? BLACK_OO : WHITE_OO;
+  const int their_ooo = us == WHITE ? BLACK_OOO : WHITE_OOO;
+
+  // Aux planes (reference encoder.cpp:283-339).
   float *aux = planes + 104 * 64;
-  // Aux planes for the classical format (reference encoder.cpp:283-339).
-  Fill(aux + 0 * 64, cur.CanCastle(us == WHITE ? WHITE_OOO : BLACK_OOO) ? 1.f : 0.f);
-  Fill(aux + 1 * 64, cur.CanCastle(us == WHITE ? WHITE_OO : BLACK_OO) ? 1.f : 0.f);
-  Fill(aux + 2 * 64, cur.CanCastle(them == WHITE ? WHITE_OOO : BLACK_OOO) ? 1.f : 0.f);
-  Fill(aux + 3 * 64, cur.CanCastle(them == WHITE ? WHITE_OO : BLACK_OO) ? 1.f : 0.f);
-  Fill(aux + 4 * 64, us == BLACK ? 1.f : 0.f);
-  Fill(aux + 5 * 64, static_cast<float>(cur.rule50));
-  Fill(aux + 6 * 64, 0.f);
+  if (fmt == INPUT_CLASSICAL_112_PLANE) {
+    Fill(aux + 0 * 64, cur.CanCastle(our_ooo) ? 1.f : 0.f);
+    Fill(aux + 1 * 64, cur.CanCastle(our_oo) ? 1.f : 0.f);
+    Fill(aux + 2 * 64, cur.CanCastle(their_ooo) ? 1.f : 0.f);
+    Fill(aux + 3 * 64, cur.CanCastle(their_oo) ? 1.f : 0.f);
+  } else {
+    // The castling rook's square: the side to move's on the first rank of
+    // its frame, the other side's on the last.
+    aux[0 * 64 + 0] = cur.CanCastle(our_ooo) ? 1.f : 0.f;
+    aux[1 * 64 + 7] = cur.CanCastle(our_oo) ? 1.f : 0.f;
+    aux[0 * 64 + 56] = cur.CanCastle(their_ooo) ? 1.f : 0.f;
+    aux[1 * 64 + 63] = cur.CanCastle(their_oo) ? 1.f : 0.f;
+  }
+  if (canonical) {
+    // The en-passant square in board coordinates (not flipped for black).
+    if (cur.ep != SQ_NONE)
+      aux[4 * 64 + cur.ep] = 1.f;
+  } else {
+    Fill(aux + 4 * 64, us == BLACK ? 1.f : 0.f);
+  }
+  Fill(aux + 5 * 64, IsHectopliesFormat(fmt) ? static_cast<float>(cur.rule50) / 100.0f
+                                             : static_cast<float>(cur.rule50));
+  Fill(aux + 6 * 64, IsCanonicalArmageddonFormat(fmt) && us == BLACK ? 1.f : 0.f);
   Fill(aux + 7 * 64, 1.f);
 
+  // Castling rights relative to the side to move (reference encoder.cpp:
+  // 341-367): a history position with other rights cannot repeat.
+  auto rights = [&](const State &p) {
+    return (p.CanCastle(our_oo) ? 1 : 0) | (p.CanCastle(our_ooo) ? 2 : 0) |
+           (p.CanCastle(their_oo) ? 4 : 0) | (p.CanCastle(their_ooo) ? 8 : 0);
+  };
+  const int root_rights = rights(cur);
+  const int planes_wanted = history_planes < 8 ? history_planes : 8;
   const int actual = static_cast<int>(history.size());
-  for (int i = 0, idx = actual - 1; i < 8; ++i, --idx) {
+  for (int i = 0, idx = actual - 1; i < planes_wanted; ++i, --idx) {
     const State &pos = history[idx >= 0 ? idx : 0];
-    // FEN_ONLY fill: repeat the oldest known position unless it is the
-    // standard start position (reference encoder.cpp:378-389).
-    if (idx < 0 && IsStartPosition(pos))
+    // Without fill, one earlier position is inferred only from an en-passant
+    // square (reference encoder.cpp:378-389).
+    if (fill == FILL_NO && (idx < -1 || (idx == -1 && pos.ep == SQ_NONE)))
       break;
+    // FEN_ONLY fill: repeat the oldest known position unless it is the
+    // standard start position.
+    if (idx < 0 && fill == FILL_FEN_ONLY && IsStartPosition(pos))
+      break;
+    if (canonical && idx < actual - 1) {
+      if (rights(pos) != root_rights || pos.ep != SQ_NONE)
+        break;
+    }
+    const bool rep = pos.IsRepetition();
+    // Canonical v2: history planes only for repeated positions, the plane
+    // index kept while non-repeats are skipped (reference encoder.cpp:
+    // 399-404).  Synthesised history (before the first position) repeats
+    // that position, which never is a repetition: the reference would skip
+    // it without end, this stops there.
+    if (skip_non_repeats && i > 0 && !rep) {
+      if (pos.rule50 == 0 || idx < 0)
+        break;
+      --i;
+      continue;
+    }
     Bitboard ours[6], theirs[6];
     for (int pt = 0; pt < 6; ++pt) {
       ours[pt] = pos.Pieces(us, pt);
@@ -617,7 +773,7 @@ void EncodeClassical112(const std::vector<State> &history, float *planes) {
       SetBits(base + pt * 64, ours[pt]);
       SetBits(base + (6 + pt) * 64, theirs[pt]);
     }
-    Fill(base + 12 * 64, pos.IsRepetition() ? 1.f : 0.f);
+    Fill(base + 12 * 64, rep ? 1.f : 0.f);
     // Synthesised-history en-passant adjustment (reference encoder.cpp:
     // 440-451); it only fires for ep squares on the first or last rank.
     if (idx < 0 && pos.ep != SQ_NONE) {
@@ -634,7 +790,30 @@ void EncodeClassical112(const std::vector<State> &history, float *planes) {
         SetBits(base + 6 * 64, theirs[0] + mask);
       }
     }
+    if (canonical && pos.rule50 == 0)
+      break;
   }
+
+  // The transform acts on every 0/1 plane up to the en-passant plane
+  // (reference encoder.cpp:456-469).
+  if (transform != 0) {
+    for (int p = 0; p <= 104 + 4; ++p) {
+      float *plane = planes + p * 64;
+      Bitboard b = 0;
+      for (int sq = 0; sq < 64; ++sq)
+        if (plane[sq] > 0.5f)
+          b |= 1ULL << sq;
+      if (b == 0 || b == ~0ULL)
+        continue;
+      Fill(plane, 0.f);
+      SetBits(plane, ApplyTransform(b, transform));
+    }
+  }
+  return transform;
+}
+
+void EncodeClassical112(const std::vector<State> &history, float *planes) {
+  EncodePositionForNN(history, INPUT_CLASSICAL_112_PLANE, 8, FILL_FEN_ONLY, planes);
 }
 
 }  // namespace mfh_chess

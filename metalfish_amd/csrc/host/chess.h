@@ -82,10 +82,43 @@ private:
 
 std::uint64_t Perft(Game &game, int depth);
 
+// Input formats of a network file (reference src/nn/proto/net.proto:256-263).
+enum InputFormat : int {
+  INPUT_CLASSICAL_112_PLANE = 1,
+  INPUT_112_WITH_CASTLING_PLANE = 2,
+  INPUT_112_WITH_CANONICALIZATION = 3,
+  INPUT_112_WITH_CANONICALIZATION_HECTOPLIES = 4,
+  INPUT_112_WITH_CANONICALIZATION_HECTOPLIES_ARMAGEDDON = 132,
+  INPUT_112_WITH_CANONICALIZATION_V2 = 5,
+  INPUT_112_WITH_CANONICALIZATION_V2_ARMAGEDDON = 133,
+};
+// How missing history is filled (reference src/nn/encoder.h:20).
+enum FillEmptyHistory : int { FILL_NO = 0, FILL_FEN_ONLY = 1, FILL_ALWAYS = 2 };
+
+// Plane transforms of the canonical formats (reference input_planes.h:16-20).
+constexpr int kFlipTransform = 1;
+constexpr int kMirrorTransform = 2;
+constexpr int kTransposeTransform = 4;
+
+bool IsCanonicalFormat(int input_format);
+bool IsHectopliesFormat(int input_format);
+bool IsCanonicalArmageddonFormat(int input_format);
+
+// The transform a canonical format applies to the current position
+// (reference ChooseTransform, src/nn/encoder.cpp:94-157).
+int ChooseTransform(const State &s);
+
+// NN::EncodePositionForNN (reference src/nn/encoder.cpp:249-475): the 112
+// planes of the last position of `history` with up to `history_planes` (8
+// at most) earlier positions, for any of the input formats above.  Returns
+// the transform applied (0 outside the canonical formats).  `planes`
+// receives 112*64 floats.
+int EncodePositionForNN(const std::vector<State> &history, int input_format,
+                        int history_planes, int fill_empty_history, float *planes);
+
 // Classical 112-plane encoding with 8-ply history and FEN_ONLY fill of
-// missing history (reference src/nn/encoder.cpp:249-475 with
-// INPUT_CLASSICAL_112_PLANE, called as in src/mcts/evaluator.cpp:155-157).
-// `planes` receives 112*64 floats.
+// missing history, as the MCTS evaluator calls it for classical nets
+// (reference src/mcts/evaluator.cpp:155-157).
 void EncodeClassical112(const std::vector<State> &history, float *planes);
 
 bool IsStartPosition(const State &s);

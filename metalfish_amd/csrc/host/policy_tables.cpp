@@ -83,9 +83,31 @@ const std::array<float, 64 * kPosEncodingChannels> &StaticPositionEncoding() {
   return table;
 }
 
-int MoveToIndex(int from, int to, char promo) {
+namespace {
+// The square map of the reference's MoveToNNIndex / IndexToNNMove
+// (policy_map.cpp:305-314): the rank is reversed under the mirror or the
+// transpose transform, the file under the flip or the transpose.  For the
+// transpose that is a half turn, not the anti-diagonal reflection the
+// encoder applies to the input planes (encoder.cpp:47-55); it is kept as
+// the reference has it, since the policy indices must equal the
+// reference's.
+int TransformSquare(int sq, int transform) {
+  int file = sq & 7, rank = sq >> 3;
+  if (transform & (kMirrorTransform | kTransposeTransform))
+    rank = 7 - rank;
+  if (transform & (kFlipTransform | kTransposeTransform))
+    file = 7 - file;
+  return rank * 8 + file;
+}
+}  // namespace
+
+int MoveToIndex(int from, int to, char promo, int transform) {
   if (from < 0 || from > 63 || to < 0 || to > 63)
     return -1;
+  if (transform != 0) {
+    from = TransformSquare(from, transform);
+    to = TransformSquare(to, transform);
+  }
   if (promo == 'q' || promo == 'r' || promo == 'b') {
     if ((from >> 3) != 6 || (to >> 3) != 7)
       return -1;
@@ -93,6 +115,31 @@ int MoveToIndex(int from, int to, char promo) {
     return B().promotion[(from & 7) * 24 + (to & 7) * 3 + p];
   }
   return B().regular[from * 64 + to];
+}
+
+// Reference IndexToNNMove (policy_map.cpp:362-410): the inverse of the
+// square map above (a transpose with one of flip / mirror takes the other).
+bool IndexToMove(int index, int transform, int *from, int *to, char *promo) {
+  if (index < 0 || index >= kPolicyOutputs)
+    return false;
+  const PolicyMove &m = MoveList()[index];
+  int f = m.from, t = m.to;
+  if (transform != 0) {
+    int inv = transform;
+    if (transform & kTransposeTransform) {
+      inv = kTransposeTransform;
+      if (transform & kFlipTransform)
+        inv |= kMirrorTransform;
+      if (transform & kMirrorTransform)
+        inv |= kFlipTransform;
+    }
+    t = TransformSquare(t, inv);
+    f = TransformSquare(f, inv);
+  }
+  *from = f;
+  *to = t;
+  *promo = m.promo;
+  return true;
 }
 
 }  // namespace mfh_policy

@@ -41,8 +41,22 @@ const std::array<std::int16_t, kPolicyOutputs> &AttentionGather();
 constexpr int kPosEncodingChannels = 64;
 const std::array<float, 64 * kPosEncodingChannels> &StaticPositionEncoding();
 
-// Index of a move given in the side-to-move-relative frame, or -1.
-// `promo` is 0 for no promotion or one of 'q','r','b','n'.
-int MoveToIndex(int from, int to, char promo);
+// Input-plane transforms of the canonical input formats (reference
+// src/nn/input_planes.h:16-20).
+constexpr int kFlipTransform = 1;       // files a <-> h
+constexpr int kMirrorTransform = 2;     // ranks 1 <-> 8
+constexpr int kTransposeTransform = 4;  // the planes' anti-diagonal reflection
+
+// Index of a move given in the side-to-move-relative frame, or -1
+// (reference MoveToNNIndex, src/nn/policy_map.cpp:316-360).  `promo` is 0
+// for no promotion or one of 'q','r','b','n'; `transform` is the one the
+// encoder chose for the position (its squares are mapped as the reference
+// maps them, see policy_tables.cpp).
+int MoveToIndex(int from, int to, char promo, int transform = 0);
+
+// Move of a policy index under `transform` (reference IndexToNNMove,
+// policy_map.cpp:362-410): from/to squares and promo 0 / 'q' / 'r' / 'b'.
+// False for an index outside 0..1857.
+bool IndexToMove(int index, int transform, int *from, int *to, char *promo);
 
 }  // namespace mfh_policy

@@ -34,7 +34,7 @@ std::uint64_t Fnv1a(const char *s) {
   return h;
 }
 
-void LegalIndices(const mfh_chess::Game &game, int16_t *out, int cap,
+void LegalIndices(const mfh_chess::Game &game, int transform, int16_t *out, int cap,
                   int *count) {
   std::vector<mfh_chess::Move> moves;
   game.LegalMoves(moves);
@@ -50,7 +50,7 @@ void LegalIndices(const mfh_chess::Game &game, int16_t *out, int cap,
     char promo = 0;
     if (m.kind == mfh_chess::MK_PROMOTION)
       promo = "pnbrqk"[m.promo];
-    out[n++] = static_cast<int16_t>(mfh_policy::MoveToIndex(from, to, promo));
+    out[n++] = static_cast<int16_t>(mfh_policy::MoveToIndex(from, to, promo, transform));
   }
   for (int i = n; i < cap; ++i)
     out[i] = -1;
@@ -148,7 +148,7 @@ int mfs_playout_batch(uint64_t seed, int first_game, int count, int min_plies,
                                   planes + static_cast<size_t>(i) * 112 * 64);
     if (legal) {
       int n = 0;
-      LegalIndices(game, legal + static_cast<size_t>(i) * 256, 256, &n);
+      LegalIndices(game, 0, legal + static_cast<size_t>(i) * 256, 256, &n);
     }
     if (text && text_stride > 0) {
       char *dst = text + static_cast<size_t>(i) * text_stride;
@@ -161,6 +161,21 @@ int mfs_playout_batch(uint64_t seed, int first_game, int count, int min_plies,
 
 int mfs_encode_game(const char *fen, const char *moves, float *planes,
                     int16_t *legal, int legal_cap) {
+  return mfs_encode_game_format(fen, moves, mfh_chess::INPUT_CLASSICAL_112_PLANE,
+                                mfh_chess::FILL_FEN_ONLY, 8, planes, legal, legal_cap, nullptr);
+}
+
+int mfs_encode_game_format(const char *fen, const char *moves, int input_format,
+                           int fill_empty_history, int history_planes, float *planes,
+                           int16_t *legal, int legal_cap, int *transform_out) {
+  const int f = input_format;
+  if ((f < mfh_chess::INPUT_CLASSICAL_112_PLANE || f > mfh_chess::INPUT_112_WITH_CANONICALIZATION_V2) &&
+      f != mfh_chess::INPUT_112_WITH_CANONICALIZATION_HECTOPLIES_ARMAGEDDON &&
+      f != mfh_chess::INPUT_112_WITH_CANONICALIZATION_V2_ARMAGEDDON)
+    return -1;
+  if (fill_empty_history < mfh_chess::FILL_NO || fill_empty_history > mfh_chess::FILL_ALWAYS ||
+      history_planes < 1)
+    return -1;
   mfh_chess::Game game;
   if (fen && *fen && !game.SetFen(fen))
     return -1;
@@ -174,12 +189,27 @@ int mfs_encode_game(const char *fen, const char *moves, float *planes,
       game.DoMove(m);
     }
   }
-  if (planes)
-    mfh_chess::EncodeClassical112(game.History(), planes);
+  std::vector<float> scratch;
+  if (!planes) {
+    scratch.resize(112 * 64);
+    planes = scratch.data();
+  }
+  const int transform = mfh_chess::EncodePositionForNN(game.History(), input_format,
+                                                       history_planes, fill_empty_history, planes);
+  if (transform_out)
+    *transform_out = transform;
   int n = 0;
   if (legal && legal_cap > 0)
-    LegalIndices(game, legal, legal_cap, &n);
+    LegalIndices(game, transform, legal, legal_cap, &n);
   return n;
+}
+
+int mfs_move_to_index(int from, int to, char promo, int transform) {
+  return mfh_policy::MoveToIndex(from, to, promo, transform);
+}
+
+int mfs_index_to_move(int index, int transform, int *from, int *to, char *promo) {
+  return mfh_policy::IndexToMove(index, transform, from, to, promo) ? 0 : -1;
 }
 
 int64_t mfs_perft(const char *fen, int depth) {

@@ -41,6 +41,13 @@ def lib():
                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
         _lib.mfs_encode_game.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_void_p,
                                          ctypes.c_void_p, ctypes.c_int]
+        _lib.mfs_encode_game_format.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                                ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        _lib.mfs_move_to_index.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_char,
+                                           ctypes.c_int]
+        _lib.mfs_index_to_move.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p]
         _lib.mfs_perft.argtypes = [ctypes.c_char_p, ctypes.c_int]
         _lib.mfs_perft.restype = ctypes.c_int64
         _lib.mfs_policy_tables.argtypes = [ctypes.c_void_p] * 3
@@ -284,6 +291,41 @@ def encode_game(fen: str = "", moves: str = ""):
     if n < 0:
         raise ValueError(f"cannot encode game fen={fen!r} moves={moves!r}")
     return planes, legal[:n]
+
+
+# net.proto InputFormat values.
+INPUT_FORMATS = {"classical": 1, "castling_plane": 2, "canonical": 3,
+                 "canonical_hectoplies": 4, "canonical_hectoplies_armageddon": 132,
+                 "canonical_v2": 5, "canonical_v2_armageddon": 133}
+FILL = {"no": 0, "fen_only": 1, "always": 2}
+
+
+def encode_game_format(fen: str = "", moves: str = "", input_format="classical",
+                       fill="fen_only", history_planes=8):
+    """EncodePositionForNN for any input format: (planes [112, 64], legal
+    policy indices under the chosen transform, transform)."""
+    planes = np.zeros((112, 64), dtype=np.float32)
+    legal = np.full((256,), -1, dtype=np.int16)
+    t = ctypes.c_int(0)
+    fmt = INPUT_FORMATS.get(input_format, input_format)
+    n = lib().mfs_encode_game_format(fen.encode(), moves.encode(), int(fmt), FILL[fill],
+                                     history_planes, planes.ctypes.data, legal.ctypes.data,
+                                     256, ctypes.byref(t))
+    if n < 0:
+        raise ValueError(f"cannot encode game fen={fen!r} moves={moves!r} format={fmt}")
+    return planes, legal[:n], t.value
+
+
+def move_to_index(frm: int, to: int, promo: str = "", transform: int = 0) -> int:
+    return lib().mfs_move_to_index(frm, to, promo.encode() if promo else b"\0", transform)
+
+
+def index_to_move(index: int, transform: int = 0):
+    f, t, p = ctypes.c_int(), ctypes.c_int(), ctypes.c_char()
+    if lib().mfs_index_to_move(index, transform, ctypes.byref(f), ctypes.byref(t),
+                               ctypes.byref(p)) != 0:
+        raise ValueError(f"bad policy index {index}")
+    return f.value, t.value, p.value.decode() if p.value != b"\0" else ""
 
 
 def perft(fen: str, depth: int) -> int:

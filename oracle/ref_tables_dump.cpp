@@ -59,6 +59,33 @@ int main(int argc, char **argv) {
       const float v = NN::Tables::kPosEncoding[sq][c];
       std::fwrite(&v, 4, 1, f);
     }
+  // Section 5: MoveToNNIndex as in section 2 under the input transforms 1..7
+  // (flip 1, mirror 2, transpose 4 and their combinations).
+  for (int t = 1; t < 8; ++t)
+    for (int from = 0; from < 64; ++from)
+      for (int to = 0; to < 64; ++to)
+        for (int p = 0; p < 5; ++p) {
+          std::int16_t v = -1;
+          if (from != to) {
+            Move m = Move(Square(from), Square(to));
+            if (p > 0) {
+              static const PieceType kPt[4] = {QUEEN, ROOK, BISHOP, KNIGHT};
+              m = Move::make<PROMOTION>(Square(from), Square(to), kPt[p - 1]);
+            }
+            v = static_cast<std::int16_t>(NN::MoveToNNIndex(m, t));
+          }
+          std::fwrite(&v, 2, 1, f);
+        }
+  // Section 6: IndexToNNMove as in section 3 under the transforms 1..7.
+  for (int t = 1; t < 8; ++t)
+    for (int i = 0; i < NN::kPolicyOutputs; ++i) {
+      const Move m = NN::IndexToNNMove(i, t);
+      std::int16_t rec[3] = {static_cast<std::int16_t>(m.from_sq()),
+                             static_cast<std::int16_t>(m.to_sq()),
+                             static_cast<std::int16_t>(
+                                 m.type_of() == PROMOTION ? m.promotion_type() : 0)};
+      std::fwrite(rec, 2, 3, f);
+    }
   std::fclose(f);
   return 0;
 }

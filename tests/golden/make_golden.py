@@ -4,7 +4,8 @@
   tables, dumped by oracle/_ref/ref_tables_dump (compiled from the
   reference's src/nn/policy_map.cpp and tables/attention_policy_map.h by
   oracle/Makefile): kAttnPolicyMap (4288 int16), MoveToNNIndex over every
-  (from, to, promotion) (64*64*5 int16), IndexToNNMove (1858 x 3 int16).
+  (from, to, promotion) (64*64*5 int16), IndexToNNMove (1858 x 3 int16), and both again under
+  the input transforms 1..7.
   Digests only: the tables themselves are not copied into this repository.
 * seeded.json -- digests of this repository's seeded inputs and of the CPU
   oracle's outputs on them (pins the generator, the encoder and the oracle
@@ -42,14 +43,19 @@ def reference_tables():
     amap = raw[:4288]
     idx = raw[4288:4288 + 64 * 64 * 5]
     inv = raw[4288 + 64 * 64 * 5:]
-    pos = np.frombuffer(data[2 * n16:], dtype=np.float32)
-    assert inv.size == 1858 * 3 and pos.size == 64 * 64
+    pos = np.frombuffer(data[2 * n16:2 * n16 + 4 * 64 * 64], dtype=np.float32)
+    rest = np.frombuffer(data[2 * n16 + 4 * 64 * 64:], dtype=np.int16)
+    idx_t = rest[:7 * 64 * 64 * 5]
+    inv_t = rest[7 * 64 * 64 * 5:]
+    assert inv.size == 1858 * 3 and pos.size == 64 * 64 and inv_t.size == 7 * 1858 * 3
     return {"source": "oracle/_ref/ref_tables.bin (reference policy_map.cpp + "
                       "tables/attention_policy_map.h)",
             "attn_policy_map_sha256": sha(amap),
             "move_to_nn_index_sha256": sha(idx),
             "index_to_nn_move_sha256": sha(inv),
-            "pos_encoding_sha256": sha(pos)}
+            "pos_encoding_sha256": sha(pos),
+            "move_to_nn_index_transforms_1_7_sha256": sha(idx_t),
+            "index_to_nn_move_transforms_1_7_sha256": sha(inv_t)}
 
 
 def seeded():

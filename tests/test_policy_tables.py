@@ -66,12 +66,36 @@ def test_oracle_move_index_matches_reference():
 
 @pytest.mark.skipif(not os.path.exists(REF_BIN), reason="oracle/_ref not built")
 def test_reference_dump_matches_committed_digests():
-    raw = np.fromfile(REF_BIN, dtype=np.int16)
+    data = open(REF_BIN, "rb").read()
+    raw = np.frombuffer(data, dtype=np.int16)
     assert sha(raw[:4288]) == GOLD["attn_policy_map_sha256"]
     assert sha(raw[4288:4288 + 64 * 64 * 5]) == GOLD["move_to_nn_index_sha256"]
     n16 = 4288 + 64 * 64 * 5 + 1858 * 3
-    pos = np.frombuffer(open(REF_BIN, "rb").read()[2 * n16:], dtype=np.float32)
+    pos = np.frombuffer(data[2 * n16:2 * n16 + 4 * 64 * 64], dtype=np.float32)
     assert sha(pos) == GOLD["pos_encoding_sha256"]
+    rest = np.frombuffer(data[2 * n16 + 4 * 64 * 64:], dtype=np.int16)
+    assert sha(rest[:7 * 64 * 64 * 5]) == GOLD["move_to_nn_index_transforms_1_7_sha256"]
+    assert sha(rest[7 * 64 * 64 * 5:]) == GOLD["index_to_nn_move_transforms_1_7_sha256"]
+
+
+def test_product_move_index_under_transforms_matches_reference():
+    """MoveToNNIndex / IndexToNNMove with the canonical formats' input
+    transforms 1..7 (reference policy_map.cpp:305-410), every (from, to,
+    promotion) and every index, against digests of the reference's own
+    functions.  Under a transpose the reference maps squares by a half turn
+    rather than by the planes' reflection; the digests hold it to that."""
+    fwd = np.concatenate([
+        _move_to_index_table(lambda f, t, p, tr=tr: synth.move_to_index(f, t, p, tr)).ravel()
+        for tr in range(1, 8)])
+    assert sha(fwd) == GOLD["move_to_nn_index_transforms_1_7_sha256"]
+    inv = np.concatenate([
+        _index_to_move_table([synth.index_to_move(i, tr) for i in range(1858)]).ravel()
+        for tr in range(1, 8)])
+    assert sha(inv) == GOLD["index_to_nn_move_transforms_1_7_sha256"]
+    # Transform 0 through the same entry points: the plain tables.
+    assert sha(_move_to_index_table(synth.move_to_index)) == GOLD["move_to_nn_index_sha256"]
+    assert sha(_index_to_move_table([synth.index_to_move(i) for i in range(1858)])) == \
+        GOLD["index_to_nn_move_sha256"]
 
 
 def test_static_position_encoding_matches_reference():
