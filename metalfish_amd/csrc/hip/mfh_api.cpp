@@ -538,6 +538,17 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // unless METALFISH_HIP_SKINNY=0, which keeps the split-K path at batch 1).
   const char *skinny_env = std::getenv("METALFISH_HIP_SKINNY");
   d.skinny = !(skinny_env && skinny_env[0] == '0');
+  // FP8 precision: the row quantiser takes rows of up to 2048 values and
+  // the fp8 GEMM a K that is a multiple of 128 (the encoder GEMMs' inputs
+  // are E and FFN wide, in the body and in policy encoder layers).
+  if (d.fp8_act) {
+    for (const int w : {d.E, d.F, d.PL ? d.PF : d.F}) {
+      if (w > 2048 || w % 128)
+        return SetError(MFH_ERR_UNSUPPORTED,
+                        "the FP8 precision needs embedding and FFN widths that are "
+                        "multiples of 128 up to 2048");
+    }
+  }
   return MFH_OK;
 }
 

@@ -229,3 +229,13 @@ def test_fp8_precision_layer_integration():
     berr = np.abs(body - _ln(pre, W("ln2_gammas"), W("ln2_betas"), eps)).max()
     print(f"FFN2 residual sum max-abs {perr:.2e}, LayerNorm {berr:.2e}")
     assert perr <= 1e-4 * np.abs(ref_pre).max() and berr <= 1e-4
+
+
+def test_fp8_precision_rejects_widths_the_quantiser_cannot_take():
+    """FFN 2560 (> 2048 values per row) is refused at creation, before any
+    device work."""
+    spec = synth.NetSpec(**{**synth.SPECS["cpu_plumbing"].__dict__, "ffn": 2560})
+    weights = synth.make_weights(spec, seed=0, fp8=True)
+    with pytest.raises(RuntimeError, match="multiples of 128 up to 2048"):
+        backend.create_network(spec, weights, max_batch=4, device=-1, precision="fp8",
+                               weights_dtype="fp8")
