@@ -285,6 +285,23 @@ __device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col,
   Finish8<MODE, ACT>(p, row, col, v, b, rv);
 }
 
+// fp8 weights (W8): the e4m3 rows go through the LDS ring as bytes (BK
+// codes per row) when a stage's 1 KiB wave-loads split evenly over the
+// waves; otherwise each wave loads its own weight fragments from global
+// memory.
+template <int BM, int BN, int BK, int WM, int WN, bool SPLIT>
+constexpr bool W8InLds() {
+  return ((SPLIT ? 2 : 1) * BM * BK * 2 + BN * BK) % (1024 * WM * WN) == 0;
+}
+
+// Bytes of one LDS ring stage: the activation rows (bf16, hi then lo) and
+// the weight rows (bf16, or e4m3 bytes, or none).
+template <int BM, int BN, int BK, int WM, int WN, bool SPLIT, bool W8>
+constexpr int GemmStageBytes() {
+  constexpr int a = (SPLIT ? 2 : 1) * BM * BK * 2;
+  return !W8 ? a + BN * BK * 2 : W8InLds<BM, BN, BK, WM, WN, SPLIT>() ? a + BN * BK : a;
+}
+
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
           bool W8, bool F8 = false>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
@@ -294,10 +311,14 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int CPR = BK / 8;                      // 16-byte chunks per LDS row
   constexpr int RPL = 64 / CPR;                    // rows per 1 KiB wave-load
   constexpr int A_ROWS = SPLIT ? 2 * BM : BM;      // hi rows then lo rows
-  constexpr int W_ROWS = W8 ? 0 : BN;              // weight rows staged in LDS
-  constexpr int STAGE = (A_ROWS + W_ROWS) * BK;    // bf16 elements per stage
-  constexpr int LOADS = (A_ROWS + W_ROWS) * BK * 2 / 1024;
-  static_assert(!W8 || ST == 2, "fp8 weights use the two-stage loop");
+  constexpr int A_BYTES = A_ROWS * BK * 2;
+  constexpr bool W8L = W8 && W8InLds<BM, BN, BK, WM, WN, SPLIT>();  // e4m3 rows in LDS
+  constexpr bool W8G = W8 && !W8L;                 // e4m3 fragments from global
+  constexpr int STAGE_BYTES = GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>();
+  constexpr int STAGE = STAGE_BYTES / 2;           // bf16 elements per stage
+  constexpr int LOADS = STAGE_BYTES / 1024;
+  static_assert(STAGE_BYTES % 1024 == 0 && A_BYTES % 1024 == 0, "whole 1 KiB wave-loads");
+  static_assert(!W8G || ST == 2, "fp8 weight fragments from global use the two-stage loop");
   // F8: both operands are e4m3 bytes staged like bf16 rows of BK = 64
   // (128-byte rows): one v_mfma_f32_16x16x128_f8f6f4 per fragment pair and
   // K step.  The launcher passes the byte operands with K and the leading
@@ -343,23 +364,38 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   // Each lane's source pointer for its LPW wave-loads.  Lane l lands in row
   // l / CPR of its wave-load, physical chunk l % CPR, so it fetches the
   // logical chunk that the swizzle puts there.  Rows past M or N read a
-  // clamped valid row: they only feed outputs that are never stored.
-  const std::uint16_t *src[LPW];
+  // clamped valid row: they only feed outputs that are never stored.  The
+  // e4m3 weight rows (W8L) are BK bytes, 1024 / BK per wave-load, lane l
+  // fetching the wave-load's l-th 16 bytes unswizzled (a fragment read
+  // covers 16 whole consecutive rows).  kstep: bytes per K step.
+  const char *src[LPW];
+  int kstep[LPW];
   int dst[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int L = wave * LPW + j;
-    const int row = L * RPL + lane / CPR;
-    const int phys = lane % CPR;
-    const int chunk = BK == 64 ? (phys ^ (row & 7)) : (phys ^ ((row >> 1) & 3));
-    if (row < BM) {
-      src[j] = p.A + static_cast<size_t>(min(m0 + row, p.M - 1)) * p.lda + k_begin + chunk * 8;
-    } else if (SPLIT && row < 2 * BM) {
-      src[j] = p.A_lo + static_cast<size_t>(min(m0 + row - BM, p.M - 1)) * p.lda + k_begin +
-               chunk * 8;
+    if (W8L && L * 1024 >= A_BYTES) {
+      const int off = L * 1024 - A_BYTES + lane * 16;
+      const int row = off / BK;
+      src[j] = reinterpret_cast<const char *>(
+          p.W8 + static_cast<size_t>(min(n0 + row, p.N - 1)) * p.ldw + k_begin + off % BK);
+      kstep[j] = BK;
     } else {
-      src[j] = p.W + static_cast<size_t>(min(n0 + row - A_ROWS, p.N - 1)) * p.ldw + k_begin +
-               chunk * 8;
+      const int row = L * RPL + lane / CPR;
+      const int phys = lane % CPR;
+      const int chunk = BK == 64 ? (phys ^ (row & 7)) : (phys ^ ((row >> 1) & 3));
+      const std::uint16_t *s16;
+      if (row < BM) {
+        s16 = p.A + static_cast<size_t>(min(m0 + row, p.M - 1)) * p.lda + k_begin + chunk * 8;
+      } else if (SPLIT && row < 2 * BM) {
+        s16 = p.A_lo + static_cast<size_t>(min(m0 + row - BM, p.M - 1)) * p.lda + k_begin +
+              chunk * 8;
+      } else {
+        s16 = p.W + static_cast<size_t>(min(n0 + row - A_ROWS, p.N - 1)) * p.ldw + k_begin +
+              chunk * 8;
+      }
+      src[j] = reinterpret_cast<const char *>(s16);
+      kstep[j] = BK * 2;
     }
     dst[j] = L * 512;
   }
@@ -370,7 +406,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   // FP8 weight fragments: lane reads 8 codes of row n at k offset 8 fc.
   const std::uint8_t *wsrc[TN];
   u32x2 wq[KK][TN];
-  if constexpr (W8) {
+  if constexpr (W8G) {
 #pragma unroll
     for (int j = 0; j < TN; ++j)
       wsrc[j] = p.W8 + static_cast<size_t>(min(n0 + wn * WTN + j * 16 + fr, p.N - 1)) * p.ldw +
@@ -387,7 +423,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     if (s < KT) {
 #pragma unroll
       for (int j = 0; j < LPW; ++j)
-        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src[j] + s * BK),
+        __builtin_amdgcn_global_load_lds(static_cast<const void *>(src[j] + s * kstep[j]),
                                          MFH_LDS_PTR(lds + s * STAGE + dst[j]), 16, 0, 0);
     }
 
@@ -419,15 +455,15 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < LPW; ++j)
         __builtin_amdgcn_global_load_lds(
-            static_cast<const void *>(src[j] + (kt + ST - 1) * BK), MFH_LDS_PTR(next + dst[j]),
-            16, 0, 0);
+            static_cast<const void *>(src[j] + (kt + ST - 1) * kstep[j]),
+            MFH_LDS_PTR(next + dst[j]), 16, 0, 0);
     }
     const std::uint16_t *sa = lds + slot * STAGE;
     slot = slot + 1 == ST ? 0 : slot + 1;
     fill = fill + 1 == ST ? 0 : fill + 1;
     const std::uint16_t *sw = sa + A_ROWS * BK;
     u32x2 wn_next[KK][TN];
-    if constexpr (W8) {
+    if constexpr (W8G) {
       if (kt + 1 < KT) {
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
@@ -469,7 +505,11 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       bf16x8 af[TM], bw[TN];
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        if constexpr (W8)
+        if constexpr (W8L)
+          bw[j] = Fp8x8ToBf16(*reinterpret_cast<const u32x2 *>(
+              reinterpret_cast<const std::uint8_t *>(sw) + (wn * WTN + j * 16 + fr) * BK +
+              kk * 32 + fc * 8));
+        else if constexpr (W8G)
           bw[j] = Fp8x8ToBf16(wq[kk][j]);
         else
           bw[j] = *reinterpret_cast<const bf16x8 *>(
@@ -498,7 +538,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       }
     }
     }  // F8 / bf16 fragments
-    if constexpr (W8) {
+    if constexpr (W8G) {
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
@@ -696,8 +736,8 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
           bool W8 = false, bool F8 = false>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
-  constexpr int A_ROWS = SPLIT ? 2 * BM : BM;
-  constexpr size_t kLds = static_cast<size_t>(ST) * (A_ROWS + (W8 ? 0 : BN)) * BK * 2;
+  constexpr size_t kLds =
+      static_cast<size_t>(ST) * GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>();
   auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
@@ -756,8 +796,11 @@ hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
 hipError_t Launch(const GemmParams &p, hipStream_t stream) {
-  if (p.W8)  // fp8 weights: two stages (their fragments bypass LDS)
-    return LaunchW<BM, BN, BK, 2, WM, WN, SPLIT, true>(p, stream);
+  // fp8 weights: the ring's stages when their rows go through LDS, else two
+  // (fragments from global memory).
+  if (p.W8)
+    return LaunchW<BM, BN, BK, W8InLds<BM, BN, BK, WM, WN, SPLIT>() ? ST : 2, WM, WN, SPLIT,
+                   true>(p, stream);
   return LaunchW<BM, BN, BK, ST, WM, WN, SPLIT, false>(p, stream);
 }
 
@@ -908,9 +951,14 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   if (f8)
     return big_tiles % 256 == 0 ? LaunchW<256, 256, 64, 2, 4, 2, false, false, true>(p, stream)
                                 : LaunchW<128, 128, 64, 2, 2, 4, false, false, true>(p, stream);
-  if (large && !p.W8 && p.k_splits == 1 && big_tiles % 256 == 0)
+  if (large && p.k_splits == 1 && big_tiles % 256 == 0) {
+    // fp8 weights too: their e4m3 rows share the ring (40 / 24 KiB stages).
+    if (p.W8)
+      return split ? LaunchW<256, 256, 32, 3, 4, 2, true, true>(p, stream)
+                   : LaunchW<256, 256, 32, 4, 4, 2, false, true>(p, stream);
     return split ? LaunchW<256, 256, 32, 3, 4, 2, true, false>(p, stream)
                  : LaunchW<256, 256, 32, 4, 4, 2, false, false>(p, stream);
+  }
   // Split precision with fewer 128 x 128 tiles than CUs (the out-projection
   // and FFN at M = 2048 .. 3072): 64 x 64 tiles, four times the workgroups
   // (out-projection at M = 2048: 13.5 instead of 25.4 us; batch 32 forward
@@ -937,8 +985,12 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
           9 * ((t256 + 255) / 256) < 5 * ((tiles128 + 255) / 256))
         return LaunchW<256, 128, 32, 2, 4, 2, true, false>(p, stream);
     }
+    // Split precision with fp8 weights: BK = 64, whose stage holds the
+    // e4m3 rows in LDS (at BK = 32 the 128 x 128 stage does not split
+    // evenly over the waves).
     if (kslice <= 1024)
-      return split ? Launch<128, 128, 32, 2, 2, 4, true>(p, stream)
+      return split ? (p.W8 ? Launch<128, 128, 64, 2, 2, 4, true>(p, stream)
+                           : Launch<128, 128, 32, 2, 2, 4, true>(p, stream))
              : p.W8 ? Launch<256, 128, 32, 2, 4, 2, false>(p, stream)
                     : LaunchW<256, 128, 32, 3, 4, 2, false, false>(p, stream);
     return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
