@@ -90,6 +90,11 @@ constexpr int kSquares = 64;
 constexpr int kMaxMoves = 256;  // edges per node (reference src/mcts/search.cpp:49)
 constexpr int kPlanes = 112;
 constexpr int kPolicy = 1858;
+// Largest batch whose smolgen dense1 / dense2 run as few-row GEMMs: forward
+// 1.513 -> 1.434 ms at batch 2, 1.662 -> 1.586 at 4, 1.673 -> 1.625 at 8,
+// 2.097 -> 2.071 at 16; from 24 up it was slower (batch 32 2.58 -> 2.78:
+// every workgroup of dense1 reads all the positions' compression rows).
+constexpr int kSmolgenFewRowMaxBatch = 16;
 
 std::uint16_t ToBf16(float f) {
   std::uint32_t u;
@@ -820,8 +825,13 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   }
   // Row statistics of the single-position smolgen chain's deferred
   // LayerNorms (partial sums per workgroup): dense1 and dense2 outputs.
-  add("lnst_s1", std::max<size_t>(256, 8 * size_t(mfh::SkinnyGemmParts(d.Hs ? d.Hs : 4))));
-  add("lnst_s2", std::max<size_t>(256, 8 * size_t(mfh::SkinnyGemmParts(d.HG ? d.HG : 4))));
+  // One (sum, sum of squares) pair per producing workgroup and row, for up
+  // to kSkinnyMaxRows rows.
+  const size_t stat_rows = std::min<size_t>(B, mfh::kSkinnyMaxRows);
+  add("lnst_s1",
+      std::max<size_t>(256, 8 * stat_rows * size_t(mfh::SkinnyGemmParts(d.Hs ? d.Hs : 4))));
+  add("lnst_s2",
+      std::max<size_t>(256, 8 * stat_rows * size_t(mfh::SkinnyGemmParts(d.HG ? d.HG : 4))));
   // Split-K partials of small-batch GEMMs (main stream, and the smolgen
   // chain on the side stream).
   add("splitk", splitk_floats * 4);
@@ -1211,13 +1221,25 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       !net->fp8 && !d.fused_bias && d.HG <= 8192 &&
       mfh::SkinnyShapeOk(B, d.Hs, kSquares * d.C) && mfh::SkinnyShapeOk(B, d.HG, d.Hs) &&
       mfh::SkinnyShapeOk(B * d.H, kSquares * kSquares, d.G);
-  auto run_sk = [&](const mfh::SkinnyParams &p, const char *role) {
+  // Up to kSmolgenFewRowMaxBatch positions: dense1 and dense2 (one row per
+  // position) run as few-row GEMMs too, dense2 applying dense1's LayerNorm
+  // as it loads its rows; dense2's LayerNorm and the global projection
+  // (B * H rows) stay separate launches.
+  const bool few_row_dense = d.smolgen && d.skinny && !few_row_smolgen &&
+                             B <= kSmolgenFewRowMaxBatch && !net->fp8 &&
+                             mfh::SkinnyShapeOk(B, d.Hs, kSquares * d.C) &&
+                             mfh::SkinnyShapeOk(B, d.HG, d.Hs);
+  auto run_sk = [&](const mfh::SkinnyParams &p, const char *role, hipStream_t on = nullptr) {
     const double flops = 2.0 * p.M * p.N * p.K;
     const double bytes = 2.0 * p.N * p.K + 4.0 * p.M * p.K + 4.0 * p.M * p.N;
-    StageTimer t(net, st, std::string("gemm_bf16:") + role, flops, bytes);
-    return mfh::LaunchSkinnyGemm(p, st, &err_);
+    hipStream_t s = on ? on : st;
+    StageTimer t(net, s, std::string("gemm_bf16:") + role, flops, bytes);
+    return mfh::LaunchSkinnyGemm(p, s, &err_);
   };
-  auto smolgen_few_row = [&](const Layer &L) -> int {
+  // dense1 (from the compression planes, writing its activated rows and their
+  // partial statistics) and dense2 (normalising dense1's rows as it loads
+  // them) as few-row GEMMs; dense2's statistics too when `dense2_stats`.
+  auto smolgen_dense_few_row = [&](const Layer &L, hipStream_t on, bool dense2_stats) -> int {
     auto base = [&](const size_t (&w)[2], int m, int n, int k, const float *bias, int act,
                     int mode, void *C, int ldc) {
       mfh::SkinnyParams p;
@@ -1240,7 +1262,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     p1.a16_lo = ws.Lo("comp");
     p1.lda = flat;
     p1.stats_out = ws.S<float>("lnst_s1");
-    MFH_RUN(run_sk(p1, "smolgen_dense1"));
+    MFH_RUN(run_sk(p1, "smolgen_dense1", on));
     mfh::SkinnyParams p2 = base(L.sg_d2_w, B, d.HG, d.Hs, net->W<float>(L.sg_d2_b),
                                 d.act_smolgen, mfh::SKINNY_OUT_F32, ws.S<float>("sg2"), d.HG);
     p2.x = ws.S<float>("sg1");
@@ -1253,8 +1275,28 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     p2.gamma = net->W<float>(L.sg_ln1_g);
     p2.beta = net->W<float>(L.sg_ln1_b);
     p2.ln_split = d.split_attn;
-    p2.stats_out = ws.S<float>("lnst_s2");
-    MFH_RUN(run_sk(p2, "smolgen_dense2"));
+    if (dense2_stats)
+      p2.stats_out = ws.S<float>("lnst_s2");
+    MFH_RUN(run_sk(p2, "smolgen_dense2", on));
+    return MFH_OK;
+  };
+  auto smolgen_few_row = [&](const Layer &L) -> int {
+    MFH_RC(smolgen_dense_few_row(L, st, true));
+    auto base = [&](const size_t (&w)[2], int m, int n, int k, const float *bias, int act,
+                    int mode, void *C, int ldc) {
+      mfh::SkinnyParams p;
+      p.W = net->W<std::uint16_t>(w[0]);
+      p.ldw = k;
+      p.M = m;
+      p.N = n;
+      p.K = k;
+      p.bias = bias;
+      p.act = act;
+      p.out_mode = mode;
+      p.C = C;
+      p.ldc = ldc;
+      return p;
+    };
     mfh::SkinnyParams pg =
         base(net->global_w, B * d.H, kSquares * kSquares, d.G, nullptr, mfh::ACT_NONE,
              d.split_attn ? mfh::SKINNY_OUT_F32 : mfh::SKINNY_OUT_BF16, ws.S<void>("bias"),
@@ -1319,6 +1361,18 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
         q.partials = sk;
         return q;
       };
+      // The shared global projection of the normalised dense2 rows into the
+      // attention bias (unless attention projects the gen vectors itself).
+      auto smolgen_global = [&](hipStream_t s) -> int {
+        if (d.fused_bias)
+          return MFH_OK;
+        MFH_RUN(run(chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares,
+                               d.G, nullptr,
+                               d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
+                               ws.S<void>("bias"), nullptr, kSquares * kSquares),
+                    "smolgen_global", s));
+        return MFH_OK;
+      };
       if (big) {
         const size_t skip = static_cast<size_t>(3) * E;  // rows of Q | K | V
         mfh::GemmParams pc = chain_gemm("act", E, L.qkv_w, E, M, d.C, E,
@@ -1331,6 +1385,13 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
           pc.W += skip * E;
         }
         MFH_RUN(run(pc, "smolgen_compress", on));
+      }
+      if (few_row_dense) {
+        MFH_RC(smolgen_dense_few_row(L, on, false));
+        MFH_RUN(run_ln(ln(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
+                          net->W<float>(L.sg_ln2_b), nullptr, "sg2n"),
+                       on));
+        return smolgen_global(on);
       }
       const int flat = kSquares * d.C;
       mfh::GemmParams p1 = chain_gemm("comp", flat, L.sg_d1_w, flat, B, d.Hs, flat, nullptr,
@@ -1359,14 +1420,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       l2.bias = net->W<float>(L.sg_d2_b);
       l2.act = d.act_smolgen;
       MFH_RUN(run_ln(l2, on));
-      if (d.fused_bias)
-        return MFH_OK;  // attention projects the gen vectors itself
-      MFH_RUN(run(chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares,
-                             d.G, nullptr,
-                             d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
-                             ws.S<void>("bias"), nullptr, kSquares * kSquares),
-                  "smolgen_global", on));
-      return MFH_OK;
+      return smolgen_global(on);
     };
     if (L.smolgen && !d.fused_bias) {
       ap.bias = ws.S<void>("bias");
