@@ -810,18 +810,43 @@ bool Aligned(const void *ptr, std::uintptr_t bytes) {
 
 }  // namespace
 
-int GemmAutoSplits(const GemmParams &p) {
+// Split-K at few positions (64 x 64 tiles, K in 64-wide steps).  A GEMM
+// kernel here costs ~5 us however short its K loop, and a separate reduce
+// launch another ~4.5 us, so:
+// * the slices fill at most one workgroup per CU (256): beyond that the
+//   extra slices lengthen the kernel more than they shorten each loop;
+// * a split whose partials need their own reduce launch (LaunchGemm) is
+//   taken for long K loops only (>= 16 steps) and at least four ways: a
+//   two-way split of FFN1 at 256 rows (10.1 + 4.8 us against 11.9 us whole)
+//   and any split of the smolgen global projection (K = 256) lost;
+// * a caller whose next kernel sums the partials anyway (the LayerNorm
+//   after a residual GEMM) also takes a two-way split up to 384 workgroups.
+// Measured forward (with the three-stage rings below): batch 1 1.29 ->
+// 1.20 ms, 2 1.43 -> 1.26, 4 1.58 -> 1.33, 8 1.62 -> 1.48, 12 1.79 -> 1.76.
+constexpr long kSplitMaxGroups = 256;
+constexpr long kSplitPairMaxGroups = 384;
+constexpr int kSplitMinSteps = 16;
+constexpr int kSplitMinParts = 4;
+
+int GemmAutoSplits(const GemmParams &p, bool summed_by_consumer) {
   const bool large = p.M >= 2048 && p.N >= 128;
   if (large || p.k_splits != 1 || !p.partials || p.N % 4 || p.K % 64 || p.M <= 0 || p.N <= 0)
     return 1;
   const long tiles = static_cast<long>((p.M + 63) / 64) * ((p.N + 63) / 64);
   const int steps = p.K / 64;
+  const auto fits = [&](int s) {
+    return static_cast<size_t>(s) * p.M * p.N <= p.partials_floats;
+  };
   int splits = 1;
-  if (tiles < 256)
+  if (summed_by_consumer || steps >= kSplitMinSteps)
     for (int s = 2; s <= steps; ++s)
-      if (steps % s == 0 && tiles * s <= 512 &&
-          static_cast<size_t>(s) * p.M * p.N <= p.partials_floats)
+      if (steps % s == 0 && tiles * s <= kSplitMaxGroups && fits(s))
         splits = s;
+  if (!summed_by_consumer && splits < kSplitMinParts)
+    splits = 1;
+  if (splits == 1 && summed_by_consumer && steps % 2 == 0 && tiles * 2 <= kSplitPairMaxGroups &&
+      fits(2))
+    splits = 2;
   return splits;
 }
 
@@ -905,9 +930,9 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   const bool split = p.A_lo != nullptr;
   const bool large = p.M >= 2048 && p.N >= 128;
   // Small problems (few positions): 64 x 64 tiles leave most CUs idle and
-  // walk K serially, so the launcher splits K over up to 512 workgroups,
-  // writes fp32 partials to p.partials and sums them in slice order in a
-  // second kernel that applies the epilogue.  The split depends on the shape
+  // walk K serially, so the launcher splits K (GemmAutoSplits), writes fp32
+  // partials to p.partials through a three-stage ring and sums them in
+  // slice order in a second kernel that applies the epilogue.  The split depends on the shape
   // only: a batch size always takes the same path and gives the same bits.
   if (!large && p.k_splits == 1 && p.partials && Aligned(p.partials, 16) && p.vec &&
       p.N % 4 == 0) {
@@ -924,8 +949,8 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       q.resid = nullptr;
       q.k_splits = splits;
       q.vec = true;
-      const hipError_t e = split ? Launch<64, 64, 64, 2, 2, 2, true>(q, stream)
-                                 : Launch<64, 64, 64, 2, 2, 2, false>(q, stream);
+      const hipError_t e = split ? Launch<64, 64, 64, 3, 2, 2, true>(q, stream)
+                                 : Launch<64, 64, 64, 3, 2, 2, false>(q, stream);
       if (e != hipSuccess)
         return e;
       // The partials already carry the fp8 row scale.
@@ -996,15 +1021,17 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
                  : Launch<128, 128, 64, 2, 2, 2, false>(p, stream);
   }
-  // 64 x 64 tiles over the whole K (Q|K|V at 6-31 positions, the
+  // 64 x 64 tiles over the whole K (Q|K|V at 4-31 positions, the
   // out-projection and FFN at 16-31, the smolgen dense2 and global
-  // projection at some batches): from 256 rows up a three-stage ring keeps
-  // two K steps in flight (batch 16 forward 2.30 -> 2.05 ms, batch 8 1.75
-  // -> 1.68, batch 256 +0.9 %); at 128 rows (smolgen dense2 at batch 128,
+  // projection at some batches): from 256 rows up, or over K >= 1024, a
+  // three-stage ring keeps two K steps in flight (batch 16 forward 2.30 ->
+  // 2.05 ms, batch 8 1.75 -> 1.68, batch 256 +0.9 %, batch 3 1.51 -> 1.36;
+  // Q|K|V took 16.0 us at 192 rows with two stages, 11.6 us at 256 rows
+  // with three); for short K at 128 rows (smolgen dense2 at batch 128,
   // beside the Q|K|V GEMM on the other stream) it was 1.7 % slower, and four
   // stages (one workgroup per CU) were slower at every batch.
   if (kslice % 64 == 0) {
-    if (p.M >= 256)
+    if (p.M >= 256 || kslice >= 1024)
       return split ? Launch<64, 64, 64, 3, 2, 2, true>(p, stream)
                    : Launch<64, 64, 64, 3, 2, 2, false>(p, stream);
     return split ? Launch<64, 64, 64, 2, 2, 2, true>(p, stream)

@@ -1167,7 +1167,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     }
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
-    const int splits = f8 ? 1 : mfh::GemmAutoSplits(p);
+    const int splits = f8 ? 1 : mfh::GemmAutoSplits(p, true);
     if (f8) {
       MFH_RC(quant(a, k));
     } else if (splits > 1) {
@@ -1406,7 +1406,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       MFH_RUN(run_ln(l1, on));
       mfh::GemmParams p2 = chain_gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr,
                                       mfh::GEMM_OUT_F32, sg2, nullptr, d.HG);
-      const int s2 = mfh::GemmAutoSplits(p2);
+      const int s2 = mfh::GemmAutoSplits(p2, true);
       if (s2 > 1) {
         p2.C = sk;
         p2.k_splits = s2;

@@ -89,8 +89,10 @@ struct GemmParams {
 hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err);
 // Number of K slices LaunchGemm splits this (small-M) problem into when
 // p.partials is set and p.k_splits == 1, or 1.  A caller that sums the
-// partials itself launches with k_splits set to this value instead.
-int GemmAutoSplits(const GemmParams &p);
+// partials itself (in a kernel it launches anyway, such as the LayerNorm
+// after a residual GEMM) passes summed_by_consumer and launches with
+// k_splits set to this value instead.
+int GemmAutoSplits(const GemmParams &p, bool summed_by_consumer = false);
 
 // Row-panel GEMM: one workgroup of eight waves owns 64 whole output rows
 // and a panel of 128 * TN columns (TN = 2, 4, 6 or 8), so a row's outputs

@@ -107,7 +107,7 @@ def test_fp8_weight_parity(spec_name, n, batch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n,batch", [(40, None), (40, 128), (8, None)])
+@pytest.mark.parametrize("n,batch", [(40, None), (40, 128)])
 def test_fp8_activation_parity(n, batch):
     """The FP8 precision (e4m3 activations into the body's Q|K|V, out-
     projection and FFN GEMMs from 2048 token rows) against the oracle on the
@@ -119,15 +119,42 @@ def test_fp8_activation_parity(n, batch):
     1.1e-2 at 40 positions / a batch of 128, while each fp8 GEMM matches
     fp64 of its codes (test_fp8_precision_layer_integration): the loss is
     the 3-bit mantissa of the activations compounding over 15 layers.  The
-    bounds below only catch regressions.  8 positions (512 rows) stay on the
-    bf16 GEMMs and keep the gates."""
+    bounds below only catch regressions."""
     if backend.device_count() < 1:
         pytest.fail("GPU tests need an MI355X; none visible")
     perr, werr, agree = _fp8_parity("bt4", n, batch=batch, precision="fp8")
-    if n * 64 < 2048 and (batch or n) * 64 < 2048:
-        assert perr <= 2e-2 and werr <= 5e-3 and agree == 1.0
-    else:
-        assert perr <= 0.3 and werr <= 0.04 and agree >= 0.7
+    assert perr <= 0.3 and werr <= 0.04 and agree >= 0.7
+
+
+@pytest.mark.gpu
+def test_fp8_precision_below_2048_rows_is_bf16():
+    """Below 2048 token rows the FP8 precision runs the BF16 path: the same
+    bits as a BF16-precision net on the same e4m3 weights.  Against the
+    oracle it is held to the single-bf16 bounds (policy max-abs 3e-2, WDL
+    5e-3; top-1 reported, since the random-init net has near-tied legal
+    logits that single-bf16 rounding reorders)."""
+    import oracle
+
+    if backend.device_count() < 1:
+        pytest.fail("GPU tests need an MI355X; none visible")
+    spec = synth.SPECS["bt4"]
+    weights = synth.make_weights(spec, seed=0, fp8=True)
+    planes, legal = synth.playout_positions(8, seed=0)
+    out = {}
+    for precision in ("fp8", "bf16"):
+        net = backend.create_network(spec, weights, max_batch=8, device=0, weights_dtype="fp8",
+                                     precision=precision)
+        out[precision] = net.evaluate_batch(planes)
+        net.close()
+    for k in ("policy", "wdl"):
+        assert np.array_equal(out["fp8"][k].view(np.uint32), out["bf16"][k].view(np.uint32)), k
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads), weights).evaluate_batch(planes)
+    perr = np.abs(out["fp8"]["policy"] - ref["policy"]).max()
+    werr = np.abs(out["fp8"]["wdl"] - ref["wdl"]).max()
+    agree = np.mean([np.argmax(out["fp8"]["policy"][i, l[l >= 0]]) ==
+                     np.argmax(ref["policy"][i, l[l >= 0]]) for i, l in enumerate(legal)])
+    print(f"fp8 below 2048 rows: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {agree:.3f}")
+    assert perr <= 3e-2 and werr <= 5e-3
 
 
 def test_fp8_precision_needs_fp8_weights():

@@ -477,7 +477,7 @@ def test_moves_left_head(precision, batch):
     out = net.evaluate_batch(planes)
     tol = 1e-3 if precision == "bf16x2" else 5e-3
     assert np.abs(out["moves_left"] - ref["moves_left"]).max() <= tol
-    assert np.abs(out["policy"] - ref["policy"]).max() <= 2e-2
+    assert np.abs(out["policy"] - ref["policy"]).max() <= _policy_tol(precision)
     assert np.abs(out["wdl"] - ref["wdl"]).max() <= 5e-3
     # Device entry with an explicit moves-left output equals the host path.
     dev = _DeviceBuffers()
@@ -516,7 +516,7 @@ def test_pe_map_static_embedding(precision, batch):
     net = backend.create_network(spec, weights, max_batch=batch, precision=precision)
     out = net.evaluate_batch(planes)
     net.close()
-    assert np.abs(out["policy"] - ref["policy"]).max() <= 2e-2
+    assert np.abs(out["policy"] - ref["policy"]).max() <= _policy_tol(precision)
     assert np.abs(out["wdl"] - ref["wdl"]).max() <= 5e-3
     if precision == "bf16x2":
         assert _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
@@ -539,7 +539,7 @@ def test_policy_encoder_layers(precision, batch, tmp_path):
     net = backend.create_network(spec, weights, max_batch=batch, precision=precision)
     out = net.evaluate_batch(planes)
     net.close()
-    assert np.abs(out["policy"] - ref["policy"]).max() <= 2e-2
+    assert np.abs(out["policy"] - ref["policy"]).max() <= _policy_tol(precision)
     assert np.abs(out["wdl"] - ref["wdl"]).max() <= 5e-3
     if precision == "bf16x2":
         assert _top1_agreement(out["policy"], ref["policy"], legal) >= 0.995
