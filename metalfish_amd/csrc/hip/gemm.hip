@@ -810,6 +810,14 @@ bool Aligned(const void *ptr, std::uintptr_t bytes) {
 
 }  // namespace
 
+// Rows from which the tile rules for large problems apply (below them,
+// 64 x 64 tiles over the whole K or split-K).  From 1536 rows (24
+// positions) Q|K|V takes 256 x 128 split tiles instead of 1176-1519
+// whole-K 64 x 64 ones: forward at batch 24 2.47 -> 2.41 ms, 28 2.60 ->
+// 2.50, 31 2.84 -> 2.56; from 1024 rows it was slower (batch 16 2.07 ->
+// 2.34).
+constexpr int kLargeRows = 1536;
+
 // Split-K at few positions (64 x 64 tiles, K in 64-wide steps).  A GEMM
 // kernel here costs ~5 us however short its K loop, and a separate reduce
 // launch another ~4.5 us, so:
@@ -829,7 +837,7 @@ constexpr int kSplitMinSteps = 16;
 constexpr int kSplitMinParts = 4;
 
 int GemmAutoSplits(const GemmParams &p, bool summed_by_consumer) {
-  const bool large = p.M >= 2048 && p.N >= 128;
+  const bool large = p.M >= kLargeRows && p.N >= 128;
   if (large || p.k_splits != 1 || !p.partials || p.N % 4 || p.K % 64 || p.M <= 0 || p.N <= 0)
     return 1;
   const long tiles = static_cast<long>((p.M + 63) / 64) * ((p.N + 63) / 64);
@@ -928,7 +936,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
             (p.resid16 ? Aligned(p.resid16, 16) && Aligned(p.resid16_lo, 16) && p.ldr % 8 == 0
                        : Aligned(p.resid, 16) && p.ldr % 4 == 0));
   const bool split = p.A_lo != nullptr;
-  const bool large = p.M >= 2048 && p.N >= 128;
+  const bool large = p.M >= kLargeRows && p.N >= 128;
   // Small problems (few positions): 64 x 64 tiles leave most CUs idle and
   // walk K serially, so the launcher splits K (GemmAutoSplits), writes fp32
   // partials to p.partials through a three-stage ring and sums them in

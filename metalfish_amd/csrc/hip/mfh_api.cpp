@@ -95,6 +95,12 @@ constexpr int kPolicy = 1858;
 // 2.097 -> 2.071 at 16; from 24 up it was slower (batch 32 2.58 -> 2.78:
 // every workgroup of dense1 reads all the positions' compression rows).
 constexpr int kSmolgenFewRowMaxBatch = 16;
+// Token rows from which each layer's smolgen chain runs on the second stream
+// beside Q|K|V (its compression then a GEMM of its own): past the few-row
+// batches, from 17 positions (forward at batch 24 2.57 -> 2.47 ms, 28 2.72
+// -> 2.59, 20 2.31 -> 2.29; with the few-row chain at 16 positions it was
+// slower, 2.07 -> 2.19).
+constexpr int kSmolgenSideRows = 1088;
 
 std::uint16_t ToBf16(float f) {
   std::uint32_t u;
@@ -871,6 +877,7 @@ struct WsView {
   template <typename T> T *S(const std::string &name) const {
     return reinterpret_cast<T *>(base + off->at(name));
   }
+  bool Has(const std::string &name) const { return off->count(name) != 0; }
   // Residual plane of a bf16 activation, or null in single precision.
   std::uint16_t *Lo(const std::string &name) const {
     auto it = off->find(name + "_lo");
@@ -1333,11 +1340,14 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // stream.  With the stage profiler on, everything stays on the main
     // stream so each launch is timed alone.
     const int li = layer_index++;
-    const bool big = M >= 2048;
+    const bool side_chain = M >= kSmolgenSideRows;
     // FP8 precision from 2048 rows: Q|K|V, out-projection and FFN GEMMs on
     // per-row e4m3 copies of their inputs (the smolgen chain stays bf16).
-    const bool f8 = d.fp8_act && big;
-    hipStream_t sg_stream = big && !net->profiling ? net->side : st;
+    const bool f8 = d.fp8_act && M >= 2048;
+    // The no-allocation layout has one split-K buffer: the chain then runs
+    // on the caller's stream (same kernels and splits, so the same bits).
+    hipStream_t sg_stream =
+        side_chain && !net->profiling && ws.Has("splitk_sg") ? net->side : st;
     mfh::AttentionParams ap;
     ap.qkv = ws.S<std::uint16_t>("qkv");
     ap.qkv_lo = ws.Lo("qkv");
@@ -1373,7 +1383,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
                     "smolgen_global", s));
         return MFH_OK;
       };
-      if (big) {
+      if (side_chain) {
         const size_t skip = static_cast<size_t>(3) * E;  // rows of Q | K | V
         mfh::GemmParams pc = chain_gemm("act", E, L.qkv_w, E, M, d.C, E,
                                         net->W<float>(L.qkv_b) + skip, mfh::GEMM_OUT_BF16,
@@ -1426,7 +1436,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       ap.bias = ws.S<void>("bias");
       ap.bias_f32 = d.split_attn ? 1 : 0;
     }
-    if (L.smolgen && big) {
+    if (L.smolgen && side_chain) {
       if (sg_stream != st) {
         MFH_HIP_CHECK(hipEventRecord(net->fork_join[2 * li], st));
         MFH_HIP_CHECK(hipStreamWaitEvent(sg_stream, net->fork_join[2 * li], 0));
@@ -1437,10 +1447,10 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       if (sg_stream != st)
         MFH_HIP_CHECK(hipEventRecord(net->fork_join[2 * li + 1], sg_stream));
     }
-    mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M, 3 * E + (L.smolgen && !big ? d.C : 0),
-                              E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
+    mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M,
+                              3 * E + (L.smolgen && !side_chain ? d.C : 0), E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
                               ws.S<std::uint16_t>("qkv"), ws.Lo("qkv"), 3 * E);
-    if (L.smolgen && !big) {
+    if (L.smolgen && !side_chain) {
       pq.split_n = 3 * E;
       pq.C2 = ws.S<std::uint16_t>("comp");
       pq.C2_lo = ws.Lo("comp");
@@ -1451,12 +1461,12 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       use_fp8(pq, "act");
     }
     MFH_RUN(run(pq, "qkv"));
-    if (L.smolgen && !big) {
+    if (L.smolgen && !side_chain) {
       const int rc = smolgen_chain(st);
       if (rc != MFH_OK)
         return rc;
     }
-    if (L.smolgen && big && sg_stream != st)
+    if (L.smolgen && side_chain && sg_stream != st)
       MFH_HIP_CHECK(hipStreamWaitEvent(st, net->fork_join[2 * li + 1], 0));
     if (L.smolgen && d.fused_bias) {
       // Attention with the smolgen global projection in the kernel
@@ -2128,8 +2138,13 @@ int mfh_net_eval_device_noalloc(mfh_net *net, int batch, const uint64_t *d_masks
   // scratch array needs clearing between calls.
   const WsView ws{base, &net->noalloc_off, kSmallSplitKFloats};
   net->noalloc_call = true;
-  const int rc = Forward(net, ws, batch, d_masks, d_values, d_policy, d_wdl,
-                         ws.S<float>("mlh"), static_cast<hipStream_t>(stream));
+  int rc;
+  try {
+    rc = Forward(net, ws, batch, d_masks, d_values, d_policy, d_wdl, ws.S<float>("mlh"),
+                 static_cast<hipStream_t>(stream));
+  } catch (const std::exception &e) {
+    rc = SetError(MFH_ERR_INVALID, std::string("mfh_net_eval_device_noalloc: ") + e.what());
+  }
   net->noalloc_call = false;
   return rc;
 }

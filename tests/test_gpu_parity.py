@@ -148,14 +148,17 @@ def test_bt4_net_parity_16_positions(precision):
         assert top1 >= 0.995
 
 
-@pytest.mark.parametrize("precision,n", [("bf16x2", 40), ("bf16", 40), ("bf16x2", 33)])
+@pytest.mark.parametrize("precision,n", [("bf16x2", 40), ("bf16", 40), ("bf16x2", 33),
+                                         ("bf16x2", 28)])
 def test_bt4_large_batch_tiles(precision, n):
     """40 positions = 2560 token rows: the dense layers take the large-M tile
     configurations: 256 x 128 split tiles for Q|K|V (240 tiles; bf16: 128 x
     128 / 256 x 128 ones), and the 64 x 64 tiles that split precision uses
     below one 128 x 128 tile per CU for the out-projection, FFN1 and FFN2
     (160 / 240 / 160 tiles).  33 positions = 2112 rows: the 256 x 128 split
-    tiles of Q|K|V end in a partial tile of 64 rows."""
+    tiles of Q|K|V end in a partial tile of 64 rows.  28 positions = 1792
+    rows: the large-M tiles below 2048 rows, with the smolgen chain on the
+    second stream."""
     gpu, ref, legal = _compare("bt4", n, check_packed=False, precision=precision)
     perr = np.abs(gpu["policy"] - ref["policy"]).max()
     werr = np.abs(gpu["wdl"] - ref["wdl"]).max()
