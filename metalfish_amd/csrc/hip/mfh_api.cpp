@@ -1358,9 +1358,9 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     ap.ctx = ws.S<std::uint16_t>("ctx");
     ap.ctx_lo = ws.Lo("ctx");
     // Dense1 on the flattened compression (split-K partials summed by the
-    // LayerNorm kernel with bias and activation), dense2 (its K slices at
-    // few positions summed the same way), then the shared global projection
-    // into the attention bias.
+    // LayerNorm kernel with bias and activation), dense2 (bias and
+    // activation in its epilogue) and its LayerNorm, then the shared global
+    // projection into the attention bias.
     auto smolgen_chain = [&](hipStream_t on) -> int {
       if (few_row_smolgen)
         return smolgen_few_row(L);
@@ -1416,22 +1416,22 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       l1.bias = net->W<float>(L.sg_d1_b);
       l1.act = d.act_smolgen;
       MFH_RUN(run_ln(l1, on));
-      mfh::GemmParams p2 = chain_gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs, nullptr,
-                                      mfh::GEMM_OUT_F32, sg2, nullptr, d.HG);
-      const int s2 = mfh::GemmAutoSplits(p2, true);
-      if (s2 > 1) {
-        p2.C = sk;
-        p2.k_splits = s2;
-        p2.partials = nullptr;
-      }
+      // Dense2 over the whole K with its bias and activation in the GEMM
+      // epilogue, spread over its 128+ workgroups; the 8192-wide LayerNorm
+      // after it (one workgroup per row) then only normalises.  Measured
+      // against a split-K dense2 whose partials, bias and activation that
+      // LayerNorm summed: forward 1.1 % faster at batch 24, 0.6 % at 32,
+      // 1.2 % at 64, 0.2 % at 256 (the LayerNorm alone 9.8 us at batch 32
+      // against ~5 us for the other small kernels of the chain).
+      mfh::GemmParams p2 = chain_gemm("sg1n", d.Hs, L.sg_d2_w, d.Hs, B, d.HG, d.Hs,
+                                      net->W<float>(L.sg_d2_b), mfh::GEMM_OUT_F32, sg2, nullptr,
+                                      d.HG);
+      p2.act = d.act_smolgen;
+      p2.partials = nullptr;  // no automatic split-K
       MFH_RUN(run(p2, "smolgen_dense2", on));
-      mfh::LayerNormParams l2 = ln(s2 > 1 ? sk : sg2, B, d.HG, 1e-3f,
-                                   net->W<float>(L.sg_ln2_g), net->W<float>(L.sg_ln2_b),
-                                   nullptr, "sg2n");
-      l2.parts = s2;
-      l2.bias = net->W<float>(L.sg_d2_b);
-      l2.act = d.act_smolgen;
-      MFH_RUN(run_ln(l2, on));
+      MFH_RUN(run_ln(ln(sg2, B, d.HG, 1e-3f, net->W<float>(L.sg_ln2_g),
+                        net->W<float>(L.sg_ln2_b), nullptr, "sg2n"),
+                     on));
       return smolgen_global(on);
     };
     if (L.smolgen && !d.fused_bias) {
