@@ -1348,8 +1348,12 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     const bool f8 = d.fp8_act && M >= 2048;
     // The no-allocation layout has one split-K buffer: the chain then runs
     // on the caller's stream (same kernels and splits, so the same bits).
-    hipStream_t sg_stream =
-        side_chain && !net->profiling && ws.Has("splitk_sg") ? net->side : st;
+    // The chain runs beside Q|K|V (its tiles then chosen to share CUs with
+    // Q|K|V's) whenever the layout has its split-K buffer; with the stage
+    // profiler on it runs on the main stream with the same tiles, so each
+    // launch is timed alone as the graph runs it.
+    const bool chain_beside = side_chain && ws.Has("splitk_sg");
+    hipStream_t sg_stream = chain_beside && !net->profiling ? net->side : st;
     mfh::AttentionParams ap;
     ap.qkv = ws.S<std::uint16_t>("qkv");
     ap.qkv_lo = ws.Lo("qkv");
@@ -1371,6 +1375,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
         mfh::GemmParams q = gemm(a, lda, w, ldw, m, n, k, bias, mfh::ACT_NONE, mode, C, C_lo,
                                  ldc);
         q.partials = sk;
+        // Beside Q|K|V: tiles small enough to share its CUs.
+        q.small_lds = chain_beside;
         return q;
       };
       // The shared global projection of the normalised dense2 rows into the
@@ -1452,6 +1458,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M,
                               3 * E + (L.smolgen && !side_chain ? d.C : 0), E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
                               ws.S<std::uint16_t>("qkv"), ws.Lo("qkv"), 3 * E);
+    pq.beside_chain = L.smolgen && chain_beside;
     if (L.smolgen && !side_chain) {
       pq.split_n = 3 * E;
       pq.C2 = ws.S<std::uint16_t>("comp");
