@@ -831,6 +831,11 @@ constexpr int kLargeRows = 1536;
 //   after a residual GEMM) also takes a two-way split up to 384 workgroups.
 // Measured forward (with the three-stage rings below): batch 1 1.29 ->
 // 1.20 ms, 2 1.43 -> 1.26, 4 1.58 -> 1.33, 8 1.62 -> 1.48, 12 1.79 -> 1.76.
+bool GemmWholeRoundTiles(const GemmParams &p) {
+  const long big_tiles = static_cast<long>((p.M + 255) / 256) * ((p.N + 255) / 256);
+  return p.M >= kLargeRows && p.N >= 128 && p.k_splits == 1 && big_tiles % 256 == 0 && !p.A8;
+}
+
 constexpr long kSplitMaxGroups = 256;
 constexpr long kSplitPairMaxGroups = 384;
 constexpr int kSplitMinSteps = 16;
@@ -987,7 +992,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   if (f8)
     return big_tiles % 256 == 0 ? LaunchW<256, 256, 64, 2, 4, 2, false, false, true>(p, stream)
                                 : LaunchW<128, 128, 64, 2, 2, 4, false, false, true>(p, stream);
-  if (large && p.k_splits == 1 && big_tiles % 256 == 0) {
+  if (GemmWholeRoundTiles(p)) {
     // fp8 weights too: their e4m3 rows share the ring (40 / 24 KiB stages).
     if (p.W8)
       return split ? LaunchW<256, 256, 32, 3, 4, 2, true, true>(p, stream)

@@ -1354,6 +1354,22 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // launch is timed alone as the graph runs it.
     const bool chain_beside = side_chain && ws.Has("splitk_sg");
     hipStream_t sg_stream = chain_beside && !net->profiling ? net->side : st;
+    mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M,
+                              3 * E + (L.smolgen && !side_chain ? d.C : 0), E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
+                              ws.S<std::uint16_t>("qkv"), ws.Lo("qkv"), 3 * E);
+    if (L.smolgen && !side_chain) {
+      pq.split_n = 3 * E;
+      pq.C2 = ws.S<std::uint16_t>("comp");
+      pq.C2_lo = ws.Lo("comp");
+      pq.ldc2 = d.C;
+    }
+    // Beside the chain, Q|K|V on whole-round 256 x 256 tiles takes two LDS
+    // stages and the chain's GEMMs 24 KiB tiles, which then fit on the CUs
+    // that hold Q|K|V workgroups.  Where Q|K|V takes 256 x 128 tiles (80
+    // KiB), the chain's usual tiles already fit beside them and are faster
+    // (24 KiB tiles there: batch 24 -1.6 %, 32 -1.1 %, 96 -1.4 %).
+    const bool share_cus = L.smolgen && chain_beside && mfh::GemmWholeRoundTiles(pq);
+    pq.beside_chain = share_cus;
     mfh::AttentionParams ap;
     ap.qkv = ws.S<std::uint16_t>("qkv");
     ap.qkv_lo = ws.Lo("qkv");
@@ -1375,8 +1391,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
         mfh::GemmParams q = gemm(a, lda, w, ldw, m, n, k, bias, mfh::ACT_NONE, mode, C, C_lo,
                                  ldc);
         q.partials = sk;
-        // Beside Q|K|V: tiles small enough to share its CUs.
-        q.small_lds = chain_beside;
+        q.small_lds = share_cus;
         return q;
       };
       // The shared global projection of the normalised dense2 rows into the
@@ -1454,16 +1469,6 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
         return rc;
       if (sg_stream != st)
         MFH_HIP_CHECK(hipEventRecord(net->fork_join[2 * li + 1], sg_stream));
-    }
-    mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M,
-                              3 * E + (L.smolgen && !side_chain ? d.C : 0), E, net->W<float>(L.qkv_b), mfh::ACT_NONE, mfh::GEMM_OUT_BF16,
-                              ws.S<std::uint16_t>("qkv"), ws.Lo("qkv"), 3 * E);
-    pq.beside_chain = L.smolgen && chain_beside;
-    if (L.smolgen && !side_chain) {
-      pq.split_n = 3 * E;
-      pq.C2 = ws.S<std::uint16_t>("comp");
-      pq.C2_lo = ws.Lo("comp");
-      pq.ldc2 = d.C;
     }
     if (f8) {
       MFH_RC(quant("act", E));

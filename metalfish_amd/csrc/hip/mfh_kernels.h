@@ -102,6 +102,10 @@ hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err)
 // k_splits set to this value instead.
 int GemmAutoSplits(const GemmParams &p, bool summed_by_consumer = false);
 
+// Whether LaunchGemm runs `p` (bf16 activations) on 256 x 256 tiles that
+// fill whole rounds of 256 workgroups.
+bool GemmWholeRoundTiles(const GemmParams &p);
+
 // Row-panel GEMM: one workgroup of eight waves owns 64 whole output rows
 // and a panel of 128 * TN columns (TN = 2, 4, 6 or 8), so a row's outputs
 // never leave the workgroup.  The activation panel goes through LDS (every
