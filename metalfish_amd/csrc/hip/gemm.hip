@@ -818,6 +818,13 @@ bool Aligned(const void *ptr, std::uintptr_t bytes) {
 // 2.34).
 constexpr int kLargeRows = 1536;
 
+// 256 x 256 tiles where they fill whole rounds of 256 workgroups (bf16
+// activations, one K slice, from the large-problem rows).
+bool GemmWholeRoundTiles(const GemmParams &p) {
+  const long big_tiles = static_cast<long>((p.M + 255) / 256) * ((p.N + 255) / 256);
+  return p.M >= kLargeRows && p.N >= 128 && p.k_splits == 1 && big_tiles % 256 == 0 && !p.A8;
+}
+
 // Split-K at few positions (64 x 64 tiles, K in 64-wide steps).  A GEMM
 // kernel here costs ~5 us however short its K loop, and a separate reduce
 // launch another ~4.5 us, so:
@@ -831,11 +838,6 @@ constexpr int kLargeRows = 1536;
 //   after a residual GEMM) also takes a two-way split up to 384 workgroups.
 // Measured forward (with the three-stage rings below): batch 1 1.29 ->
 // 1.20 ms, 2 1.43 -> 1.26, 4 1.58 -> 1.33, 8 1.62 -> 1.48, 12 1.79 -> 1.76.
-bool GemmWholeRoundTiles(const GemmParams &p) {
-  const long big_tiles = static_cast<long>((p.M + 255) / 256) * ((p.N + 255) / 256);
-  return p.M >= kLargeRows && p.N >= 128 && p.k_splits == 1 && big_tiles % 256 == 0 && !p.A8;
-}
-
 constexpr long kSplitMaxGroups = 256;
 constexpr long kSplitPairMaxGroups = 384;
 constexpr int kSplitMinSteps = 16;

@@ -80,12 +80,14 @@ struct GemmParams {
   // == 0, lda % 16 == 0, M >= 2048 rows.
   const std::uint8_t *A8 = nullptr;
   const float *ascale = nullptr;
-  // Tiles that leave room for a concurrent launch on another stream (split
-  // precision, bf16 weights).  beside_chain: whole-round 256 x 256 tiles
+  // Tiles that leave room for a concurrent launch on another stream (bf16
+  // weights).  beside_chain (split precision): whole-round 256 x 256 tiles
   // take two LDS stages (96 KiB) instead of three (144 KiB).  small_lds:
   // below the large-problem rows, 64 x 64 tiles over BK = 32 with two
-  // stages (24 KiB) instead of BK = 64 with three (72 KiB), so they fit on a
-  // CU beside a two-stage 256 x 256 tile.  Neither changes the result bits.
+  // stages (24 KiB split, 16 KiB single bf16) instead of BK = 64 with three
+  // (72 / 48 KiB), so they fit on a CU beside a two-stage split or a
+  // four-stage single-bf16 256 x 256 tile.  Neither changes the result
+  // bits (the K order of the MFMAs is the same).
   bool beside_chain = false;
   bool small_lds = false;
   // Set by LaunchGemm: every output row start allows 4-column vector stores
