@@ -33,6 +33,7 @@
 #include "mfh_kernels.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace mfh {
 namespace {
@@ -302,8 +303,269 @@ constexpr int GemmStageBytes() {
   return !W8 ? a + BN * BK * 2 : W8InLds<BM, BN, BK, WM, WN, SPLIT>() ? a + BN * BK : a;
 }
 
+// Software-pipelined main loop (bf16 weights, BK = 32): LDS fragment reads
+// for the next MFMAs are issued while earlier MFMAs run, so neither the LDS
+// latency nor the LDS pipe's time opens a gap in the MFMA stream.  In the
+// lock-step loop the compiler waited for each group of fragment reads just
+// before the MFMAs using them (five exposed LDS latencies per K step).
+//
+// Split precision (hi + lo activation planes): a K step runs as two halves,
+// the hi plane's MFMAs (TM x TN fragment pairs), then the lo plane's.
+// During the hi half the lo fragments of the step are read; during the lo
+// half the hi fragments of step k + 1 are read, and W_j of step k + 1 is
+// read into W_j's registers as soon as its last MFMA of step k is issued.
+// Nothing is double-buffered (256 x 256 tile: 128 accumulators + 16 + 16
+// activation + 32 weight registers).  Single bf16: the activation
+// fragments feed every MFMA of a step, so step k + 1's go into a second
+// set; the weight fragments roll the same way.
+//
+// One barrier per step, before the reads of stage k + 1 begin: this wave's
+// loads of stage k + 1 have landed (the loads of the ST - 2 later stages
+// may stay in flight), so the barrier makes stage k + 1 visible; and every
+// wave has waited for its reads of stage k, so that slot takes stage
+// k + ST right after the barrier.  The loop is rotated so that it begins
+// right after that barrier: the compiler's wait-count pass waits for every
+// outstanding LDS read where a loop begins, and there none is in flight.
+// Fragment i of activation plane q sits at a_off + (q BM + 16 i) BK
+// elements of a stage and weight fragment j at w_off + 16 j BK (the swizzle
+// of Swz repeats every 16 rows).
+// (The buffer-resource type exists only in the device pass.)
+#if defined(__HIP_DEVICE_COMPILE__)
+// Buffer resource over a whole operand (raw addressing: stride 0, byte
+// offsets below 2^31; the loads' offsets are clamped to valid rows, so the
+// range check never triggers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t BufferRsrc(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int STAGE>
+__device__ __forceinline__ void PipelinedLoop(const GemmParams &p, std::uint16_t *lds, int m0,
+                                              int n0, int k_begin, int KT,
+                                              f32x4 (&acc)[BM / WM / 16][BN / WN / 16]) {
+  static_assert(BK == 32, "one MFMA K step per LDS stage");
+  constexpr int NWAVES = WM * WN;
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int P = SPLIT ? 2 : 1;
+  constexpr int A_ROWS = P * BM;
+  constexpr int CPR = BK / 8, RPL = 64 / CPR;  // 16-byte chunks per row, rows per wave-load
+  constexpr int LPW = STAGE * 2 / 1024 / NWAVES;
+  static_assert(BM % RPL == 0 && BN % RPL == 0, "a wave-load stays inside one operand");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int fr = lane & 15, fc = lane >> 4;
+
+  // Global -> LDS loads of this wave: wave-load L covers rows L RPL ..
+  // L RPL + RPL - 1 of the stage (A rows, then A_lo rows, then W rows).
+  // They are MUBUF loads (buffer_load_dwordx4 ... lds): a buffer resource
+  // per operand, the lane's byte offset in a register and the K step's in
+  // a scalar one.  (The FLAT form, global_load_lds, counts as a possible
+  // LDS access for the compiler's wait-count pass, which then waits for
+  // every outstanding LDS read, lgkmcnt(0), wherever it waits for one.)
+  __amdgpu_buffer_rsrc_t rsrc[LPW];
+  unsigned goff[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int L = wave * LPW + j;
+    const int row = L * RPL + lane / CPR;
+    const int chunk = (lane % CPR) ^ ((row >> 1) & 3);
+    if (L * RPL < BM) {
+      rsrc[j] = BufferRsrc(p.A);
+      goff[j] = 2u * (static_cast<unsigned>(min(m0 + row, p.M - 1)) * p.lda + k_begin + chunk * 8);
+    } else if (SPLIT && L * RPL < 2 * BM) {
+      rsrc[j] = BufferRsrc(p.A_lo);
+      goff[j] = 2u * (static_cast<unsigned>(min(m0 + row - BM, p.M - 1)) * p.lda + k_begin +
+                      chunk * 8);
+    } else {
+      rsrc[j] = BufferRsrc(p.W);
+      goff[j] = 2u * (static_cast<unsigned>(min(n0 + row - A_ROWS, p.N - 1)) * p.ldw + k_begin +
+                      chunk * 8);
+    }
+  }
+  const int ldsw = __builtin_amdgcn_readfirstlane(wave * LPW * 512);  // elements
+  auto fill = [&](int s, int slot) {
+    std::uint16_t *d = lds + slot * STAGE + ldsw;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc[j], MFH_LDS_PTR(d + j * 512), 16, goff[j],
+                                               s * (BK * 2), 0, 0);
+  };
+
+  const int a_off = Swz<BK>(wm * (BM / WM) + fr, fc);
+  const int w_off = A_ROWS * BK + Swz<BK>(wn * (BN / WN) + fr, fc);
+  auto read_a = [&](bf16x8 (&a)[TM], const std::uint16_t *base, int q) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      a[i] = *reinterpret_cast<const bf16x8 *>(base + a_off + (q * BM + i * 16) * BK);
+  };
+  auto read_w = [&](bf16x8 &w, const std::uint16_t *base, int j) {
+    w = *reinterpret_cast<const bf16x8 *>(base + w_off + j * 16 * BK);
+  };
+  auto mfma_group = [&](const bf16x8 &w, const bf16x8 (&a)[TM], int j) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, a[i], acc[i][j], 0, 0, 0);
+  };
+  // s_waitcnt encodings (expcnt always left alone): vmcnt(kVmKeep) and
+  // lgkmcnt(0); vmcnt(0) and lgkmcnt(0); lgkmcnt(0) alone; the prologue's
+  // vmcnt(kPro) alone.
+  constexpr int kVmKeep = (ST - 2) * LPW;
+  constexpr int kPro = (ST - 1) * LPW;
+  static_assert(kPro < 64, "vmcnt holds at most 63");
+  constexpr int kWaitKeep = (kVmKeep & 15) | ((kVmKeep >> 4) << 14) | (7 << 4);
+  constexpr int kWaitAll = 7 << 4;
+  constexpr int kWaitLgkm = 0xC00F | (7 << 4);  // lgkmcnt(0) alone
+  constexpr int kWaitPro = (kPro & 15) | ((kPro >> 4) << 14) | (7 << 4) | (15 << 8);
+
+#pragma unroll
+  for (int s = 0; s < ST; ++s)
+    if (s < KT)
+      fill(s, s);
+  if (KT >= ST)
+    __builtin_amdgcn_s_waitcnt(kWaitPro);
+  else
+    __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_barrier" ::: "memory");
+  // Scalar loads (kernel arguments) share the LDS read counter and complete
+  // out of order; none may be pending once the fragment reads begin, or
+  // every wait on those reads becomes lgkmcnt(0).
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+
+  // Stage k + 1 visible, slot of stage k refilled with stage k + ST.
+  // (The lgkmcnt(0) wait is unconditional: a wait chosen between two
+  // branches leaves the wait-count pass a path with no wait at all, and it
+  // then waits for every read issued after the barrier.)
+  auto sync_next = [&](int k, int fslot) {
+    __builtin_amdgcn_s_waitcnt(kWaitKeep);
+    if (k + ST - 1 >= KT)
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+    asm volatile("s_barrier" ::: "memory");
+    if (k + ST < KT)
+      fill(k + ST, fslot);
+  };
+
+  bf16x8 w[TN];
+  // The last step reads nothing more: it is peeled off so that the steady
+  // loop's reads are unconditional and the wait counts stay exact.
+  using More = std::integral_constant<bool, true>;
+  using Last = std::integral_constant<bool, false>;
+  int cslot = 0;  // slot of stage k
+  if constexpr (SPLIT) {
+    // The loop is rotated so that its header follows the step's barrier,
+    // whose lgkmcnt(0) already drained the reads: an iteration is the lo
+    // half of step k (reading stage k + 1) and the hi half of step k + 1.
+    bf16x8 ahi[TM], alo[TM];
+    read_a(ahi, lds, 0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      read_w(w[j], lds, j);
+    // hi half of a step whose stage is `cur`: the step's lo fragments are
+    // read behind its first MFMA group.
+    auto hi_half = [&](const std::uint16_t *cur) {
+      mfma_group(w[0], ahi, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      read_a(alo, cur, 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 1; j < TN; ++j) {
+        mfma_group(w[j], ahi, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    // lo half: behind its first MFMA group the next step's hi fragments
+    // are read (the hi half has consumed this step's), and W_j of the next
+    // step rolls in behind its last MFMA.  (No read precedes the first
+    // group: the wait-count pass waits for every outstanding LDS read
+    // where the loop begins, and nothing is in flight there yet.)
+    auto lo_half = [&](auto tag, const std::uint16_t *nxt) {
+      constexpr bool more = decltype(tag)::value;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        mfma_group(w[j], alo, j);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (more) {
+          if (j == 0)
+            read_a(ahi, nxt, 0);
+          read_w(w[j], nxt, j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    hi_half(lds);
+    if (KT > 1)
+      sync_next(0, 0);
+    for (int k = 0; k + 2 < KT; ++k) {
+      const int nslot = cslot + 1 == ST ? 0 : cslot + 1;
+      const std::uint16_t *nxt = lds + nslot * STAGE;
+      lo_half(More(), nxt);
+      hi_half(nxt);
+      sync_next(k + 1, nslot);
+      cslot = nslot;
+    }
+    if (KT > 1) {
+      const int nslot = cslot + 1 == ST ? 0 : cslot + 1;
+      const std::uint16_t *nxt = lds + nslot * STAGE;
+      lo_half(More(), nxt);
+      hi_half(nxt);
+    }
+    lo_half(Last(), lds);
+  } else {
+    // Single bf16: the step's activation fragments feed every MFMA group,
+    // so the next step's go into a second set; the loop is rotated like
+    // the split one (an iteration is MFMA groups 1 .. TN-1 of step k,
+    // reading stage k + 1, then group 0 of step k + 1 and the barrier).
+    bf16x8 a[TM], an[TM];
+    read_a(a, lds, 0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      read_w(w[j], lds, j);
+    auto rest = [&](auto tag, const std::uint16_t *nxt) {
+      constexpr bool more = decltype(tag)::value;
+      // Nothing is in flight here (the barrier's wait drained the reads);
+      // saying so keeps the wait-count pass from draining mid-step.
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm);
+      if constexpr (more) {
+        read_a(an, nxt, 0);
+        read_w(w[0], nxt, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 1; j < TN; ++j) {
+        mfma_group(w[j], a, j);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (more)
+          read_w(w[j], nxt, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (more) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          a[i] = an[i];
+        mfma_group(w[0], a, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    mfma_group(w[0], a, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (KT > 1)
+      sync_next(0, 0);
+    for (int k = 0; k + 2 < KT; ++k) {
+      const int nslot = cslot + 1 == ST ? 0 : cslot + 1;
+      rest(More(), lds + nslot * STAGE);
+      sync_next(k + 1, nslot);
+      cslot = nslot;
+    }
+    if (KT > 1) {
+      const int nslot = cslot + 1 == ST ? 0 : cslot + 1;
+      rest(More(), lds + nslot * STAGE);
+    }
+    rest(Last(), lds);
+  }
+}
+#endif  // __HIP_DEVICE_COMPILE__
+
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8, bool F8 = false>
+          bool W8, bool F8 = false, bool PIPE = false>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -325,6 +587,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   // dimensions halved.
   static_assert(!F8 || (BK == 64 && !SPLIT && !W8), "fp8 activations: BK = 64 bytes pairs");
   static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
+  static_assert(!PIPE || (!W8 && !F8 && BK == 32), "pipelined loop: bf16 weights, BK = 32");
   static_assert(LOADS % NWAVES == 0, "stage loads must split evenly over waves");
   constexpr int LPW = LOADS / NWAVES;
   extern __shared__ __attribute__((aligned(1024))) std::uint16_t lds[];
@@ -417,10 +680,11 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       for (int j = 0; j < TN; ++j)
         wq[kk][j] = *reinterpret_cast<const u32x2 *>(wsrc[j] + kk * 32);
   }
-  // Stages 0 .. ST-2 in flight before the loop.
+  // Stages 0 .. ST-2 in flight before the loop (the pipelined loop issues
+  // its own).
 #pragma unroll
   for (int s = 0; s < ST - 1; ++s)
-    if (s < KT) {
+    if (!PIPE && s < KT) {
 #pragma unroll
       for (int j = 0; j < LPW; ++j)
         __builtin_amdgcn_global_load_lds(static_cast<const void *>(src[j] + s * kstep[j]),
@@ -435,6 +699,11 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     for (int j = 0; j < TN; ++j)
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  if constexpr (PIPE) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    PipelinedLoop<BM, BN, BK, ST, WM, WN, SPLIT, STAGE>(p, lds, m0, n0, k_begin, KT, acc);
+#endif
+  } else {
   int slot = 0;                       // kt % ST
   int fill = (ST - 1) % ST;           // (kt + ST - 1) % ST
   for (int kt = 0; kt < KT; ++kt) {
@@ -546,6 +815,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
           wq[kk][j] = wn_next[kk][j];
     }
   }
+  }  // PIPE / lock-step loop
 
   // fp8 activations: each row's quantisation scale (the weight row scale
   // follows in the epilogue).
@@ -734,11 +1004,11 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8 = false, bool F8 = false>
+          bool W8 = false, bool F8 = false, bool PIPE = false>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   constexpr size_t kLds =
       static_cast<size_t>(ST) * GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>();
-  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8>;
+  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8, PIPE>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&]() {
@@ -777,21 +1047,22 @@ hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_
 
 // Epilogue dispatch: the activations the network uses (none, mish) get
 // dedicated instances, anything else the runtime switch.
-template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8, bool F8 = false>
+template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8, bool F8 = false,
+          bool PIPE = false>
 hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
   if (p.k_splits > 1 || (p.out_mode == GEMM_OUT_F32 && p.act == ACT_NONE))
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8, F8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8, F8, PIPE>(p, stream);
   if (p.out_mode == GEMM_OUT_RESID_F32)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8, F8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8, F8, PIPE>(p, stream);
   if (p.out_mode == GEMM_OUT_F32)
     return p.act == ACT_MISH
-               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8, F8>(p, stream)
-               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8, F8>(p, stream);
+               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8, F8, PIPE>(p, stream)
+               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8, F8, PIPE>(p, stream);
   if (p.act == ACT_NONE)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8, F8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8, F8, PIPE>(p, stream);
   if (p.act == ACT_MISH)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8, F8>(p, stream);
-  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8, F8>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8, F8, PIPE>(p, stream);
+  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8, F8, PIPE>(p, stream);
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
@@ -1004,10 +1275,15 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     // a round of these tiles to end (batch 256 forward 23.01k -> 23.55k
     // positions/s with the chain on small-LDS tiles; two stages alone
     // 23.15k, batch 1024 unchanged).
+    // bf16 weights: the software-pipelined main loop (PipelinedLoop).
+    // Isolated at batch 256, split precision: Q|K|V 223 -> 209 us, the
+    // out-projection 76.7 -> 70.7, FFN2 103.8 -> 93.6; single bf16 Q|K|V
+    // 112 -> 104; the batch-256 forward 23.15k -> 23.64k positions/s
+    // (bit-equal outputs: the MFMAs accumulate in the same order).
     if (p.beside_chain && split)
-      return LaunchW<256, 256, 32, 2, 4, 2, true, false>(p, stream);
-    return split ? LaunchW<256, 256, 32, 3, 4, 2, true, false>(p, stream)
-                 : LaunchW<256, 256, 32, 4, 4, 2, false, false>(p, stream);
+      return LaunchW<256, 256, 32, 2, 4, 2, true, false, false, true>(p, stream);
+    return split ? LaunchW<256, 256, 32, 3, 4, 2, true, false, false, true>(p, stream)
+                 : LaunchW<256, 256, 32, 4, 4, 2, false, false, false, true>(p, stream);
   }
   // Split precision with fewer 128 x 128 tiles than CUs (the out-projection
   // and FFN at M = 2048 .. 3072): 64 x 64 tiles, four times the workgroups
@@ -1033,7 +1309,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       const long t256 = static_cast<long>((p.M + 255) / 256) * ((p.N + 127) / 128);
       if ((t256 >= 256 || p.M <= 2048) &&
           9 * ((t256 + 255) / 256) < 5 * ((tiles128 + 255) / 256))
-        return LaunchW<256, 128, 32, 2, 4, 2, true, false>(p, stream);
+        return LaunchW<256, 128, 32, 2, 4, 2, true, false, false, true>(p, stream);
     }
     // Split precision with fp8 weights: BK = 64, whose stage holds the
     // e4m3 rows in LDS (at BK = 32 the 128 x 128 stage does not split
@@ -1042,7 +1318,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       return split ? (p.W8 ? Launch<128, 128, 64, 2, 2, 4, true>(p, stream)
                            : Launch<128, 128, 32, 2, 2, 4, true>(p, stream))
              : p.W8 ? Launch<256, 128, 32, 2, 4, 2, false>(p, stream)
-                    : LaunchW<256, 128, 32, 3, 4, 2, false, false>(p, stream);
+                    : LaunchW<256, 128, 32, 3, 4, 2, false, false, false, true>(p, stream);
     return split ? Launch<64, 128, 64, 2, 2, 2, true>(p, stream)
                  : Launch<128, 128, 64, 2, 2, 2, false>(p, stream);
   }
