@@ -463,6 +463,7 @@ def main():
         # Q|K|V, out-projection and FFN GEMMs on the fp8 MFMA.  Measured below
         # the parity gates on the random-init net (top-1 0.79-0.83 against
         # the oracle), so it is reported beside config 5, never as its value.
+        os.environ["METALFISH_HIP_EXPERIMENTAL_FP8"] = "1"
         r8 = Runner(backend, torch, np, spec, fweights, masks, values, fb, "fp8", stream,
                     weights_dtype="fp8")
         ms8 = r8.time_steps(fb, max(3, args.steps // 4), 2)

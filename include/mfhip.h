@@ -73,7 +73,13 @@ enum { MFH_WEIGHTS_BF16 = 0, MFH_WEIGHTS_FP8 = 1 };
  * FP8 (needs MFH_WEIGHTS_FP8): from 2048 token rows (32 positions) up, the
  * Q|K|V, out-projection and FFN GEMMs of the encoder layers run on the fp8
  * MFMA, their inputs quantised per row to OCP e4m3 (scale max|row| / 448)
- * just before each GEMM; everything else as in BF16. */
+ * just before each GEMM; everything else as in BF16.
+ * FP8 is EXPERIMENTAL and does not meet the parity gates against the fp32
+ * CPU backend: on the random-init BT4-shape net, same top-1 move on ~80 % of
+ * positions, policy max-abs ~0.15, WDL ~1e-2 (the gates are 99.5 %, 2e-2
+ * and 5e-3).  mfh_net_create refuses it (MFH_ERR_UNSUPPORTED) unless the
+ * environment sets METALFISH_HIP_EXPERIMENTAL_FP8=1.  For e4m3 weights
+ * within the gates use MFH_WEIGHTS_FP8 with BF16X2. */
 enum {
   MFH_PRECISION_BF16 = 0,
   MFH_PRECISION_BF16X2 = 1,

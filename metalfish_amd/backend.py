@@ -494,7 +494,9 @@ def create_network(spec, weights, max_batch=256, device=-1, precision="bf16x2",
                    weights_dtype="bf16", fused_layernorm=False):
     """HipNetwork for a synth.NetSpec and its weights.  ``precision`` is
     "bf16x2" (split activations, default: meets every parity gate),
-    "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput);
+    "bf16x2_gemm" or "bf16" (single-pass, twice the MFMA throughput), or
+    "fp8" (e4m3 activations; experimental, below the parity gates, refused
+    unless METALFISH_HIP_EXPERIMENTAL_FP8=1);
     ``weights_dtype`` "bf16" or "fp8" (e4m3 with per-row scales);
     ``fused_layernorm`` selects the row-panel residual GEMM + LayerNorm."""
     return HipNetwork(weights, spec.heads, wdl=spec.wdl, moves_left=spec.moves_left_dim > 0,

@@ -1109,8 +1109,7 @@ bool GemmWholeRoundTiles(const GemmParams &p) {
 //   after a residual GEMM) also takes a two-way split up to 384 workgroups.
 // Measured forward (with the three-stage rings below): batch 1 1.29 ->
 // 1.20 ms, 2 1.43 -> 1.26, 4 1.58 -> 1.33, 8 1.62 -> 1.48, 12 1.79 -> 1.76.
-constexpr long kSplitMaxGroups = 256;
-constexpr long kSplitPairMaxGroups = 384;
+// (kSplitMaxGroups and kSplitPairMaxGroups are in mfh_kernels.h.)
 constexpr int kSplitMinSteps = 16;
 constexpr int kSplitMinParts = 4;
 

@@ -559,6 +559,14 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
                         "the FP8 precision needs embedding and FFN widths that are "
                         "multiples of 128 up to 2048");
     }
+    // e4m3 activations move near-tied policy logits (top-1 ~80 % against
+    // the fp32 CPU backend on the random-init BT4 net, policy max-abs
+    // ~0.15): below the parity gates, so a caller has to ask for it.
+    const char *fp8_env = std::getenv("METALFISH_HIP_EXPERIMENTAL_FP8");
+    if (!(fp8_env && fp8_env[0] == '1'))
+      return SetError(MFH_ERR_UNSUPPORTED,
+                      "the FP8 precision is experimental and below the parity gates; "
+                      "set METALFISH_HIP_EXPERIMENTAL_FP8=1 to use it");
   }
   return MFH_OK;
 }
@@ -745,10 +753,15 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
 
 // fp32 scratch for the split-K partials LaunchGemm may use on small batches.
 constexpr size_t kSplitKFloats = size_t(8) << 20;
-// What those partials can need at most: LaunchGemm splits K only while the
-// 64 x 64 tiles times the slices stay within 512 workgroups, so the slices
-// of one GEMM hold at most 512 * 64 * 64 floats.
+// The no-allocation layout's partials buffer.  GemmAutoSplits splits K only
+// while the 64 x 64 tiles times the slices stay within kSplitMaxGroups
+// (kSplitPairMaxGroups for a split the LayerNorm sums) workgroups, so a
+// split GEMM's partials fit in this buffer as they fit in kSplitKFloats, and
+// both layouts take the same splits (the same bits).
 constexpr size_t kSmallSplitKFloats = size_t(512) * 64 * 64;
+static_assert(kSmallSplitKFloats >= size_t(mfh::kSplitPairMaxGroups) * 64 * 64 &&
+                  kSmallSplitKFloats >= size_t(mfh::kSplitMaxGroups) * 64 * 64,
+              "no-allocation partials must hold the largest automatic split");
 // Largest batch the no-allocation entry point takes (below 2048 token rows).
 // That entry point runs the smolgen chain on the caller's stream, so its
 // layout needs no second partials buffer.
@@ -858,8 +871,25 @@ void PlanWorkspace(mfh_net *net) {
   net->ws_bytes = PlanLayout(net->d, net->max_batch, kSplitKFloats, net->d.smolgen, net->ws_off);
   // The no-allocation entry point's layout in the scratch array: the largest
   // single-stream batch whose workspace fits.
+  // The limit stays below the first batch whose Q|K|V would take whole-round
+  // 256 x 256 tiles: beside the side-stream smolgen chain those tiles (and
+  // the chain's) are chosen to share CUs, which the single-stream
+  // no-allocation forward does not do, so its bits could differ from
+  // mfh_net_eval_device's.  (For the nets here the first such batch is far
+  // above the limit.)
+  int limit = std::min(net->max_batch, kNoAllocMaxBatch);
+  for (int b = 1; b <= limit; ++b) {
+    mfh::GemmParams q;
+    q.M = b * kSquares;
+    q.N = 3 * net->d.E;
+    q.K = net->d.E;
+    if (mfh::GemmWholeRoundTiles(q)) {
+      limit = b - 1;
+      break;
+    }
+  }
   net->noalloc_max_batch = 0;
-  for (int b = std::min(net->max_batch, kNoAllocMaxBatch); b >= 1; --b) {
+  for (int b = limit; b >= 1; --b) {
     const size_t bytes = PlanLayout(net->d, b, kSmallSplitKFloats, false, net->noalloc_off);
     if (bytes <= kScratchBytes) {
       net->noalloc_max_batch = b;
@@ -2335,6 +2365,10 @@ int mfh_debug_encoder_layer(mfh_net *net, int batch, int layer, int iterations,
   rc = BeginUse(net, st);
   if (rc != MFH_OK)
     return rc;
+  // The copies below are synchronous on the null stream, which does not wait
+  // for a non-blocking caller stream: wait for the last call's device work
+  // on the workspace first.
+  MFH_HIP_CHECK(hipEventSynchronize(net->last_use));
   // The layer's input: the residual stream's bf16 planes and, in single
   // precision, its fp32 copy.
   MFH_HIP_CHECK(hipMemcpy(ws.S<std::uint16_t>("act"), x, n * 2, hipMemcpyHostToDevice));

@@ -103,6 +103,12 @@ hipError_t LaunchGemm(const GemmParams &p, hipStream_t stream, std::string *err)
 // after a residual GEMM) passes summed_by_consumer and launches with
 // k_splits set to this value instead.
 int GemmAutoSplits(const GemmParams &p, bool summed_by_consumer = false);
+// Workgroup limits of those splits (64 x 64 tiles times slices): slices that
+// need a reduce launch, and the two-way split a consumer sums.  The partials
+// of one split GEMM therefore hold at most kSplitPairMaxGroups * 64 * 64
+// floats.
+constexpr long kSplitMaxGroups = 256;
+constexpr long kSplitPairMaxGroups = 384;
 
 // Whether LaunchGemm runs `p` (bf16 activations) on 256 x 256 tiles that
 // fill whole rounds of 256 workgroups.

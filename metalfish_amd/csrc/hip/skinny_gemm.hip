@@ -334,6 +334,8 @@ int SkinnyNt(int N) { return N > 4096 ? 2 : 1; }
 
 
 bool Aligned16(const void *ptr) { return (reinterpret_cast<std::uintptr_t>(ptr) & 15) == 0; }
+// Null, or 8-byte aligned (the u32x2 stores and loads of bf16 planes).
+bool Aligned8OrNull(const void *ptr) { return (reinterpret_cast<std::uintptr_t>(ptr) & 7) == 0; }
 
 template <int NT, bool LN>
 hipError_t LaunchSkinnyVariant(const SkinnyParams &p, hipStream_t stream) {
@@ -395,6 +397,9 @@ hipError_t LaunchSkinnyGemm(const SkinnyParams &p, hipStream_t stream, std::stri
     if (p.ldc % 4 || (p.split_n < p.N && (p.split_n % 16 || !p.C2 || p.ldc2 % 4)) ||
         p.stats_out)
       return fail("bf16 output (ldc % 4 == 0, split_n % 16 == 0, no statistics)");
+    if (!Aligned8OrNull(p.C) || !Aligned8OrNull(p.C_lo) || !Aligned8OrNull(p.C2) ||
+        !Aligned8OrNull(p.C2_lo))
+      return fail("bf16 output planes must be 8-byte aligned");
   } else if (p.out_mode == SKINNY_OUT_F32 || p.out_mode == SKINNY_OUT_RESID) {
     if (!Aligned16(p.C) || p.ldc % 4 || p.split_n < p.N)
       return fail("fp32 output (16-byte aligned, ldc % 4 == 0, no column split)");
@@ -402,6 +407,10 @@ hipError_t LaunchSkinnyGemm(const SkinnyParams &p, hipStream_t stream, std::stri
         ((!p.resid && !p.resid16) || (p.resid && p.resid16) || (p.resid16 && !p.resid16_lo) ||
          p.ldr % 4))
       return fail("residual (fp32 or hi + lo planes, ldr % 4 == 0)");
+    if (p.out_mode == SKINNY_OUT_RESID &&
+        ((p.resid && !Aligned16(p.resid)) || !Aligned8OrNull(p.resid16) ||
+         !Aligned8OrNull(p.resid16_lo)))
+      return fail("residual alignment (fp32 16 bytes, bf16 planes 8 bytes)");
   } else {
     return fail("output mode");
   }

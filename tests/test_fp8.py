@@ -10,6 +10,13 @@ import pytest
 from metalfish_amd import backend, synth
 
 
+@pytest.fixture(autouse=True)
+def _experimental_fp8(monkeypatch):
+    """The FP8 precision is below the parity gates, so mfh_net_create takes
+    it only on explicit request; these tests make that request."""
+    monkeypatch.setenv("METALFISH_HIP_EXPERIMENTAL_FP8", "1")
+
+
 def _finite_table():
     vals = []
     for c in range(0x7F):  # positive codes, 0x7F is NaN
@@ -165,6 +172,18 @@ def test_fp8_precision_needs_fp8_weights():
     weights = synth.make_weights(spec, seed=0)
     with pytest.raises(RuntimeError, match="FP8 precision needs FP8"):
         backend.create_network(spec, weights, max_batch=4, device=-1, precision="fp8")
+
+
+def test_fp8_precision_needs_explicit_request(monkeypatch):
+    """Without METALFISH_HIP_EXPERIMENTAL_FP8=1 the FP8 precision is refused
+    at creation with a message that says why; e4m3 weights with the bf16x2
+    precision need no request."""
+    monkeypatch.delenv("METALFISH_HIP_EXPERIMENTAL_FP8")
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=0, fp8=True)
+    with pytest.raises(RuntimeError, match="experimental and below the parity gates"):
+        backend.create_network(spec, weights, max_batch=4, device=-1, precision="fp8",
+                               weights_dtype="fp8")
 
 
 def _e4m3_decode(codes):

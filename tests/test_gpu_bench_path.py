@@ -6,7 +6,7 @@
   all 256 distinct seeded positions the bench uses (its inputs:
   ``synth.playout_positions(256, seed=0)``) and hold every precision to the
   north_star gates against the CPU oracle, run on this host's cores.
-* Graph replays at batches 24, 32, 40 and 256 with a different position set
+* Graph replays at batches 8, 24, 32, 40 and 256 with a different position set
   between replays, through both ``mfh_net_eval_device`` (caller's buffers
   and stream) and ``mfh_net_eval`` (the net's pinned staging): every replay
   equals the eager forward of the same inputs bit for bit and meets the
@@ -125,11 +125,13 @@ def test_config2_gate_all_256_positions(bt4, precision):
            f"config 2, {precision}, {B} distinct positions")
 
 
-@pytest.mark.parametrize("batch", [24, 32, 40, 256])
+@pytest.mark.parametrize("batch", [8, 24, 32, 40, 256])
 def test_graph_replay_with_changing_inputs(bt4, batch):
-    """Graph replays of the BT4 forward (smolgen chain on the second stream
-    from 1088 token rows, i.e. all four batches; 24 positions = 1536 rows,
-    the fewest that take the large-M GEMM tiles) with a different position
+    """Graph replays of the BT4 forward (batch 8, config 3's MCTS batch:
+    512 token rows, where the out-projection and FFN2 take the two-way
+    split-K whose partials the LayerNorm sums; smolgen chain on the second
+    stream from 1088 token rows; 24 positions = 1536 rows, the fewest that
+    take the large-M GEMM tiles) with a different position
     set before every call, through mfh_net_eval_device and mfh_net_eval,
     with another batch size run in between: each call equals the eager
     forward of its inputs bit for bit and meets the gates."""

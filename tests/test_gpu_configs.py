@@ -1,0 +1,287 @@
+"""GPU parity of the configurations bench.py reports beside the headline.
+
+* Config 5: the BT4-shape net with e4m3 weights (per-row scales) and bf16x2
+  activations at batch 1024, the batch bench.py's ``fp8_weights`` line times.
+  Its 1024 slots are the 256 distinct bench positions four times over, as
+  bench.py fills them.  It runs through ``mfh_net_eval_device`` (eager run,
+  graph capture, two replays, all bit-equal), every slot meets the gates
+  against the CPU oracle on the same dequantised weights, and the four
+  copies of each position agree bit for bit (each row's arithmetic does not
+  depend on its slot).  At 65,536 token rows the Q|K|V and FFN1 GEMMs take
+  the whole-round 256 x 256 e4m3-weight tiles and the residual GEMMs the
+  row-panel kernel with the fused LayerNorm.
+* Config 4: one encoder layer alone (``mfh_debug_encoder_layer``, the
+  microbenchmark bench.py's ``encoder_layer`` line times) in single bf16 at
+  batches 256 and 1024 on bf16 N(0, 1) inputs, checked stage by stage
+  against float64 numpy on sampled positions.  Each stage's reference starts
+  from the GPU's own input to that stage (the debug tensors "qkv", "ctx",
+  "hid", "pre", "body", "act"), so each tolerance covers one stage's
+  rounding: Q|K|V against x.W^T + b; the attention context against the
+  smolgen chain and softmax recomputed from x and the GPU's Q|K|V; the FFN
+  hidden rows against LayerNorm 1 of the out-projection residual; the FFN2
+  residual sum; LayerNorm 2.  A whole-layer float64 forward from x alone is
+  checked too, with a bound for the layer's compounded bf16 rounding.
+
+Gates: policy logits max-abs <= 2e-2 and the same top-1
+legal move on >= 99.5 % of positions; WDL max-abs <= 5e-3
+(tools/compare_nn_backend_outputs.py:21-22 in the reference).
+"""
+
+import os
+import time
+
+import numpy as np
+import pytest
+
+import gpu_util
+import oracle
+from metalfish_amd import backend, synth
+
+pytestmark = pytest.mark.gpu
+
+POLICY_TOL = 2e-2
+WDL_TOL = 5e-3
+TOP1_GATE = 0.995
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if backend.device_count() < 1:
+        pytest.fail("GPU tests need an MI355X; none visible")
+
+
+def _top1(pol, ref_pol, legal):
+    agree = 0
+    for i in range(pol.shape[0]):
+        idx = legal[i][legal[i] >= 0]
+        agree += int(idx[np.argmax(pol[i, idx])] == idx[np.argmax(ref_pol[i, idx])])
+    return agree / pol.shape[0]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+@pytest.mark.timeout(900)
+def test_config5_fp8_weights_batch_1024():
+    """Config 5 as bench.py runs it: e4m3 weights, bf16x2 activations,
+    batch 1024 from the 256 bench positions repeated, mfh_net_eval_device
+    with graph replay."""
+    spec = synth.SPECS["bt4"]
+    weights = synth.make_weights(spec, seed=0, fp8=True)
+    n, B = 256, 1024
+    planes, legal = synth.playout_positions(n, seed=0)
+    threads = min(16, os.cpu_count() or 1)
+    t0 = time.time()
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads),
+                           weights).evaluate_batch(planes, threads=threads)
+    print(f"oracle: {n} fp8-weight BT4 positions on {threads} threads in "
+          f"{time.time() - t0:.1f} s", flush=True)
+    masks, values = backend.pack_planes(planes)
+    idx = np.arange(B) % n
+    net = backend.create_network(spec, weights, max_batch=B, device=0, weights_dtype="fp8",
+                                 precision="bf16x2")
+    assert "fp8" in net.info() or "e4m3" in net.info(), net.info()
+    dev = gpu_util.DeviceBuffers()
+    stream = dev.stream()
+    pol0 = np.zeros((B, 1858), np.float32)
+    wdl0 = np.zeros((B, 3), np.float32)
+    d_m, d_v = dev.put(masks[idx]), dev.put(values[idx])
+    d_p, d_w = dev.put(pol0), dev.put(wdl0)
+    runs = []
+    for _ in range(4):  # eager warm-up, capture + launch, two replays
+        net.eval_device(B, d_m, d_v, d_p, d_w, stream=stream)
+        dev.sync(stream)
+        runs.append((dev.get(d_p, pol0), dev.get(d_w, wdl0)))
+    dev.free()
+    net.close()
+    for pol, wdl in runs[1:]:
+        assert np.array_equal(_bits(pol), _bits(runs[0][0]))
+        assert np.array_equal(_bits(wdl), _bits(runs[0][1]))
+    pol, wdl = runs[-1]
+    for r in range(1, B // n):  # each position's four slots
+        assert np.array_equal(_bits(pol[r * n:(r + 1) * n]), _bits(pol[:n])), r
+        assert np.array_equal(_bits(wdl[r * n:(r + 1) * n]), _bits(wdl[:n])), r
+    perr = float(np.abs(pol - ref["policy"][idx]).max())
+    werr = float(np.abs(wdl - ref["wdl"][idx]).max())
+    top1 = _top1(pol, ref["policy"][idx], legal[idx])
+    print(f"config 5, batch {B}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} "
+          f"top-1 {top1:.4f}", flush=True)
+    assert perr <= POLICY_TOL and werr <= WDL_TOL and top1 >= TOP1_GATE
+
+
+# ---- Config 4: one encoder layer against float64 ------------------------
+
+S = 64
+
+
+def _bf16_bits(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _f64(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _bf16r(x):
+    """Round float64 values to bf16 (through fp32, nearest even)."""
+    return _f64(_bf16_bits(np.asarray(x, np.float64).astype(np.float32)))
+
+
+def _ln(x, g, b, eps):
+    m = x.mean(-1, keepdims=True)
+    v = (x * x).mean(-1, keepdims=True) - m * m
+    return (x - m) / np.sqrt(np.maximum(v, 0.0) + eps) * g + b
+
+
+def _mish(x):
+    return x * np.tanh(np.log1p(np.exp(x)))
+
+
+def _swish(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def _softmax(x):
+    e = np.exp(x - x.max(-1, keepdims=True))
+    return e / e.sum(-1, keepdims=True)
+
+
+class _Layer:
+    """Float64 copies of encoder layer 0's weights (bf16-valued)."""
+
+    def __init__(self, weights, spec):
+        p = "body.encoder.0."
+        g = lambda n: weights[p + n].astype(np.float64)  # noqa: E731
+        self.E, self.H = spec.embedding, spec.heads
+        self.wqkv = np.concatenate([g("mha.q_w"), g("mha.k_w"), g("mha.v_w")])
+        self.bqkv = np.concatenate([g("mha.q_b"), g("mha.k_b"), g("mha.v_b")])
+        self.wo, self.bo = g("mha.dense_w"), g("mha.dense_b")
+        self.w1, self.b1 = g("ffn.dense1_w"), g("ffn.dense1_b")
+        self.w2, self.b2 = g("ffn.dense2_w"), g("ffn.dense2_b")
+        self.g1, self.be1 = g("ln1_gammas"), g("ln1_betas")
+        self.g2, self.be2 = g("ln2_gammas"), g("ln2_betas")
+        sg = "mha.smolgen."
+        self.wc = g(sg + "compress")
+        self.sd1, self.sb1 = g(sg + "dense1_w"), g(sg + "dense1_b")
+        self.sd2, self.sb2 = g(sg + "dense2_w"), g(sg + "dense2_b")
+        self.sg1, self.sbe1 = g(sg + "ln1_gammas"), g(sg + "ln1_betas")
+        self.sg2, self.sbe2 = g(sg + "ln2_gammas"), g(sg + "ln2_betas")
+        self.wg = weights["body.smolgen_w"].astype(np.float64)
+        self.alpha = (2.0 * spec.layers) ** -0.25
+        self.eps = 1e-3  # PE_DENSE body (network_execution_plan.cpp:1164-1193)
+
+    def smolgen_bias(self, x, emulate):
+        """[H, 64, 64] bias of one position's rows x [64, E]; `emulate`
+        rounds to bf16 where the single-bf16 forward stores bf16."""
+        r = _bf16r if emulate else (lambda v: v)
+        comp = r(x @ self.wc.T).reshape(-1)
+        h1 = r(_ln(_swish(comp @ self.sd1.T + self.sb1), self.sg1, self.sbe1, 1e-3))
+        h2 = r(_ln(_swish(h1 @ self.sd2.T + self.sb2), self.sg2, self.sbe2, 1e-3))
+        return r(h2.reshape(self.H, -1) @ self.wg.T).reshape(self.H, S, S)
+
+    def attention(self, qkv, bias, emulate):
+        E, H = self.E, self.H
+        q, k, v = (qkv[:, i * E:(i + 1) * E].reshape(S, H, -1).transpose(1, 0, 2)
+                   for i in range(3))
+        s = q @ k.transpose(0, 2, 1) / np.sqrt(q.shape[-1]) + bias
+        p = _softmax(s)
+        if emulate:
+            p = _bf16r(p)
+        return (p @ v).transpose(1, 0, 2).reshape(S, E)
+
+    def forward(self, x):
+        """Whole layer in float64 from x alone (no bf16 rounding)."""
+        qkv = x @ self.wqkv.T + self.bqkv
+        ctx = self.attention(qkv, self.smolgen_bias(x, False), False)
+        y = _ln(x + self.alpha * (ctx @ self.wo.T + self.bo), self.g1, self.be1, self.eps)
+        f = _mish(y @ self.w1.T + self.b1) @ self.w2.T + self.b2
+        return _ln(y + self.alpha * f, self.g2, self.be2, self.eps)
+
+
+def _close(got, ref, rel, abs_frac, what, outliers=0.0, cap=None):
+    """|got - ref| <= rel |ref| + abs_frac max|ref| everywhere, or on all but
+    a fraction `outliers` of the elements, which stay within `cap`."""
+    err = np.abs(got - ref)
+    bound = rel * np.abs(ref) + abs_frac * np.abs(ref).max()
+    over = err > bound
+    print(f"  {what}: max-abs {err.max():.3e} mean-abs {err.mean():.3e} "
+          f"(max |ref| {np.abs(ref).max():.3g}), {int(over.sum())} of {err.size} over the "
+          f"bound", flush=True)
+    assert over.mean() <= outliers, (what, float(err.max()), int(over.sum()))
+    if outliers:
+        assert err.max() <= cap, (what, float(err.max()))
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("batch", [256, 1024])
+def test_config4_encoder_layer_against_fp64(batch):
+    """The encoder-layer microbenchmark's forward (single bf16, x ~ N(0, 1)
+    bf16, layer 0 of the BT4-shape net, as bench.py runs it) stage by stage
+    against float64 on six positions spread over the batch."""
+    spec = synth.SPECS["bt4"]
+    weights = synth.make_weights(spec, seed=0)
+    E, F = spec.embedding, spec.ffn
+    B, M = batch, batch * S
+    rng = np.random.default_rng(0)
+    x = _bf16_bits(rng.standard_normal((M, E), dtype=np.float32))
+    net = backend.create_network(spec, weights, max_batch=B, device=0, precision="bf16")
+    net.set_graphs(False)
+    net.encoder_layer_ms(B, 0, 1, x)
+    qkv = net.debug_tensor("qkv", (M, 3 * E), np.uint16)
+    ctx = net.debug_tensor("ctx", (M, E), np.uint16)
+    hid = net.debug_tensor("hid", (M, F), np.uint16)
+    pre = net.debug_tensor("pre", (M, E), np.float32)
+    body = net.debug_tensor("body", (M, E), np.float32)
+    act = net.debug_tensor("act", (M, E), np.uint16)
+    net.close()
+    L = _Layer(weights, spec)
+    positions = sorted({0, 1, B // 3, B // 2 + 5, B - 2, B - 1})
+    print(f"batch {B}: positions {positions}", flush=True)
+    st = {k: [] for k in ("qkv", "qkv_ref", "ctx", "ctx_ref", "hid", "hid_ref", "pre",
+                          "pre_ref", "body", "body_ref", "act", "e2e")}
+    for p in positions:
+        rows = slice(p * S, (p + 1) * S)
+        x64 = _f64(x[rows])
+        q_gpu = _f64(qkv[rows])
+        st["qkv"].append(q_gpu)
+        st["qkv_ref"].append(x64 @ L.wqkv.T + L.bqkv)
+        c_gpu = _f64(ctx[rows])
+        st["ctx"].append(c_gpu)
+        st["ctx_ref"].append(L.attention(q_gpu, L.smolgen_bias(x64, True), True))
+        y = _ln(x64 + L.alpha * (c_gpu @ L.wo.T + L.bo), L.g1, L.be1, L.eps)
+        h_gpu = _f64(hid[rows])
+        st["hid"].append(h_gpu)
+        st["hid_ref"].append(_mish(_bf16r(y) @ L.w1.T + L.b1))
+        st["pre"].append(pre[rows].astype(np.float64))
+        st["pre_ref"].append(y + L.alpha * (h_gpu @ L.w2.T + L.b2))
+        out_ref = _ln(pre[rows].astype(np.float64), L.g2, L.be2, L.eps)
+        st["body"].append(body[rows].astype(np.float64))
+        st["body_ref"].append(out_ref)
+        st["act"].append(_f64(act[rows]))
+        st["e2e"].append(L.forward(x64))
+    cat = {k: np.concatenate(v) for k, v in st.items()}
+    # bf16 outputs: half an ulp (2^-9 relative) of rounding plus fp32
+    # summation order and rare rounding-boundary flips of bf16 inputs.
+    _close(cat["qkv"], cat["qkv_ref"], 2 ** -8, 1e-4, "Q|K|V")
+    # The context: rounding flips of the stored bf16 smolgen bias (the fp32
+    # sum and the float64 one on either side of a bf16 rounding boundary, one
+    # ulp = 2^-8 of a bias up to ~5) move a query's probabilities by up to
+    # ~1 %, i.e. one head's 32 context values by up to ~1e-2: a few hundred
+    # of the 393,216 values checked may exceed the tight bound.  A wrong
+    # head, scale or bias layout moves most of them.
+    _close(cat["ctx"], cat["ctx_ref"], 2 ** -8, 2e-3, "attention context", outliers=1e-3,
+           cap=3e-2)
+    assert np.abs(cat["ctx"] - cat["ctx_ref"]).mean() <= 1e-3
+    _close(cat["hid"], cat["hid_ref"], 2 ** -8, 2e-3, "FFN hidden")
+    _close(cat["pre"], cat["pre_ref"], 0.0, 1e-5, "FFN2 residual sum")
+    _close(cat["body"], cat["body_ref"], 0.0, 1e-5, "LayerNorm 2 (fp32)")
+    _close(cat["act"], cat["body_ref"], 2 ** -8, 1e-6, "LayerNorm 2 (bf16)")
+    # The whole layer from x alone: the bf16 rounding of the stored Q|K|V,
+    # smolgen rows, bias, probabilities, context and FFN input, applied to a
+    # float64 forward, moves the output by up to ~5e-3 (mean ~7e-4).
+    e2e = np.abs(cat["body"] - cat["e2e"])
+    print(f"  layer vs float64 from x: max-abs {e2e.max():.3e} mean-abs {e2e.mean():.3e}",
+          flush=True)
+    assert e2e.mean() <= 3e-3 and e2e.max() <= 3e-2
