@@ -53,7 +53,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=256)
-    ap.add_argument("--precision", choices=["bf16x2", "bf16x2_gemm", "bf16"], default="bf16x2")
+    ap.add_argument("--precision", choices=["bf16x2", "bf16x2_fp8lo", "bf16x2_gemm", "bf16"],
+                    default="bf16x2")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--latency-iters", type=int, default=200)
     ap.add_argument("--small-batches", default="1,8,32,64")

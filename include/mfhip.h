@@ -80,11 +80,22 @@ enum { MFH_WEIGHTS_BF16 = 0, MFH_WEIGHTS_FP8 = 1 };
  * and 5e-3).  mfh_net_create refuses it (MFH_ERR_UNSUPPORTED) unless the
  * environment sets METALFISH_HIP_EXPERIMENTAL_FP8=1.  For e4m3 weights
  * within the gates use MFH_WEIGHTS_FP8 with BF16X2. */
+/* BF16X2_FP8LO: BF16X2 with the lo parts of the encoder layers' dense-layer
+ * inputs (Q|K|V, out-projection, FFN1, FFN2) carried as OCP e4m3 codes of
+ * lo * 2^10, from 8192 token rows (128 positions) up: each of those GEMMs
+ * is hi . W on the bf16 MFMA plus lo . W8 on the fp8 MFMA
+ * (v_mfma_f32_16x16x128_f8f6f4), W8 the e4m3 codes of each weight row over a
+ * power-of-two (bf16 weights) or its max|row| / 448 (fp8 weights) scale.
+ * The lo product carries ~4 of lo's 8 bits; the product is ~2^-13 relative
+ * instead of BF16X2's 2^-17, at three quarters of BF16X2's MFMA time.
+ * Attention, smolgen, the residual stream and the heads are as in BF16X2;
+ * below 8192 rows the whole forward is BF16X2. */
 enum {
   MFH_PRECISION_BF16 = 0,
   MFH_PRECISION_BF16X2 = 1,
   MFH_PRECISION_BF16X2_GEMM = 2,
-  MFH_PRECISION_FP8 = 3
+  MFH_PRECISION_FP8 = 3,
+  MFH_PRECISION_BF16X2_FP8LO = 4
 };
 
 /* Network description: the format fields of the weights file plus the
@@ -366,6 +377,18 @@ int mfh_debug_gemm_bf16(int M, int N, int K, const uint16_t *A,
 int mfh_debug_gemm_fp8(int M, int N, int K, const uint8_t *A8, const float *ascale,
                        const uint8_t *W8, const float *wscale, const float *bias,
                        int act, float *C);
+
+/* The GEMM of the BF16X2_FP8LO precision on host arrays, for tests: the hi
+ * product on the bf16 MFMA plus the lo product on the fp8 MFMA, accumulated
+ * together: acc = A . W^T + A_lo8 . W_lo8^T, A and W [M,K] / [N,K] bf16 bits,
+ * A_lo8 and W_lo8 OCP e4m3 codes of the same shapes (code values, no
+ * scale), then act(acc * wscale[n] + bias).  Into C (fp32), or as bf16 bits
+ * C_hi with the lo part C_lo8 = e4m3((out - C_hi) * 2^10) (the BF16X2_FP8LO
+ * activation codes).  K % 128 == 0.  No counterpart in the reference. */
+int mfh_debug_gemm_lo8(int M, int N, int K, const uint16_t *A, const uint8_t *A_lo8,
+                       const uint16_t *W, const uint8_t *W_lo8, const float *wscale,
+                       const float *bias, int act, float *C, uint16_t *C_hi,
+                       uint8_t *C_lo8);
 
 /* The device row quantiser of the fp8-activation precision on host arrays,
  * for tests: rows of bf16 bits x (+ lo plane x_lo) as OCP e4m3 codes with

@@ -20,7 +20,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libmfhip.so")
 
 MFH_OK = 0
-PRECISION = {"bf16": 0, "bf16x2": 1, "bf16x2_gemm": 2, "fp8": 3}
+PRECISION = {"bf16": 0, "bf16x2": 1, "bf16x2_gemm": 2, "fp8": 3, "bf16x2_fp8lo": 4}
 WEIGHTS = {"bf16": 0, "fp8": 1}
 ACTIVATION = {"default": 0, "mish": 1, "relu": 2, "none": 3, "tanh": 4, "sigmoid": 5,
               "selu": 6, "swish": 7, "relu_2": 8}
@@ -37,7 +37,7 @@ EXPORTS = ("mfh_net_create", "mfh_net_destroy", "mfh_net_eval", "mfh_net_eval_pl
            "mfh_net_eval_priors", "mfh_net_eval_priors_device",
            "mfh_net_eval_device_moves_left", "mfh_net_eval_device_noalloc",
            "mfh_debug_encoder_layer", "mfh_debug_skinny_gemm", "mfh_debug_gemm_fp8",
-           "mfh_debug_quantize_rows_e4m3")
+           "mfh_debug_quantize_rows_e4m3", "mfh_debug_gemm_lo8")
 FORMAT_FIELDS = ("input", "output", "network", "policy", "value", "moves_left",
                  "default_activation", "smolgen_activation", "ffn_activation", "input_embedding")
 
@@ -105,6 +105,7 @@ def lib():
                                        i, i, vp, vp, vp, ctypes.c_float, vp, vp, vp,
                                        ctypes.POINTER(i), vp, vp, vp], i),
             "mfh_debug_gemm_fp8": ([i, i, i, vp, vp, vp, vp, vp, i, vp], i),
+            "mfh_debug_gemm_lo8": ([i, i, i, vp, vp, vp, vp, vp, vp, i, vp, vp, vp], i),
             "mfh_debug_quantize_rows_e4m3": ([i, i, vp, vp, vp, vp], i),
             "mfh_net_debug_tensor": ([vp, ctypes.c_char_p, vp, u64], i),
             "mfh_debug_quantize_fp8": ([i, i, vp, vp, vp], i),
@@ -397,6 +398,30 @@ def gemm_fp8(a_codes, ascale, w_codes, wscale, bias=None, act="none"):
     _check(lib().mfh_debug_gemm_fp8(m, n, k, _ptr(a), _ptr(sa), _ptr(w), _ptr(sw), _ptr(b),
                                     ACTIVATION[act], _ptr(out)), "mfh_debug_gemm_fp8")
     return out
+
+
+def gemm_lo8(a_bits, a_lo8, w_bits, w_lo8, wscale, bias=None, act="none", bf16_out=False):
+    """The BF16X2_FP8LO GEMM through mfh_debug_gemm_lo8 (a test hook):
+    act((A.W^T + A_lo8.W_lo8^T) * wscale[n] + bias), bf16 bits and e4m3 codes
+    as given.  fp32 output, or with ``bf16_out`` (hi bits, lo e4m3 codes of
+    (out - hi) * 2^10)."""
+    u16 = lambda x: np.ascontiguousarray(x, dtype=np.uint16)  # noqa: E731
+    u8 = lambda x: np.ascontiguousarray(x, dtype=np.uint8)  # noqa: E731
+    a, al, w, wl = u16(a_bits), u8(a_lo8), u16(w_bits), u8(w_lo8)
+    sc = np.ascontiguousarray(wscale, dtype=np.float32)
+    m, k = a.shape
+    n = w.shape[0]
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = hi = lo = None
+    if bf16_out:
+        hi = np.zeros((m, n), np.uint16)
+        lo = np.zeros((m, n), np.uint8)
+    else:
+        out = np.zeros((m, n), np.float32)
+    _check(lib().mfh_debug_gemm_lo8(m, n, k, _ptr(a), _ptr(al), _ptr(w), _ptr(wl), _ptr(sc),
+                                    _ptr(b), ACTIVATION[act], _ptr(out), _ptr(hi), _ptr(lo)),
+           "mfh_debug_gemm_lo8")
+    return (hi, lo) if bf16_out else out
 
 
 def quantize_rows_e4m3(x_bits, x_lo_bits=None):

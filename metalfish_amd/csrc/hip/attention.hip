@@ -286,10 +286,24 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       const int row = threadIdx.x >> 4, chunk = threadIdx.x & 15;
       const int src = row * kCtxCols + (chunk ^ row) * 8;
       const size_t idx = out_off + static_cast<size_t>(q * 16 + row) * E + chunk * 8;
+      *reinterpret_cast<u32x4 *>(ap.ctx + idx) = *reinterpret_cast<const u32x4 *>(stage[0] + src);
+      if constexpr (OUT_PLANES > 1) {
+        const u32x4 l = *reinterpret_cast<const u32x4 *>(stage[1] + src);
+        if (ap.ctx_lo8) {
+          // The lo plane as e4m3 codes of lo * 2^kLo8Shift (rounded from
+          // its bf16 value).
+          float f[8];
 #pragma unroll
-      for (int pl = 0; pl < OUT_PLANES; ++pl)
-        *reinterpret_cast<u32x4 *>((pl ? ap.ctx_lo : ap.ctx) + idx) =
-            *reinterpret_cast<const u32x4 *>(stage[pl] + src);
+          for (int h = 0; h < 4; ++h) {
+            f[2 * h] = __uint_as_float(l[h] << 16);
+            f[2 * h + 1] = __uint_as_float(l[h] & 0xFFFF0000u);
+          }
+          *reinterpret_cast<u32x2 *>(ap.ctx_lo8 + idx) =
+              u32x2{Lo8Pack4(f[0], f[1], f[2], f[3]), Lo8Pack4(f[4], f[5], f[6], f[7])};
+        } else {
+          *reinterpret_cast<u32x4 *>(ap.ctx_lo + idx) = l;
+        }
+      }
     }
     if (qi + 1 < qn) {
       qcur = qnext;
@@ -661,15 +675,17 @@ hipError_t LaunchAttentionSmolgen(const AttentionSmolgenParams &ap, hipStream_t 
 
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::string *err) {
   const bool split = ap.qkv_lo != nullptr;
-  const bool split_out = ap.ctx_lo != nullptr;
+  const bool split_out = ap.ctx_lo != nullptr || ap.ctx_lo8 != nullptr;
   if (ap.batch <= 0 || ap.heads <= 0 || ap.heads % kHeadsPerBlock || !ap.qkv || !ap.ctx ||
       Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 16) ||
       (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
       (split && (!split_out || Misaligned(ap.qkv_lo, 16))) ||
-      (split_out && Misaligned(ap.ctx_lo, 16))) {
+      (ap.ctx_lo && Misaligned(ap.ctx_lo, 16)) || (ap.ctx_lo && ap.ctx_lo8) ||
+      (ap.ctx_lo8 && Misaligned(ap.ctx_lo8, 8))) {
     if (err)
       *err = "attention: needs batch > 0, heads % 4 == 0, 16-byte aligned qkv and ctx, "
-             "8-byte aligned bias, and a lo output plane whenever the input has one";
+             "8-byte aligned bias, and one lo output plane (bf16 or e4m3) whenever the "
+             "input has one";
     return hipErrorInvalidValue;
   }
   if (ap.q_tiles != 0 && ap.q_tiles != 1 && ap.q_tiles != 2 && ap.q_tiles != 4) {

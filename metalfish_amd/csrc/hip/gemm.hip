@@ -136,6 +136,12 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
         hi[r] = f32_to_bf16(v[r]);
         lo[r] = f32_to_bf16(v[r] - bf16_to_f32(hi[r]));
       }
+      // The lo parts as e4m3 codes (C_lo8, never beside a split output).
+      std::uint8_t *c8 = p.C_lo8 ? p.C_lo8 + static_cast<size_t>(row) * p.ldc8 + col : nullptr;
+      const unsigned q8 =
+          c8 ? Lo8Pack4(v[0] - bf16_to_f32(hi[0]), v[1] - bf16_to_f32(hi[1]),
+                        v[2] - bf16_to_f32(hi[2]), v[3] - bf16_to_f32(hi[3]))
+             : 0u;
       if (full) {
         *reinterpret_cast<u32x2 *>(c) = u32x2{hi[0] | (static_cast<unsigned>(hi[1]) << 16),
                                               hi[2] | (static_cast<unsigned>(hi[3]) << 16)};
@@ -143,6 +149,8 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
           *reinterpret_cast<u32x2 *>(c_lo + off) =
               u32x2{lo[0] | (static_cast<unsigned>(lo[1]) << 16),
                     lo[2] | (static_cast<unsigned>(lo[3]) << 16)};
+        if (c8)
+          *reinterpret_cast<unsigned *>(c8) = q8;
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -150,6 +158,8 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
             c[r] = hi[r];
             if (c_lo)
               c_lo[off + r] = lo[r];
+            if (c8)
+              c8[r] = static_cast<std::uint8_t>(q8 >> (8 * r));
           }
       }
     }
@@ -195,6 +205,16 @@ __device__ __forceinline__ void Finish8(const GemmParams &p, int row, int col, f
       *reinterpret_cast<u32x4 *>(c) = hi;
       if (c_lo)
         *reinterpret_cast<u32x4 *>(c_lo + off) = lo;
+      if (p.C_lo8) {
+        float l[8];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          l[2 * h] = v[2 * h] - __uint_as_float(hi[h] << 16);
+          l[2 * h + 1] = v[2 * h + 1] - __uint_as_float(hi[h] & 0xFFFF0000u);
+        }
+        *reinterpret_cast<u32x2 *>(p.C_lo8 + static_cast<size_t>(row) * p.ldc8 + col) =
+            u32x2{Lo8Pack4(l[0], l[1], l[2], l[3]), Lo8Pack4(l[4], l[5], l[6], l[7])};
+      }
     }
   }
 }
@@ -562,10 +582,102 @@ __device__ __forceinline__ void PipelinedLoop(const GemmParams &p, std::uint16_t
     rest(Last(), lds);
   }
 }
+
+// The fp8 lo-correction pass of the BF16X2_FP8LO precision, run after the
+// hi pass (PipelinedLoop) into the same accumulators: A_lo8 . W_lo8^T over
+// the whole K on v_mfma_f32_16x16x128_f8f6f4, 128-byte K steps.  A stage is
+// the BM activation code rows then the BN weight code rows, 128 bytes each,
+// their 16-byte chunks XOR-swizzled with row & 7 (the F8 path's layout);
+// ST2 stages of (BM + BN) * 128 bytes share the kernel's LDS ring.  Lane
+// (r, c) of a fragment feeds bytes 32 c .. 32 c + 31 of row r's K step
+// (chunks 2 c and 2 c + 1), for A and W alike.
+template <int BM, int BN, int WM, int WN, int ST2>
+__device__ __forceinline__ void Lo8Loop(const GemmParams &p, std::uint16_t *lds, int m0, int n0,
+                                        f32x4 (&acc)[BM / WM / 16][BN / WN / 16]) {
+  constexpr int NWAVES = WM * WN;
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int STAGE = (BM + BN) * 64;        // 16-bit units per stage
+  constexpr int LOADS = (BM + BN) * 128 / 1024;  // 1 KiB wave-loads (8 rows)
+  static_assert(LOADS % NWAVES == 0, "stage loads must split evenly over waves");
+  constexpr int LPW = LOADS / NWAVES;
+  static_assert(BM % 8 == 0 && ST2 == 2, "wave-loads inside one operand; two stages");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int fr = lane & 15, fc = lane >> 4;
+  const int KT = p.K / 128;
+
+  // A wave's LPW wave-loads are 8 LPW consecutive rows of one operand (BM
+  // is a multiple of them), so one buffer resource, one lane offset and a
+  // scalar offset per wave-load and K step address them.  The resource
+  // covers the operand's rows exactly: rows past M or N read zeros (they
+  // only feed outputs that are never stored).  Lane l takes row l / 8 of a
+  // wave-load and its logical chunk (l % 8) ^ (row & 7), the same for all
+  // its wave-loads.
+  static_assert(BM % (8 * LPW) == 0, "a wave's loads stay inside one operand");
+  const bool w_rows = wave * LPW * 8 >= BM;
+  const int row0 = wave * LPW * 8 - (w_rows ? BM : 0);  // first row of the wave's loads
+  const int ld = w_rows ? p.ldw8 : p.lda8;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<std::uint8_t *>(w_rows ? p.W_lo8 : p.A_lo8), 0,
+      static_cast<int>((w_rows ? p.N : p.M) * static_cast<long>(ld)), 0x00020000);
+  const unsigned goff =
+      static_cast<unsigned>((w_rows ? n0 : m0) + row0 + lane / 8) * ld + ((lane % 8) ^ (lane / 8)) * 16;
+  const int ldsw = __builtin_amdgcn_readfirstlane(wave * LPW * 512);  // 16-bit units
+  auto fill = [&](int s, int slot) {
+    std::uint16_t *d = lds + slot * STAGE + ldsw;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, MFH_LDS_PTR(d + j * 512), 16, goff,
+                                               s * 128 + j * 8 * ld, 0, 0);
+  };
+  // The hi pass's fragment reads of the ring are done before it is refilled.
+  __builtin_amdgcn_s_waitcnt(0xC00F | (7 << 4));  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int s = 0; s < ST2 - 1; ++s)
+    if (s < KT)
+      fill(s, s);
+  int slot = 0, fslot = ST2 - 1;
+  for (int kt = 0; kt < KT; ++kt) {
+    // Stage kt landed (this wave's loads; the barrier makes every wave's
+    // visible), and slot fslot, read in step kt - 1, is free again.
+    __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0), lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + ST2 - 1 < KT)
+      fill(kt + ST2 - 1, fslot);
+    const std::uint16_t *sa = lds + slot * STAGE;
+    const std::uint16_t *sw = sa + BM * 64;
+    slot = slot + 1 == ST2 ? 0 : slot + 1;
+    fslot = fslot + 1 == ST2 ? 0 : fslot + 1;
+    i32x8 af[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = wm * WTM + i * 16 + fr;
+      const u32x4 c0 = *reinterpret_cast<const u32x4 *>(sa + Swz<64>(row, 2 * fc));
+      const u32x4 c1 = *reinterpret_cast<const u32x4 *>(sa + Swz<64>(row, 2 * fc + 1));
+      af[i] = i32x8{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
+                    (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int row = wn * WTN + j * 16 + fr;
+      const u32x4 c0 = *reinterpret_cast<const u32x4 *>(sw + Swz<64>(row, 2 * fc));
+      const u32x4 c1 = *reinterpret_cast<const u32x4 *>(sw + Swz<64>(row, 2 * fc + 1));
+      const i32x8 bw = i32x8{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
+                             (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bw, af[i], acc[i][j], 0, 0,
+                                                                    0, 0, 0, 0);
+    }
+  }
+}
 #endif  // __HIP_DEVICE_COMPILE__
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8, bool F8 = false, bool PIPE = false>
+          bool W8, bool F8 = false, bool PIPE = false, bool LO8 = false>
 __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -588,6 +700,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   static_assert(!F8 || (BK == 64 && !SPLIT && !W8), "fp8 activations: BK = 64 bytes pairs");
   static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
   static_assert(!PIPE || (!W8 && !F8 && BK == 32), "pipelined loop: bf16 weights, BK = 32");
+  static_assert(!LO8 || (PIPE && !SPLIT), "fp8 lo correction follows the single-plane hi pass");
   static_assert(LOADS % NWAVES == 0, "stage loads must split evenly over waves");
   constexpr int LPW = LOADS / NWAVES;
   extern __shared__ __attribute__((aligned(1024))) std::uint16_t lds[];
@@ -702,6 +815,8 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   if constexpr (PIPE) {
 #if defined(__HIP_DEVICE_COMPILE__)
     PipelinedLoop<BM, BN, BK, ST, WM, WN, SPLIT, STAGE>(p, lds, m0, n0, k_begin, KT, acc);
+    if constexpr (LO8)
+      Lo8Loop<BM, BN, WM, WN, 2>(p, lds, m0, n0, acc);
 #endif
   } else {
   int slot = 0;                       // kt % ST
@@ -1004,11 +1119,15 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8 = false, bool F8 = false, bool PIPE = false>
+          bool W8 = false, bool F8 = false, bool PIPE = false, bool LO8 = false>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
-  constexpr size_t kLds =
+  // The LDS ring: ST stages of the main loop, or two stages of the fp8 lo
+  // pass's 128-byte rows when larger.
+  constexpr size_t kRing =
       static_cast<size_t>(ST) * GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>();
-  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8, PIPE>;
+  constexpr size_t kLo8Ring = LO8 ? static_cast<size_t>(2) * (BM + BN) * 128 : 0;
+  constexpr size_t kLds = kRing > kLo8Ring ? kRing : kLo8Ring;
+  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8, PIPE, LO8>;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&]() {
@@ -1048,21 +1167,21 @@ hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_
 // Epilogue dispatch: the activations the network uses (none, mish) get
 // dedicated instances, anything else the runtime switch.
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8, bool F8 = false,
-          bool PIPE = false>
+          bool PIPE = false, bool LO8 = false>
 hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
   if (p.k_splits > 1 || (p.out_mode == GEMM_OUT_F32 && p.act == ACT_NONE))
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8, F8, PIPE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8, F8, PIPE, LO8>(p, stream);
   if (p.out_mode == GEMM_OUT_RESID_F32)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8, F8, PIPE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8, F8, PIPE, LO8>(p, stream);
   if (p.out_mode == GEMM_OUT_F32)
     return p.act == ACT_MISH
-               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8, F8, PIPE>(p, stream)
-               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8, F8, PIPE>(p, stream);
+               ? LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_MISH, W8, F8, PIPE, LO8>(p, stream)
+               : LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_RUNTIME, W8, F8, PIPE, LO8>(p, stream);
   if (p.act == ACT_NONE)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8, F8, PIPE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8, F8, PIPE, LO8>(p, stream);
   if (p.act == ACT_MISH)
-    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8, F8, PIPE>(p, stream);
-  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8, F8, PIPE>(p, stream);
+    return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8, F8, PIPE, LO8>(p, stream);
+  return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8, F8, PIPE, LO8>(p, stream);
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT>
@@ -1142,6 +1261,12 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     return hipErrorInvalidValue;
   };
   GemmParams p = p_in;
+  const bool lo8 = p.A_lo8 != nullptr;
+  if (lo8 && (!p.A || p.A_lo || !p.W || p.W8 || !p.wscale || !p.W_lo8 || p.A8 ||
+              p.k_splits != 1 || p.K % 128 || p.lda8 % 16 || p.ldw8 % 16 || p.lda8 < p.K ||
+              p.ldw8 < p.K || !Aligned(p.A_lo8, 16) || !Aligned(p.W_lo8, 16)))
+    return fail("fp8 lo correction needs A (hi) + A_lo8 with W (bf16) + W_lo8 + wscale, "
+                "one K slice, K % 128 == 0, lda8 / ldw8 % 16 == 0 and 16-byte aligned codes");
   const bool f8 = p.A8 != nullptr;
   if (f8) {
     // fp8 activations x fp8 weights: the byte operands go through the bf16
@@ -1191,6 +1316,10 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     return fail("split output needs lo planes for both parts or neither");
   if (p.ldc < (p.split_n < p.N ? p.split_n : p.N))
     return fail("ldc too small");
+  if (p.C_lo8 && (p.out_mode != GEMM_OUT_BF16 || p.C_lo || p.split_n < p.N || p.k_splits != 1 ||
+                  p.ldc8 < p.N || p.ldc8 % 8 || !Aligned(p.C_lo8, 8)))
+    return fail("e4m3 lo output: bf16 mode, one output, no bf16 lo plane, ldc8 >= N, "
+                "ldc8 % 8 == 0, 8-byte aligned");
   // Vector (4-column) stores need every output row start aligned to 4
   // elements' width; otherwise the epilogue stores element by element.
   const bool f32 = p.out_mode != GEMM_OUT_BF16 || p.k_splits > 1;
@@ -1212,6 +1341,11 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
            (p.out_mode != GEMM_OUT_RESID_F32 ||
             (p.resid16 ? Aligned(p.resid16, 16) && Aligned(p.resid16_lo, 16) && p.ldr % 8 == 0
                        : Aligned(p.resid, 16) && p.ldr % 4 == 0));
+  // fp8 lo correction: 256 x 256 tiles of eight waves, the hi pass on the
+  // four-stage single-bf16 pipelined ring (128 KiB), then the lo pass on two
+  // 64 KiB stages of code rows.
+  if (lo8)
+    return LaunchW<256, 256, 32, 4, 4, 2, false, false, false, true, true>(p, stream);
   const bool split = p.A_lo != nullptr;
   const bool large = p.M >= kLargeRows && p.N >= 128;
   // Small problems (few positions): 64 x 64 tiles leave most CUs idle and

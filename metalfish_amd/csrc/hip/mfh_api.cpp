@@ -102,6 +102,10 @@ constexpr int kSmolgenFewRowMaxBatch = 16;
 // slower, 2.07 -> 2.19).
 constexpr int kSmolgenSideRows = 1088;
 
+// BF16X2_FP8LO: the fp8 lo correction runs from this many token rows (128
+// positions); below, the forward is the BF16X2 one.
+constexpr int kLo8MinRows = 8192;
+
 std::uint16_t ToBf16(float f) {
   std::uint32_t u;
   std::memcpy(&u, &f, 4);
@@ -141,6 +145,13 @@ void QuantizeRowE4m3(const float *row, int n, std::uint8_t *codes, float *scale)
   for (int i = 0; i < n; ++i)
     codes[i] = EncodeE4m3(row[i] / s);
   *scale = s;
+}
+
+// Value of an OCP e4m3 code (finite codes only).
+float DecodeE4m3(std::uint8_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  const float v = e ? std::ldexp(1.0f + m / 8.0f, e - 7) : std::ldexp(static_cast<float>(m), -9);
+  return (c & 0x80) ? -v : v;
 }
 
 int ActFromProto(int proto_act, int default_act) {
@@ -209,6 +220,8 @@ struct Dims {
   bool fused_bias = false;  // smolgen bias generated inside the attention kernel
   bool skinny = true;       // few-row GEMMs for single-position forwards
   bool fp8_act = false;     // e4m3 activations on the fp8 MFMA (FP8 precision)
+  bool lo8 = false;         // BF16X2_FP8LO: e4m3 lo parts on the fp8 MFMA
+  bool lo8_ffn1 = false;    // ... also on FFN1 (else its BF16X2 GEMM, lo8 output)
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -240,6 +253,9 @@ struct mfh_net {
   size_t in_ffn1_b, in_ffn2_b, in_ln_g, in_ln_b;
   std::vector<Layer> layers;
   std::vector<Layer> pol_layers;  // policy encoder layers
+  // BF16X2_FP8LO: offset of a dense weight's W' (bf16, with column scales) ->
+  // offset of its e4m3 codes.
+  std::map<size_t, size_t> lo8_codes;
   size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
   size_t head_w[2], qk_w[2], val1_w[2];
   size_t mov_b = 0, mov1_b = 0, mov2_w = 0, mov2_b = 0;  // moves-left head
@@ -397,6 +413,65 @@ GemmW AddGemmW(Blob &blob, bool fp8, const std::vector<const float *> &parts,
   return g;
 }
 
+// A GEMM weight of the BF16X2_FP8LO precision: for each output row n a
+// scale s_n, the row times 2^kLo8Shift / s_n as bf16 (W'), the e4m3 codes of
+// the row / s_n (W8, the fp8 lo-correction operand) and cs_n = s_n /
+// 2^kLo8Shift (the GEMM's column scale), so that (hi . W'_n + lo8 . W8_n)
+// cs_n = hi . W_n + lo . W_n up to the e4m3 rounding of the lo product.
+// bf16 weights: s_n is the power of two with max|W_n| / s_n in (224, 448],
+// so W' is exact.  fp8 weights: the codes and row scale of AddGemmW, and W'
+// the codes' values times 2^kLo8Shift (exact in bf16).  Returns {W', cs}
+// and the codes' offset in *codes.
+GemmW AddGemmWLo8(Blob &blob, bool fp8, const std::vector<const float *> &parts,
+                  const std::vector<int> &part_rows, int cols, int ld, size_t *codes_off) {
+  size_t rows = 0;
+  for (int r : part_rows)
+    rows += r;
+  std::vector<std::uint16_t> wp(rows * ld, 0);
+  std::vector<std::uint8_t> codes(rows * ld, 0);
+  std::vector<float> cs(rows, 1.0f);
+  std::vector<float> tmp(ld);
+  const float lo_scale = static_cast<float>(1 << mfh::kLo8Shift);
+  size_t row = 0;
+  for (size_t p = 0; p < parts.size(); ++p) {
+    for (int r = 0; r < part_rows[p]; ++r, ++row) {
+      std::fill(tmp.begin(), tmp.end(), 0.f);
+      if (parts[p])
+        std::memcpy(tmp.data(), parts[p] + static_cast<size_t>(r) * cols, cols * 4);
+      std::uint8_t *c = codes.data() + row * ld;
+      std::uint16_t *w = wp.data() + row * ld;
+      if (fp8) {
+        float ws = 1.f;
+        QuantizeRowE4m3(tmp.data(), ld, c, &ws);
+        for (int i = 0; i < ld; ++i)
+          w[i] = ToBf16(DecodeE4m3(c[i]) * lo_scale);
+        cs[row] = ws / lo_scale;
+      } else {
+        float mx = 0.f;
+        for (int i = 0; i < ld; ++i) {
+          std::uint16_t b = ToBf16(tmp[i]);
+          const std::uint32_t u = static_cast<std::uint32_t>(b) << 16;
+          std::memcpy(&tmp[i], &u, 4);
+          mx = std::fmax(mx, std::fabs(tmp[i]));
+        }
+        const float sc = mx > 0.f ? std::ldexp(1.0f, static_cast<int>(std::ceil(
+                                                       std::log2(mx / 448.0f))))
+                                  : 1.0f;
+        for (int i = 0; i < ld; ++i) {
+          c[i] = EncodeE4m3(tmp[i] / sc);
+          w[i] = ToBf16(tmp[i] * (lo_scale / sc));
+        }
+        cs[row] = sc / lo_scale;
+      }
+    }
+  }
+  GemmW g;
+  g.w = blob.Add(wp.data(), wp.size() * 2);
+  g.s = blob.Add(cs.data(), cs.size() * 4);
+  *codes_off = blob.Add(codes.data(), codes.size());
+  return g;
+}
+
 size_t AddF32(Blob &blob, const std::vector<const float *> &parts,
               const std::vector<int> &counts) {
   std::vector<float> buf;
@@ -423,16 +498,20 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   if (desc.weights_dtype != MFH_WEIGHTS_BF16 && desc.weights_dtype != MFH_WEIGHTS_FP8)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported weight storage type");
   if (desc.precision != MFH_PRECISION_BF16 && desc.precision != MFH_PRECISION_BF16X2 &&
-      desc.precision != MFH_PRECISION_BF16X2_GEMM && desc.precision != MFH_PRECISION_FP8)
+      desc.precision != MFH_PRECISION_BF16X2_GEMM && desc.precision != MFH_PRECISION_FP8 &&
+      desc.precision != MFH_PRECISION_BF16X2_FP8LO)
     return SetError(MFH_ERR_UNSUPPORTED, "unsupported precision mode");
   if (desc.precision == MFH_PRECISION_FP8 && desc.weights_dtype != MFH_WEIGHTS_FP8)
     return SetError(MFH_ERR_UNSUPPORTED, "the FP8 precision needs FP8 (e4m3) weights");
   d.fp8_act = desc.precision == MFH_PRECISION_FP8;
-  d.split = desc.precision == MFH_PRECISION_BF16X2 || desc.precision == MFH_PRECISION_BF16X2_GEMM;
-  d.split_attn = desc.precision == MFH_PRECISION_BF16X2;
+  d.lo8 = desc.precision == MFH_PRECISION_BF16X2_FP8LO;
+  d.split = desc.precision == MFH_PRECISION_BF16X2 ||
+            desc.precision == MFH_PRECISION_BF16X2_GEMM || d.lo8;
+  d.split_attn = desc.precision == MFH_PRECISION_BF16X2 || d.lo8;
   // Measured at the BT4 shape: the panel wins with e4m3 weights (half the
   // weight bytes to stream), the tiled GEMM + LayerNorm kernel with bf16.
-  d.fused_ln = desc.fused_layernorm != 0 || desc.weights_dtype == MFH_WEIGHTS_FP8;
+  // The panel has no fp8 lo correction: BF16X2_FP8LO keeps the tiled GEMM.
+  d.fused_ln = !d.lo8 && (desc.fused_layernorm != 0 || desc.weights_dtype == MFH_WEIGHTS_FP8);
   d.wdl = desc.value == MFH_VALUE_WDL;
   d.mlh = desc.moves_left == 1;
   d.act_default = desc.default_activation == MFH_DEFAULT_ACTIVATION_MISH ? mfh::ACT_MISH
@@ -542,7 +621,9 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // METALFISH_HIP_SMOLGEN_BIAS=attention the attention kernel generates the
   // bias itself (gen widths 64, 128 or 256) and no bias tensor exists.
   const char *bias_env = std::getenv("METALFISH_HIP_SMOLGEN_BIAS");
-  d.fused_bias = d.smolgen && bias_env && std::string(bias_env) == "attention" &&
+  const char *ffn1_env = std::getenv("METALFISH_HIP_LO8_FFN1");
+  d.lo8_ffn1 = ffn1_env && ffn1_env[0] == '1';
+  d.fused_bias = d.smolgen && !d.lo8 && bias_env && std::string(bias_env) == "attention" &&
                  (d.G == 64 || d.G == 128 || d.G == 256) &&
                  mfh::AttentionSmolgenLds(d.G, d.split_attn) <= 160 * 1024;
   // Single-position forward with few-row GEMMs and deferred LayerNorms (on
@@ -656,15 +737,27 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       cw = need(p + ".mha.smolgen.compress", static_cast<size_t>(d.C) * E);
     if (!ld.error.empty())
       return SetError(MFH_ERR_INVALID, ld.error);
-    SetW(L.qkv_w, AddGemmW(blob, net->fp8, {qw, kw, vw, cw}, {E, E, E, smolgen ? d.C : 0}, E, E));
+    // BF16X2_FP8LO: the four dense weights of the layer also carry e4m3
+    // codes for the fp8 lo correction (AddGemmWLo8); every GEMM on them
+    // then applies their column scales.
+    auto gemm_w = [&](const std::vector<const float *> &parts, const std::vector<int> &rows,
+                      int cols, int ldw) {
+      if (!d.lo8)
+        return AddGemmW(blob, net->fp8, parts, rows, cols, ldw);
+      size_t codes = 0;
+      const GemmW g = AddGemmWLo8(blob, net->fp8, parts, rows, cols, ldw, &codes);
+      net->lo8_codes[g.w] = codes;
+      return g;
+    };
+    SetW(L.qkv_w, gemm_w({qw, kw, vw, cw}, {E, E, E, smolgen ? d.C : 0}, E, E));
     L.qkv_b = AddF32(blob, {qb, kb, vb, nullptr}, {E, E, E, smolgen ? d.C : 0});
-    SetW(L.out_w, AddGemmW(blob, net->fp8, {ow}, {E}, E, E));
+    SetW(L.out_w, gemm_w({ow}, {E}, E, E));
     L.out_b = AddF32(blob, {ob}, {E});
     L.ln1_g = AddF32(blob, {l1g}, {E});
     L.ln1_b = AddF32(blob, {l1b}, {E});
-    SetW(L.ffn1_w, AddGemmW(blob, net->fp8, {f1w}, {ffn}, E, E));
+    SetW(L.ffn1_w, gemm_w({f1w}, {ffn}, E, E));
     L.ffn1_b = AddF32(blob, {f1b}, {ffn});
-    SetW(L.ffn2_w, AddGemmW(blob, net->fp8, {f2w}, {E}, ffn, ffn));
+    SetW(L.ffn2_w, gemm_w({f2w}, {E}, ffn, ffn));
     L.ffn2_b = AddF32(blob, {f2b}, {E});
     L.ln2_g = AddF32(blob, {l2g}, {E});
     L.ln2_b = AddF32(blob, {l2b}, {E});
@@ -844,6 +937,13 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
     add("hid8", M * (hid ? hid : 1));
     add("sc_hid", M * 4);
   }
+  // e4m3 lo parts of the encoder GEMM inputs (BF16X2_FP8LO), at the batches
+  // whose forward uses them.
+  if (d.lo8 && M >= static_cast<size_t>(kLo8MinRows)) {
+    add("act_lo8", M * d.E);
+    add("ctx_lo8", M * d.E);
+    add("hid_lo8", M * (hid ? hid : 1));
+  }
   // Row statistics of the single-position smolgen chain's deferred
   // LayerNorms (partial sums per workgroup): dense1 and dense2 outputs.
   // One (sum, sum of squares) pair per producing workgroup and row, for up
@@ -1017,7 +1117,12 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     p.A = ws.S<std::uint16_t>(a);
     p.A_lo = ws.Lo(a);
     p.lda = lda;
-    if (net->fp8) {
+    if (net->lo8_codes.count(w[0])) {
+      // A BF16X2_FP8LO weight: bf16 rows scaled per column, for the plain
+      // product too.
+      p.W = net->W<std::uint16_t>(w[0]);
+      p.wscale = net->W<float>(w[1]);
+    } else if (net->fp8) {
       p.W8 = net->W<std::uint8_t>(w[0]);
       p.wscale = net->W<float>(w[1]);
     } else {
@@ -1043,6 +1148,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     const double flops = 2.0 * p.M * p.N * p.K;
     const double out_bytes = p.out_mode == mfh::GEMM_OUT_BF16 ? 2.0 * plane_mult : 4.0;
     const double bytes = 2.0 * p.M * p.K * (p.A_lo ? 2.0 : 1.0) + (p.W8 ? 1.0 : 2.0) * p.N * p.K +
+                         (p.A_lo8 ? 1.0 * p.M * p.K + 1.0 * p.N * p.K : 0.0) +
                          out_bytes * p.M * p.N * p.k_splits +
                          (p.out_mode == mfh::GEMM_OUT_RESID_F32 ? 4.0 * p.M * p.N : 0.0);
     hipStream_t s = on ? on : st;
@@ -1057,9 +1163,15 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     StageTimer t(net, s, "layernorm", 0.0, bytes);
     return mfh::LaunchLayerNorm(lp, s, &err_);
   };
+  // BF16X2_FP8LO at this batch: the LayerNorms writing "act" also write its
+  // e4m3 lo codes, attention and FFN1 write theirs instead of bf16 lo planes,
+  // and the encoder GEMMs on those inputs add the fp8 lo product.
+  const bool lo8 = d.lo8 && M >= kLo8MinRows && ws.Has("act_lo8");
   auto ln = [&](const float *x, int rows, int width, float eps, const float *g, const float *b,
                 float *y32, const std::string &y16) {
     mfh::LayerNormParams lp;
+    if (lo8 && y16 == "act")
+      lp.y_lo8 = ws.S<std::uint8_t>("act_lo8");
     lp.x = x;
     lp.rows = rows;
     lp.width = width;
@@ -1134,12 +1246,29 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     p.A = nullptr;
     p.A_lo = nullptr;
   };
+  // BF16X2_FP8LO: the GEMM on workspace input `a` (hi plane + e4m3 lo codes
+  // "<a>_lo8") with the codes of weight w_off for the fp8 lo product; false
+  // (p unchanged) where this forward or weight has none.
+  auto use_lo8 = [&](mfh::GemmParams &p, const std::string &a, const size_t (&w_off)[2]) {
+    const auto it = net->lo8_codes.find(w_off[0]);
+    if (!lo8 || it == net->lo8_codes.end())
+      return false;
+    p.A_lo = nullptr;
+    p.A_lo8 = ws.S<std::uint8_t>(a + "_lo8");
+    p.lda8 = p.lda;
+    p.W_lo8 = net->W<std::uint8_t>(it->second);
+    p.ldw8 = p.ldw;
+    p.partials = nullptr;
+    return true;
+  };
   auto residual_gemm = [&](const std::string &a, int k, const size_t (&w_off)[2],
                            const float *bias, const char *role, float alpha, bool f8 = false) {
     mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
                              mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
     if (f8)
       use_fp8(p, a);
+    else
+      use_lo8(p, a, w_off);
     if (d.split) {
       p.resid16 = ws.S<std::uint16_t>("act");
       p.resid16_lo = ws.Lo("act");
@@ -1407,6 +1536,10 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     ap.heads = heads;
     ap.ctx = ws.S<std::uint16_t>("ctx");
     ap.ctx_lo = ws.Lo("ctx");
+    if (lo8 && net->lo8_codes.count(L.out_w[0])) {
+      ap.ctx_lo = nullptr;
+      ap.ctx_lo8 = ws.S<std::uint8_t>("ctx_lo8");
+    }
     // Dense1 on the flattened compression (split-K partials summed by the
     // LayerNorm kernel with bias and activation), dense2 (bias and
     // activation in its epilogue) and its LayerNorm, then the shared global
@@ -1446,6 +1579,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
           pc.wscale += skip;
         } else {
           pc.W += skip * E;
+          if (pc.wscale)  // BF16X2_FP8LO column scales
+            pc.wscale += skip;
         }
         MFH_RUN(run(pc, "smolgen_compress", on));
       }
@@ -1503,6 +1638,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     if (f8) {
       MFH_RC(quant("act", E));
       use_fp8(pq, "act");
+    } else if (pq.N == 3 * E) {
+      use_lo8(pq, "act", L.qkv_w);
     }
     MFH_RUN(run(pq, "qkv"));
     if (L.smolgen && !side_chain) {
@@ -1565,6 +1702,13 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     if (f8) {
       MFH_RC(quant("act", E));
       use_fp8(pf, "act");
+    } else if (lo8 && net->lo8_codes.count(L.ffn2_w[0])) {
+      // FFN2 adds the fp8 lo product: FFN1 writes its lo parts as codes.
+      if (d.lo8_ffn1)
+        use_lo8(pf, "act", L.ffn1_w);
+      pf.C_lo = nullptr;
+      pf.C_lo8 = ws.S<std::uint8_t>("hid_lo8");
+      pf.ldc8 = ffn;
     }
     MFH_RUN(run(pf, "ffn1"));
     rc = residual_ln("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, eps_ffn,
@@ -2281,7 +2425,11 @@ int mfh_net_info(const mfh_net *net, char *buf, size_t len) {
     o << ", moves left " << d.Md << "/" << d.Mh;
   o << ", activations " << ActName(d.act_default) << "/"
     << ActName(d.act_smolgen) << "/" << ActName(d.act_ffn) << ", precision "
-    << (d.split_attn ? "bf16x2" : d.split ? "bf16x2_gemm" : d.fp8_act ? "fp8" : "bf16")
+    << (d.lo8          ? "bf16x2_fp8lo"
+        : d.split_attn ? "bf16x2"
+        : d.split      ? "bf16x2_gemm"
+        : d.fp8_act    ? "fp8"
+                       : "bf16")
     << ", weights "
     << (net->fp8 ? "e4m3 " : "bf16 ") << net->weight_bytes << " B, workspace " << net->ws_bytes << " B, max_batch "
     << net->max_batch << ", no-allocation batch <= " << net->noalloc_max_batch;
@@ -2374,6 +2522,18 @@ int mfh_debug_encoder_layer(mfh_net *net, int batch, int layer, int iterations,
   MFH_HIP_CHECK(hipMemcpy(ws.S<std::uint16_t>("act"), x, n * 2, hipMemcpyHostToDevice));
   if (net->d.split) {
     MFH_HIP_CHECK(hipMemcpy(ws.Lo("act"), x_lo, n * 2, hipMemcpyHostToDevice));
+    if (net->d.lo8 && batch * kSquares >= kLo8MinRows && ws.Has("act_lo8")) {
+      // BF16X2_FP8LO: the lo plane's e4m3 codes (lo * 2^kLo8Shift).
+      std::vector<std::uint8_t> codes(n);
+      for (size_t i = 0; i < n; ++i) {
+        const std::uint32_t u = static_cast<std::uint32_t>(x_lo[i]) << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        codes[i] = EncodeE4m3(f * static_cast<float>(1 << mfh::kLo8Shift));
+      }
+      MFH_HIP_CHECK(hipMemcpy(ws.S<std::uint8_t>("act_lo8"), codes.data(), n,
+                              hipMemcpyHostToDevice));
+    }
   } else {
     std::vector<float> x32(n);
     for (size_t i = 0; i < n; ++i) {
@@ -2706,6 +2866,61 @@ int mfh_debug_gemm_fp8(int M, int N, int K, const uint8_t *A8, const float *asca
     if (hipDeviceSynchronize() != hipSuccess ||
         hipMemcpy(C, p.C, nc * 4, hipMemcpyDeviceToHost) != hipSuccess)
       return SetError(MFH_ERR_HIP, "fp8 gemm execution failed");
+  } catch (const std::exception &e) {
+    return SetError(MFH_ERR_HIP, e.what());
+  }
+  return MFH_OK;
+}
+
+int mfh_debug_gemm_lo8(int M, int N, int K, const uint16_t *A, const uint8_t *A_lo8,
+                       const uint16_t *W, const uint8_t *W_lo8, const float *wscale,
+                       const float *bias, int act, float *C, uint16_t *C_hi, uint8_t *C_lo8) {
+  if (M <= 0 || N <= 0 || K <= 0 || !A || !A_lo8 || !W || !W_lo8 || !wscale ||
+      (!C && !(C_hi && C_lo8)) || (C && (C_hi || C_lo8)))
+    return SetError(MFH_ERR_INVALID, "mfh_debug_gemm_lo8: bad arguments");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+    return SetError(MFH_ERR_NO_DEVICE, "no HIP device available");
+  const size_t na = static_cast<size_t>(M) * K, nw = static_cast<size_t>(N) * K,
+               nc = static_cast<size_t>(M) * N;
+  try {
+    DebugBuffers buf;
+    mfh::GemmParams p;
+    p.A = buf.Put(A, na);
+    p.lda = K;
+    p.A_lo8 = buf.Put(A_lo8, na);
+    p.lda8 = K;
+    p.W = buf.Put(W, nw);
+    p.ldw = K;
+    p.W_lo8 = buf.Put(W_lo8, nw);
+    p.ldw8 = K;
+    p.wscale = buf.Put(wscale, N);
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.bias = buf.Put(bias, N);
+    p.act = ActFromProto(act, mfh::ACT_RELU);
+    if (act == MFH_ACTIVATION_NONE || act == MFH_ACTIVATION_DEFAULT)
+      p.act = mfh::ACT_NONE;
+    if (C) {
+      p.out_mode = mfh::GEMM_OUT_F32;
+      p.C = buf.Put<float>(nullptr, nc, false);
+    } else {
+      p.out_mode = mfh::GEMM_OUT_BF16;
+      p.C = buf.Put<std::uint16_t>(nullptr, nc, false);
+      p.C_lo8 = buf.Put<std::uint8_t>(nullptr, nc, false);
+      p.ldc8 = N;
+    }
+    p.ldc = N;
+    std::string err;
+    if (mfh::LaunchGemm(p, nullptr, &err) != hipSuccess)
+      return SetError(MFH_ERR_INVALID, err);
+    if (hipDeviceSynchronize() != hipSuccess)
+      return SetError(MFH_ERR_HIP, "fp8 lo-correction gemm execution failed");
+    if (C ? hipMemcpy(C, p.C, nc * 4, hipMemcpyDeviceToHost) != hipSuccess
+          : (hipMemcpy(C_hi, p.C, nc * 2, hipMemcpyDeviceToHost) != hipSuccess ||
+             hipMemcpy(C_lo8, p.C_lo8, nc, hipMemcpyDeviceToHost) != hipSuccess))
+      return SetError(MFH_ERR_HIP, "copy to host failed");
   } catch (const std::exception &e) {
     return SetError(MFH_ERR_HIP, e.what());
   }

@@ -84,6 +84,16 @@ __device__ __forceinline__ bf16x8 Fp8x8ToBf16(u32x2 q) {
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// e4m3 codes of four lo parts scaled by 2^kLo8Shift (the BF16X2_FP8LO
+// activation lo plane), round to nearest even, clamped to +-448 first.
+__device__ __forceinline__ unsigned Lo8Pack4(float a, float b, float c, float d) {
+  constexpr float kScale = static_cast<float>(1 << kLo8Shift);
+  const auto q = [](float x) { return fminf(fmaxf(x * kScale, -448.0f), 448.0f); };
+  int packed = __builtin_amdgcn_cvt_pk_fp8_f32(q(a), q(b), 0, false);
+  packed = __builtin_amdgcn_cvt_pk_fp8_f32(q(c), q(d), packed, true);
+  return static_cast<unsigned>(packed);
+}
+
 // Generic pointer to LDS memory as the address-space-3 pointer that the
 // direct global->LDS load builtin takes.
 #define MFH_LDS_PTR(p) ((__attribute__((address_space(3))) void *)(p))

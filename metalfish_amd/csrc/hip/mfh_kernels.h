@@ -11,6 +11,14 @@
 
 namespace mfh {
 
+// Fixed power-of-two scale of the e4m3 lo parts of activations in the
+// BF16X2_FP8LO precision: code = e4m3(lo * 2^kLo8Shift).  |lo| <= 2^-9 |x|
+// for lo = x - bf16(x), so codes saturate (448) only for |x| > 224, far above
+// the LayerNorm, attention and FFN outputs that carry them; lo parts below
+// 2^-16 (|x| below ~2^-7) lose bits to e4m3 subnormals, an absolute error
+// under 2^-20.
+constexpr int kLo8Shift = 10;
+
 // Activation ids used by kernel epilogues (the C ABI maps the
 // reference's ActivationFunction values onto these).
 enum Act : int {
@@ -80,6 +88,21 @@ struct GemmParams {
   // == 0, lda % 16 == 0, M >= 2048 rows.
   const std::uint8_t *A8 = nullptr;
   const float *ascale = nullptr;
+  // fp8 lo correction (the BF16X2_FP8LO precision): the activation is hi + lo
+  // with hi = A (bf16) and lo = A_lo8 / 2^kLo8Shift (e4m3 codes [M][lda8]),
+  // and the product is hi . W^T on the bf16 MFMA plus A_lo8 . W_lo8^T
+  // (e4m3 codes [N][ldw8]) on the fp8 MFMA, accumulated together; W then
+  // holds the weights times 2^kLo8Shift / s_n and W_lo8 the e4m3 codes of
+  // W_n / s_n, and wscale[n] = s_n / 2^kLo8Shift brings the sum back.
+  // K % 128 == 0; whole 256 x 256 tiles over one K slice.
+  const std::uint8_t *A_lo8 = nullptr;
+  int lda8 = 0;
+  const std::uint8_t *W_lo8 = nullptr;
+  int ldw8 = 0;
+  // bf16 outputs: the lo part as e4m3 codes of lo * 2^kLo8Shift [M][ldc8]
+  // (instead of the bf16 C_lo plane), the A_lo8 of a following GEMM.
+  std::uint8_t *C_lo8 = nullptr;
+  int ldc8 = 0;
   // Tiles that leave room for a concurrent launch on another stream (bf16
   // weights).  beside_chain (split precision): whole-round 256 x 256 tiles
   // take two LDS stages (96 KiB) instead of three (144 KiB).  small_lds:
@@ -296,6 +319,9 @@ struct LayerNormParams {
   float *y_f32 = nullptr;
   std::uint16_t *y_bf16 = nullptr;
   std::uint16_t *y_bf16_lo = nullptr;
+  // The lo part of each bf16 output as e4m3 codes of lo * 2^kLo8Shift
+  // ([rows][width] bytes), beside or instead of y_bf16_lo.
+  std::uint8_t *y_lo8 = nullptr;
 };
 hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream,
                            std::string *err);
@@ -314,6 +340,9 @@ struct AttentionParams {
   int batch = 0, heads = 0;
   std::uint16_t *ctx = nullptr;
   std::uint16_t *ctx_lo = nullptr;
+  // With split outputs: the lo plane as e4m3 codes of lo * 2^kLo8Shift
+  // ([B*64][E] bytes) instead of ctx_lo.
+  std::uint8_t *ctx_lo8 = nullptr;
   // Query tiles (of 4) per workgroup: 4, 2 or 1 (the rest over grid.y), or
   // 0 to choose by batch (fewer per workgroup when there are few of them).
   int q_tiles = 0;

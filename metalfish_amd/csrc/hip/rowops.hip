@@ -210,6 +210,7 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
     if (c0 >= width)
       break;
     unsigned hi2[2 * Q], lo2[2 * Q];  // bf16 pairs of the group
+    unsigned q8[Q];                    // e4m3 lo codes of the group
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
       const int c = c0 + 4 * q;
@@ -225,11 +226,14 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
       if (lp.y_f32)
         *reinterpret_cast<f32x4 *>(lp.y_f32 + row_off + c) = y;
       std::uint16_t hi[4], lo[4];
+      float lf[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         hi[e] = f32_to_bf16(y[e]);
-        lo[e] = f32_to_bf16(y[e] - bf16_to_f32(hi[e]));
+        lf[e] = y[e] - bf16_to_f32(hi[e]);
+        lo[e] = f32_to_bf16(lf[e]);
       }
+      q8[q] = lp.y_lo8 ? Lo8Pack4(lf[0], lf[1], lf[2], lf[3]) : 0u;
       hi2[2 * q] = hi[0] | (static_cast<unsigned>(hi[1]) << 16);
       hi2[2 * q + 1] = hi[2] | (static_cast<unsigned>(hi[3]) << 16);
       lo2[2 * q] = lo[0] | (static_cast<unsigned>(lo[1]) << 16);
@@ -246,6 +250,12 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
         *reinterpret_cast<u32x2 *>(lp.y_bf16 + row_off + c0) = u32x2{hi2[0], hi2[1]};
         if (lp.y_bf16_lo)
           *reinterpret_cast<u32x2 *>(lp.y_bf16_lo + row_off + c0) = u32x2{lo2[0], lo2[1]};
+      }
+      if (lp.y_lo8) {
+        if constexpr (G == 8)
+          *reinterpret_cast<u32x2 *>(lp.y_lo8 + row_off + c0) = u32x2{q8[0], q8[1]};
+        else
+          *reinterpret_cast<unsigned *>(lp.y_lo8 + row_off + c0) = q8[0];
       }
     }
   }
@@ -426,6 +436,7 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
   if (lp.width % 4 || !aligned(lp.x, 16) || (lp.bias && !aligned(lp.bias, 16)) ||
       !aligned(lp.gamma, 16) || !aligned(lp.beta, 16) || (lp.y_f32 && !aligned(lp.y_f32, 16)) ||
       (lp.y_bf16 && !aligned(lp.y_bf16, 8)) || (lp.y_bf16_lo && !aligned(lp.y_bf16_lo, 8)) ||
+      (lp.y_lo8 && (!lp.y_bf16 || !aligned(lp.y_lo8, 8))) ||
       (lp.resid && !aligned(lp.resid, 16)) ||
       (lp.resid16 && (!aligned(lp.resid16, 8) || !aligned(lp.resid16_lo, 8)))) {
     Fail(err, "layernorm: width % 4 == 0 and 16-byte aligned rows required");
