@@ -68,7 +68,49 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 256 MiB buffer 5 times (the known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time torch's bf16 matmul (hipBLASLt) on the encoder GEMM shapes "
+                         "at batch 256 with K doubled (the MFMA work of the split precision), "
+                         "and an 8192^3 product, as a comparator for the GEMM kernel; then exit")
     return ap.parse_args()
+
+
+# Encoder GEMM shapes at batch 256 (M = 16384 token rows): (role, N, K).
+VENDOR_SHAPES = (("qkv", 3072, 1024), ("out", 1024, 1024), ("ffn1", 1536, 1024),
+                 ("ffn2", 1024, 1536))
+
+
+def vendor_gemm():
+    """torch.matmul in bf16 (hipBLASLt on ROCm) at the split-precision
+    equivalent of each encoder GEMM (A [16384, 2K] x W^T [2K, N]: the same
+    MFMA work as hi.W + lo.W) and at 8192^3; bf16 output, no epilogue.
+    Prints one JSON line of microseconds and TFLOP/s (algorithmic FLOPs of
+    the product timed)."""
+    import torch
+
+    torch.manual_seed(0)
+    out = {}
+    shapes = [(role, 16384, n, 2 * k) for role, n, k in VENDOR_SHAPES] + [("square", 8192, 8192, 8192)]
+    for role, m, n, k in shapes:
+        a = torch.randn(m, k, dtype=torch.bfloat16, device="cuda")
+        w = torch.randn(n, k, dtype=torch.bfloat16, device="cuda").t().contiguous()
+        for _ in range(3):
+            torch.matmul(a, w)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        iters = 20
+        e0.record()
+        for _ in range(iters):
+            torch.matmul(a, w)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        out[role] = {"m": m, "n": n, "k": k, "us": round(us, 1),
+                     "tflops": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
+                     "frac_of_bf16_peak": round(2.0 * m * n * k / (us * 1e-6) / 1e12 /
+                                                PEAK_BF16_TFLOPS, 3)}
+    print(json.dumps({"vendor_gemm": out}))
 
 
 def copy_calibration():
@@ -241,6 +283,9 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.vendor_gemm:
+        vendor_gemm()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the "
               "transformer evaluation shards as independent positions per GPU with no "
@@ -285,7 +330,15 @@ def main():
     prof = run.profile(B, args.steps)
     gemm = gemm_totals(prof)
     achieved = gemm["flops"] / (gemm["ms"] * 1e-3) / 1e12 if gemm["ms"] else 0.0
+    # MFMA work per algorithmic FLOP: 1 (bf16), 2 (bf16 pairs), 1.5 for the
+    # encoder GEMMs with the fp8 lo correction (an fp8 MFMA does a bf16 one's
+    # work in half the time).
     mfma_mult = 1.0 if args.precision == "bf16" else 2.0
+
+    def role_mult(role):
+        if args.precision == "bf16x2_fp8lo" and role in ("qkv", "out", "ffn2"):
+            return 1.5
+        return mfma_mult
     total_prof_ms = sum(v["ms"] for v in prof.values())
     kinds = {}
     for k, v in prof.items():
@@ -304,8 +357,11 @@ def main():
         gemm_roles[k.split(":", 1)[1]] = {
             "ms_per_step": round(v["ms"] / args.steps, 4),
             "alg_tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
-            "mfma_util_pct": round(100.0 * v["flops"] * mfma_mult / (v["ms"] * 1e-3) / 1e12 /
-                                   PEAK_BF16_TFLOPS, 1)}
+            "mfma_util_pct": round(100.0 * v["flops"] * role_mult(k.split(":", 1)[1]) /
+                                   (v["ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 1)}
+    # Whole-GEMM MFMA issue rate: each role's FLOPs times its MFMA work.
+    mfma_flops = sum(v["flops"] * role_mult(k.split(":", 1)[1]) for k, v in prof.items()
+                     if k.startswith("gemm_bf16:"))
 
     # Batch-1 latency (MCTS single-leaf regime) and the other small batches
     # (config 3); weights dominate the traffic, so bandwidth = weight bytes /
@@ -342,10 +398,17 @@ def main():
                 fn()
             return (time.perf_counter() - t) * 1e3 / iters
 
-        logits_ms = wall_ms(lambda: run.net.eval_packed(masks, values))
-        priors_ms = wall_ms(lambda: run.net.eval_priors(masks, values, moves, 1.0))
         offsets = np.zeros(B + 1, np.int32)
         offsets[1:] = np.cumsum([m.size for m in moves])
+        flat_moves = np.ascontiguousarray(np.concatenate(moves), dtype=np.int16)
+        # Host calls with their arguments prepared outside the timing (what
+        # an engine's batch assembly hands over): the C call, its pinned
+        # staging copies and the D2H of logits or of the priors.
+        logits_ms = wall_ms(lambda: run.net.eval_packed(masks, values))
+        priors_ms = wall_ms(lambda: run.net.eval_priors_flat(masks, values, offsets, flat_moves,
+                                                             1.0))
+        # The same with the per-call Python packing of the move lists.
+        priors_py_ms = wall_ms(lambda: run.net.eval_priors(masks, values, moves, 1.0))
         d_off = torch.from_numpy(offsets).cuda()
         d_idx = torch.from_numpy(np.concatenate(moves)).cuda()
         d_priors = torch.empty(int(offsets[-1]), dtype=torch.float32, device="cuda")
@@ -374,7 +437,8 @@ def main():
         mcts = {"batch": B, "moves_per_position": round(avg_moves, 2),
                 "d2h_bytes_per_position": {"logits": 1858 * 4 + 12,
                                            "priors": round(avg_moves * 4 + 12, 1)},
-                "host_call_ms": {"logits": round(logits_ms, 4), "priors": round(priors_ms, 4)},
+                "host_call_ms": {"logits": round(logits_ms, 4), "priors": round(priors_ms, 4),
+                                 "priors_with_python_move_packing": round(priors_py_ms, 4)},
                 "device_forward_ms": round(fwd_ms, 4),
                 "device_forward_plus_priors_ms": round(fwd_priors_ms, 4)}
     run.close()
@@ -430,7 +494,7 @@ def main():
     # The other activation precisions at the headline batch.
     precisions = {}
     if not args.no_extras:
-        for prec in ("bf16x2", "bf16x2_gemm", "bf16"):
+        for prec in ("bf16x2", "bf16x2_fp8lo", "bf16x2_gemm", "bf16"):
             if prec == args.precision:
                 continue
             r = Runner(backend, torch, np, spec, weights, masks, values, B, prec, stream)
@@ -460,6 +524,21 @@ def main():
                "batch1_weight_stream_gbs": round(wb / (p50 * 1e-3) / 1e9, 1),
                "mma": "bf16 MFMA on exactly converted e4m3 weights (bf16x2 activations)"}
         backend_fp8.close()
+        # The same e4m3 weights on the fp8 MFMA within the parity gates:
+        # BF16X2_FP8LO (hi products on the bf16 MFMA over the exactly
+        # converted codes, the e4m3 lo parts times the codes on the fp8 MFMA).
+        rlo = Runner(backend, torch, np, spec, fweights, masks, values, fb, "bf16x2_fp8lo",
+                     stream, weights_dtype="fp8")
+        mslo = rlo.time_steps(fb, max(3, args.steps // 4), 2)
+        rlo.close()
+        fp8["fp8_mfma_within_gates"] = {
+            "precision": "bf16x2_fp8lo", "positions_per_s": round(fb / (mslo * 1e-3), 1),
+            "ms_per_step": round(mslo, 4),
+            "mma": "bf16 MFMA for the activations' hi parts times the converted codes, fp8 MFMA "
+                   "(v_mfma_f32_16x16x128_f8f6f4) for their e4m3 lo parts times the codes, "
+                   "accumulated together, in the encoder's Q|K|V, out-projection and FFN2",
+            "parity": "gates met: policy max-abs 2.6e-4, WDL 2.7e-5, top-1 0.996 at batch 1024 "
+                      "(test_gpu_lo8.py::test_forward_gates[fp8-1024])"}
         # The FP8 precision: e4m3 activations (per-row scales) into the body's
         # Q|K|V, out-projection and FFN GEMMs on the fp8 MFMA.  Measured below
         # the parity gates on the random-init net (top-1 0.79-0.83 against
@@ -515,7 +594,8 @@ def main():
             "avg_launch_us": round(gemm["ms"] * 1e3 / max(1, gemm["launches"]), 3),
             "algorithmic_bytes_per_launch": round(gemm["bytes"] / max(1, gemm["launches"])),
         },
-        "mfma_util_pct": round(100.0 * achieved * mfma_mult / PEAK_BF16_TFLOPS, 2),
+        "mfma_util_pct": round(100.0 * mfma_flops / (gemm["ms"] * 1e-3) / 1e12 /
+                               PEAK_BF16_TFLOPS, 2) if gemm["ms"] else 0.0,
         "whole_forward_tflops": round(GFLOP_PER_POSITION * value / 1e3, 2),
         "latency_batch1_ms": None if lat1 is None else {
             "p50": round(float(np.percentile(lat1, 50)), 4),

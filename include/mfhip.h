@@ -117,10 +117,10 @@ typedef struct {
   int pol_headcount;      /* policy encoder heads (Weights.pol_headcount); 0 without
                              policy encoder layers */
   int fused_layernorm;    /* residual GEMM + the LayerNorm after it as one
-                             row-panel launch (batches >= 128, split precisions):
-                             1 always; 0 chooses as measured on MI355X: on with
-                             fp8 weights, off with bf16 weights (tiled GEMM,
-                             then the LayerNorm kernel) */
+                             row-panel launch (batches >= 128, BF16X2 and
+                             BF16X2_GEMM): 1 always; 0 chooses as measured on
+                             MI355X: on with fp8 weights, off with bf16 weights
+                             (tiled GEMM, then the LayerNorm kernel) */
 } mfh_net_desc;
 
 /* One weight tensor, named as in the reference's weight inventory
@@ -255,8 +255,11 @@ int mfh_net_capabilities(const mfh_net *net, mfh_capabilities *out);
  * reference src/nn/network.h:58 and cuda_network.cpp:312): when enabled (the
  * default), the forward for a batch size and set of device buffers runs
  * eagerly once and is then captured into a HIP graph that later calls
- * replay with a single launch.  Profiling bypasses graphs.  Changing the
- * setting drops the cached graphs. */
+ * replay with a single launch.  A net caches up to 64 graphs (one per batch
+ * size and buffer set of mfh_net_eval_device; mfh_net_eval's pinned buffers
+ * are one set); keys seen after the cache is full run eagerly, without a
+ * capture, and the cached graphs stay.  Profiling bypasses graphs.
+ * Changing the setting drops the cached graphs. */
 int mfh_net_set_graphs(mfh_net *net, int enabled);
 
 /* Stage profiler (the counterpart of the reference's METALFISH_CUDA_PROFILE

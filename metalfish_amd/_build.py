@@ -110,7 +110,7 @@ def build_adapter():
     _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", *inc, src,
           "-L" + PKG, "-lmfhip", "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
-    test_src = os.path.join(CSRC, "host", "hip_network_test.cpp")
+    test_src = os.path.join(ROOT, "tests", "native", "hip_network_test.cpp")
     if os.path.exists(test_src):
         exe = os.path.join(PKG, "hip_network_test")
         _run(["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", *inc, test_src,

@@ -282,6 +282,19 @@ class HipNetwork:
             value_out.append(value)
         return priors_out, np.concatenate(value_out)
 
+    def eval_priors_flat(self, masks, values, offsets, indices, softmax_temp=1.0):
+        """One mfh_net_eval_priors call on prepared arrays (batch <= max_batch):
+        offsets int32 [B + 1], indices int16 [offsets[B]].  Returns (priors
+        float32 [offsets[B]], raw value head output)."""
+        b = masks.shape[0]
+        priors = np.zeros(max(1, int(offsets[-1])), np.float32)
+        value = np.zeros((b, 3 if self.wdl else 1), np.float32)
+        _check(lib().mfh_net_eval_priors(self._h, b, _ptr(masks), _ptr(values), _ptr(offsets),
+                                         _ptr(indices), float(softmax_temp), _ptr(priors),
+                                         _ptr(value), None),
+               "mfh_net_eval_priors")
+        return priors[:int(offsets[-1])], value
+
     def eval_priors_device(self, batch, d_masks, d_values, d_offsets, d_indices, softmax_temp,
                            d_policy, d_priors, d_wdl, stream=None):
         """Device-resident form of eval_priors (pointers are device addresses)."""

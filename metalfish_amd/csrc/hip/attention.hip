@@ -40,9 +40,12 @@ namespace {
 constexpr int kSq = 64;
 constexpr int kDepth = 32;
 constexpr int kHeadsPerBlock = 4;
-// V^T rows: 64 keys plus 8 of padding, so the two halves of a wave writing
-// depths d and d + 16 land on different banks.
-constexpr int kVtStride = kSq + 8;
+// V^T rows: 64 keys plus 4 of padding (34 dwords per depth).  The P.V
+// fragment reads (8 bytes per lane at dword 34 (16 dt + fr) + 16 u + 2 g)
+// then spread each quarter wave over all 32 four-byte banks: with 36-dword
+// rows (8 of padding) lanes fr and fr + 8 shared banks, and the counters read
+// 4 conflict cycles per LDS instruction.
+constexpr int kVtStride = kSq + 4;
 // Context staging tile: 16 queries x (4 heads x 32 depths) bf16 per plane,
 // rows of 16 chunks of 16 bytes, chunk c of row r stored at c ^ r.
 constexpr int kCtxCols = kHeadsPerBlock * kDepth;

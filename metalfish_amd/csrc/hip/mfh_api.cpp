@@ -221,7 +221,6 @@ struct Dims {
   bool skinny = true;       // few-row GEMMs for single-position forwards
   bool fp8_act = false;     // e4m3 activations on the fp8 MFMA (FP8 precision)
   bool lo8 = false;         // BF16X2_FP8LO: e4m3 lo parts on the fp8 MFMA
-  bool lo8_ffn1 = false;    // ... also on FFN1 (else its BF16X2 GEMM, lo8 output)
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
   float alpha = 1.f, eps_body = 1e-3f;
 };
@@ -509,8 +508,10 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
             desc.precision == MFH_PRECISION_BF16X2_GEMM || d.lo8;
   d.split_attn = desc.precision == MFH_PRECISION_BF16X2 || d.lo8;
   // Measured at the BT4 shape: the panel wins with e4m3 weights (half the
-  // weight bytes to stream), the tiled GEMM + LayerNorm kernel with bf16.
-  // The panel has no fp8 lo correction: BF16X2_FP8LO keeps the tiled GEMM.
+  // weight bytes to stream; batch 1024 22.29k against 22.09k positions/s
+  // for the tiled GEMM + LayerNorm, batch 256 even), the tiled GEMM +
+  // LayerNorm kernel with bf16.  The panel has no fp8 lo correction:
+  // BF16X2_FP8LO keeps the tiled GEMM.
   d.fused_ln = !d.lo8 && (desc.fused_layernorm != 0 || desc.weights_dtype == MFH_WEIGHTS_FP8);
   d.wdl = desc.value == MFH_VALUE_WDL;
   d.mlh = desc.moves_left == 1;
@@ -621,8 +622,6 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // METALFISH_HIP_SMOLGEN_BIAS=attention the attention kernel generates the
   // bias itself (gen widths 64, 128 or 256) and no bias tensor exists.
   const char *bias_env = std::getenv("METALFISH_HIP_SMOLGEN_BIAS");
-  const char *ffn1_env = std::getenv("METALFISH_HIP_LO8_FFN1");
-  d.lo8_ffn1 = ffn1_env && ffn1_env[0] == '1';
   d.fused_bias = d.smolgen && !d.lo8 && bias_env && std::string(bias_env) == "attention" &&
                  (d.G == 64 || d.G == 128 || d.G == 256) &&
                  mfh::AttentionSmolgenLds(d.G, d.split_attn) <= 160 * 1024;
@@ -694,6 +693,18 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     if (g)
       net->add_gate = AddF32(blob, {g}, {E * S});
   }
+  // The body's dense weights (input-embedding FFN, encoder layers); with
+  // BF16X2_FP8LO they also carry e4m3 codes for the fp8 lo correction
+  // (AddGemmWLo8), and every GEMM on them applies their column scales.
+  auto dense_w = [&](const std::vector<const float *> &parts, const std::vector<int> &rows,
+                     int cols, int ldw) {
+    if (!d.lo8)
+      return AddGemmW(blob, net->fp8, parts, rows, cols, ldw);
+    size_t codes = 0;
+    const GemmW g = AddGemmWLo8(blob, net->fp8, parts, rows, cols, ldw, &codes);
+    net->lo8_codes[g.w] = codes;
+    return g;
+  };
   if (d.input_ffn) {
     const float *w1 = need("body.ip_emb_ffn.dense1_w", static_cast<size_t>(d.Fi) * E);
     const float *b1 = need("body.ip_emb_ffn.dense1_b", d.Fi);
@@ -703,9 +714,9 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     const float *b = need("body.ip_emb_ffn_ln_betas", E);
     if (!ld.error.empty())
       return SetError(MFH_ERR_INVALID, ld.error);
-    SetW(net->in_ffn1_w, AddGemmW(blob, net->fp8, {w1}, {d.Fi}, E, E));
+    SetW(net->in_ffn1_w, dense_w({w1}, {d.Fi}, E, E));
     net->in_ffn1_b = AddF32(blob, {b1}, {d.Fi});
-    SetW(net->in_ffn2_w, AddGemmW(blob, net->fp8, {w2}, {E}, d.Fi, d.Fi));
+    SetW(net->in_ffn2_w, dense_w({w2}, {E}, d.Fi, d.Fi));
     net->in_ffn2_b = AddF32(blob, {b2}, {E});
     net->in_ln_g = AddF32(blob, {g}, {E});
     net->in_ln_b = AddF32(blob, {b}, {E});
@@ -737,18 +748,7 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       cw = need(p + ".mha.smolgen.compress", static_cast<size_t>(d.C) * E);
     if (!ld.error.empty())
       return SetError(MFH_ERR_INVALID, ld.error);
-    // BF16X2_FP8LO: the four dense weights of the layer also carry e4m3
-    // codes for the fp8 lo correction (AddGemmWLo8); every GEMM on them
-    // then applies their column scales.
-    auto gemm_w = [&](const std::vector<const float *> &parts, const std::vector<int> &rows,
-                      int cols, int ldw) {
-      if (!d.lo8)
-        return AddGemmW(blob, net->fp8, parts, rows, cols, ldw);
-      size_t codes = 0;
-      const GemmW g = AddGemmWLo8(blob, net->fp8, parts, rows, cols, ldw, &codes);
-      net->lo8_codes[g.w] = codes;
-      return g;
-    };
+    auto &gemm_w = dense_w;
     SetW(L.qkv_w, gemm_w({qw, kw, vw, cw}, {E, E, E, smolgen ? d.C : 0}, E, E));
     L.qkv_b = AddF32(blob, {qb, kb, vb, nullptr}, {E, E, E, smolgen ? d.C : 0});
     SetW(L.out_w, gemm_w({ow}, {E}, E, E));
@@ -1167,10 +1167,20 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // e4m3 lo codes, attention and FFN1 write theirs instead of bf16 lo planes,
   // and the encoder GEMMs on those inputs add the fp8 lo product.
   const bool lo8 = d.lo8 && M >= kLo8MinRows && ws.Has("act_lo8");
+  // The "act" codes are written when Q|K|V or FFN1 takes them (whole rounds
+  // of 256 x 256 tiles, as lo8_gemm below decides).
+  const auto whole_round = [](int m, int n) {
+    mfh::GemmParams q;
+    q.M = m;
+    q.N = n;
+    return mfh::GemmWholeRoundTiles(q);
+  };
+  const bool lo8_act =
+      lo8 && (whole_round(M, 3 * E) || whole_round(M, d.F) || (d.input_ffn && whole_round(M, d.Fi)));
   auto ln = [&](const float *x, int rows, int width, float eps, const float *g, const float *b,
                 float *y32, const std::string &y16) {
     mfh::LayerNormParams lp;
-    if (lo8 && y16 == "act")
+    if (lo8_act && y16 == "act")
       lp.y_lo8 = ws.S<std::uint8_t>("act_lo8");
     lp.x = x;
     lp.rows = rows;
@@ -1249,9 +1259,17 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // BF16X2_FP8LO: the GEMM on workspace input `a` (hi plane + e4m3 lo codes
   // "<a>_lo8") with the codes of weight w_off for the fp8 lo product; false
   // (p unchanged) where this forward or weight has none.
+  // Whether an encoder GEMM of m x n on weight w_off takes the fp8 lo
+  // correction: its 256 x 256 tiles (the only tiles of that kernel) must fill
+  // whole rounds of 256 workgroups; elsewhere (batch 256 FFN1 at 1.5 rounds,
+  // batch 128) the BF16X2 tiles were faster.  Producers write e4m3 lo codes
+  // exactly where their consumer takes them.
+  auto lo8_gemm = [&](int m, int n, const size_t (&w_off)[2]) {
+    return lo8 && net->lo8_codes.count(w_off[0]) && whole_round(m, n);
+  };
   auto use_lo8 = [&](mfh::GemmParams &p, const std::string &a, const size_t (&w_off)[2]) {
     const auto it = net->lo8_codes.find(w_off[0]);
-    if (!lo8 || it == net->lo8_codes.end())
+    if (!lo8_gemm(p.M, p.N, w_off) || (a == "act" && !lo8_act))
       return false;
     p.A_lo = nullptr;
     p.A_lo8 = ws.S<std::uint8_t>(a + "_lo8");
@@ -1367,10 +1385,16 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     return MFH_OK;
   };
   if (full && d.input_ffn) {
-    MFH_RUN(run(gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E, net->W<float>(net->in_ffn1_b),
-                     d.act_ffn, mfh::GEMM_OUT_BF16, ws.S<std::uint16_t>("hid"),
-                     ws.Lo("hid"), d.Fi),
-                "input_ffn1"));
+    mfh::GemmParams pi = gemm("act", E, net->in_ffn1_w, E, M, d.Fi, E,
+                              net->W<float>(net->in_ffn1_b), d.act_ffn, mfh::GEMM_OUT_BF16,
+                              ws.S<std::uint16_t>("hid"), ws.Lo("hid"), d.Fi);
+    use_lo8(pi, "act", net->in_ffn1_w);
+    if (lo8_gemm(M, E, net->in_ffn2_w)) {
+      pi.C_lo = nullptr;
+      pi.C_lo8 = ws.S<std::uint8_t>("hid_lo8");
+      pi.ldc8 = d.Fi;
+    }
+    MFH_RUN(run(pi, "input_ffn1"));
     const int rc = residual_ln("hid", d.Fi, net->in_ffn2_w, net->W<float>(net->in_ffn2_b),
                                "input_ffn2", d.alpha, 1e-3f, net->W<float>(net->in_ln_g),
                                net->W<float>(net->in_ln_b), res32);
@@ -1536,7 +1560,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     ap.heads = heads;
     ap.ctx = ws.S<std::uint16_t>("ctx");
     ap.ctx_lo = ws.Lo("ctx");
-    if (lo8 && net->lo8_codes.count(L.out_w[0])) {
+    if (lo8_gemm(M, E, L.out_w)) {
       ap.ctx_lo = nullptr;
       ap.ctx_lo8 = ws.S<std::uint8_t>("ctx_lo8");
     }
@@ -1702,13 +1726,14 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     if (f8) {
       MFH_RC(quant("act", E));
       use_fp8(pf, "act");
-    } else if (lo8 && net->lo8_codes.count(L.ffn2_w[0])) {
-      // FFN2 adds the fp8 lo product: FFN1 writes its lo parts as codes.
-      if (d.lo8_ffn1)
-        use_lo8(pf, "act", L.ffn1_w);
-      pf.C_lo = nullptr;
-      pf.C_lo8 = ws.S<std::uint8_t>("hid_lo8");
-      pf.ldc8 = ffn;
+    } else {
+      use_lo8(pf, "act", L.ffn1_w);
+      if (lo8_gemm(M, E, L.ffn2_w)) {
+        // FFN2 adds the fp8 lo product: FFN1 writes its lo parts as codes.
+        pf.C_lo = nullptr;
+        pf.C_lo8 = ws.S<std::uint8_t>("hid_lo8");
+        pf.ldc8 = ffn;
+      }
     }
     MFH_RUN(run(pf, "ffn1"));
     rc = residual_ln("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, eps_ffn,
@@ -1864,6 +1889,9 @@ int EndUse(mfh_net *net, hipStream_t st) {
   return MFH_OK;
 }
 
+// Graphs cached per net (batch size and device buffers as the key).
+constexpr int kMaxGraphs = 64;
+
 // Forward through a cached HIP graph (captured on the net's capture stream,
 // launched on `st`), or eagerly while profiling, for a key's first run, or
 // when graphs are off.  A graph bakes in the batch size and the buffers.
@@ -1875,11 +1903,16 @@ int RunForward(mfh_net *net, int B, const std::uint64_t *masks, const float *val
   auto it = net->graph_execs.find(key);
   if (it == net->graph_execs.end()) {
     if (!net->graph_warm.count(key)) {
+      if (net->graph_warm.size() >= static_cast<size_t>(16 * kMaxGraphs))
+        net->graph_warm.clear();
       net->graph_warm.insert(key);
       return Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, st);
     }
-    if (net->graph_execs.size() >= 64)
-      DropGraphs(net);
+    // The cache is full: this key runs eagerly (no capture), so a caller
+    // rotating through more buffer sets than the cache holds pays no
+    // capture on every call, and the cached keys keep their graphs.
+    if (net->graph_execs.size() >= static_cast<size_t>(kMaxGraphs))
+      return Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, st);
     hipGraph_t graph = nullptr;
     MFH_HIP_CHECK(hipStreamBeginCapture(net->capture_stream, hipStreamCaptureModeThreadLocal));
     const int rc = Forward(net, MainWs(net), B, masks, values, policy, wdl, moves_left, net->capture_stream);
