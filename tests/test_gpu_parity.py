@@ -363,6 +363,33 @@ def test_graph_replay_matches_eager():
     net.close()
 
 
+def test_graph_cache_past_its_capacity():
+    """mfh_net_eval_device with more output buffer sets than the net caches
+    graphs for (64): the first keys are captured and replayed, later keys run
+    eagerly, and every call gives the eager bits, including the cached keys
+    revisited after the cache filled."""
+    spec = synth.SPECS["cpu_plumbing"]
+    weights = synth.make_weights(spec, seed=6)
+    planes, _ = synth.playout_positions(2, seed=6)
+    masks, values = backend.pack_planes(planes)
+    net = backend.create_network(spec, weights, max_batch=2, device=0)
+    ref = net.eval_packed(masks, values)
+    dev = gpu_util.DeviceBuffers()
+    stream = dev.stream()
+    d_m, d_v = dev.put(masks), dev.put(values)
+    pol0 = np.zeros((2, 1858), np.float32)
+    wdl0 = np.zeros((2, 3), np.float32)
+    outs = [(dev.put(pol0), dev.put(wdl0)) for _ in range(70)]
+    for rep in range(3):  # eager first run, capture (first 64 keys), replays
+        for i, (d_p, d_w) in enumerate(outs):
+            net.eval_device(2, d_m, d_v, d_p, d_w, stream=stream)
+            dev.sync(stream)
+            assert np.array_equal(dev.get(d_p, pol0), ref[0]), (rep, i)
+            assert np.array_equal(dev.get(d_w, wdl0), ref[1]), (rep, i)
+    dev.free()
+    net.close()
+
+
 def test_bt4_net_from_network_file(tmp_path):
     """A BT4-shape net written as a .pb network file and read back through
     mfh_weights_load gives the same device results, bit for bit, as the net
