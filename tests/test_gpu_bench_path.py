@@ -27,14 +27,10 @@ random-init nets the two best legal logits of some positions lie within
 flip a few of them (bf16x2_gemm: 1-3 of 256, bf16: ~10).
 """
 
-import os
-import time
-
 import numpy as np
 import pytest
 
 import gpu_util
-import oracle
 from metalfish_amd import backend, synth
 
 pytestmark = pytest.mark.gpu
@@ -53,18 +49,12 @@ def _need_gpu():
 
 
 @pytest.fixture(scope="module")
-def bt4():
+def bt4(bt4_bench_oracle):
     """The bench's net and positions, with the oracle's outputs for all 256."""
     spec = synth.SPECS["bt4"]
-    weights = synth.make_weights(spec, seed=0)
-    planes, legal = synth.playout_positions(N_POSITIONS, seed=0)
+    weights, planes, legal, ref = bt4_bench_oracle(False)
+    assert planes.shape[0] == N_POSITIONS
     assert len({p.tobytes() for p in planes}) == N_POSITIONS  # all distinct
-    threads = min(16, os.cpu_count() or 1)
-    t0 = time.time()
-    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads),
-                           weights).evaluate_batch(planes, threads=threads)
-    print(f"oracle: {N_POSITIONS} BT4 positions on {threads} threads in "
-          f"{time.time() - t0:.1f} s", flush=True)
     masks, values = backend.pack_planes(planes)
     return dict(spec=spec, weights=weights, planes=planes, legal=legal, ref=ref,
                 masks=masks, values=values)

@@ -27,14 +27,10 @@ legal move on >= 99.5 % of positions; WDL max-abs <= 5e-3
 (tools/compare_nn_backend_outputs.py:21-22 in the reference).
 """
 
-import os
-import time
-
 import numpy as np
 import pytest
 
 import gpu_util
-import oracle
 from metalfish_amd import backend, synth
 
 pytestmark = pytest.mark.gpu
@@ -63,20 +59,13 @@ def _bits(a):
 
 
 @pytest.mark.timeout(900)
-def test_config5_fp8_weights_batch_1024():
+def test_config5_fp8_weights_batch_1024(bt4_bench_oracle):
     """Config 5 as bench.py runs it: e4m3 weights, bf16x2 activations,
     batch 1024 from the 256 bench positions repeated, mfh_net_eval_device
     with graph replay."""
     spec = synth.SPECS["bt4"]
-    weights = synth.make_weights(spec, seed=0, fp8=True)
+    weights, planes, legal, ref = bt4_bench_oracle(True)
     n, B = 256, 1024
-    planes, legal = synth.playout_positions(n, seed=0)
-    threads = min(16, os.cpu_count() or 1)
-    t0 = time.time()
-    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads),
-                           weights).evaluate_batch(planes, threads=threads)
-    print(f"oracle: {n} fp8-weight BT4 positions on {threads} threads in "
-          f"{time.time() - t0:.1f} s", flush=True)
     masks, values = backend.pack_planes(planes)
     idx = np.arange(B) % n
     net = backend.create_network(spec, weights, max_batch=B, device=0, weights_dtype="fp8",

@@ -14,14 +14,10 @@ plus the lo product on the fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4).
   on bf16 and on e4m3 weights, and graph replays equal the eager forward.
 """
 
-import os
-import time
-
 import numpy as np
 import pytest
 
 import gpu_util
-import oracle
 from metalfish_amd import backend, synth
 
 pytestmark = pytest.mark.gpu
@@ -123,17 +119,6 @@ def positions():
     return dict(planes=planes, legal=legal, masks=masks, values=values)
 
 
-def _oracle(weights, planes):
-    spec = synth.SPECS["bt4"]
-    threads = min(16, os.cpu_count() or 1)
-    t0 = time.time()
-    ref = oracle.OracleNet(oracle.NetFormat(body_heads=spec.heads),
-                           weights).evaluate_batch(planes, threads=threads)
-    print(f"oracle: {planes.shape[0]} BT4 positions on {threads} threads in "
-          f"{time.time() - t0:.1f} s", flush=True)
-    return ref
-
-
 def _device_runs(net, masks, values, runs=4):
     """mfh_net_eval_device on a caller stream: eager run, graph capture and
     replays; returns the outputs of each call."""
@@ -170,16 +155,17 @@ def test_below_threshold_equals_bf16x2(positions):
 
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("weights_dtype,batch", [("bf16", 256), ("bf16", 128), ("fp8", 1024)])
-def test_forward_gates(positions, weights_dtype, batch):
+def test_forward_gates(positions, bt4_bench_oracle, weights_dtype, batch):
     """bf16 weights at batches 256 (the headline shape) and 128 (the first
     batch with the lo correction); e4m3 weights at batch 1024 (config 5: the
     256 bench positions four times over, each copy bit-equal).  Eager run,
     graph capture and two replays bit-equal; gates against the oracle on the
     same (dequantised) weights."""
     spec = synth.SPECS["bt4"]
-    weights = synth.make_weights(spec, seed=0, fp8=weights_dtype == "fp8")
+    weights, planes, _, ref_all = bt4_bench_oracle(weights_dtype == "fp8")
+    assert np.array_equal(planes, positions["planes"])
     n = min(batch, 256)
-    ref = _oracle(weights, positions["planes"][:n])
+    ref = {k: v[:n] for k, v in ref_all.items()}
     idx = np.arange(batch) % n
     net = backend.create_network(spec, weights, max_batch=batch, device=0,
                                  weights_dtype=weights_dtype, precision="bf16x2_fp8lo")
