@@ -60,8 +60,9 @@ __device__ __forceinline__ bf16x8 Join(u32x2 a, u32x2 b) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
-template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
+template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32, bool LO8_IN = false>
 __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
+  static_assert(!LO8_IN || SPLIT, "e4m3 lo inputs are the lo planes of split inputs");
   constexpr int PLANES = SPLIT ? 2 : 1;
   constexpr int OUT_PLANES = SPLIT_OUT ? 2 : 1;
   __shared__ __attribute__((aligned(16))) std::uint16_t vt_lds[kHeadsPerBlock][PLANES]
@@ -90,6 +91,17 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   u32x4 vrow[PLANES][4];
 #pragma unroll
   for (int pl = 0; pl < PLANES; ++pl) {
+    if (LO8_IN && pl == 1) {
+      // The lo plane from its e4m3 codes (16 per row), converted exactly.
+      const std::uint8_t *base = ap.qkv_lo8 + pos + vcol + dh;
+      const u32x4 c0 = *reinterpret_cast<const u32x4 *>(base + (2 * kp) * ld);
+      const u32x4 c1 = *reinterpret_cast<const u32x4 *>(base + (2 * kp + 1) * ld);
+      vrow[1][0] = __builtin_bit_cast(u32x4, Lo8x8ToBf16(u32x2{c0[0], c0[1]}));
+      vrow[1][1] = __builtin_bit_cast(u32x4, Lo8x8ToBf16(u32x2{c0[2], c0[3]}));
+      vrow[1][2] = __builtin_bit_cast(u32x4, Lo8x8ToBf16(u32x2{c1[0], c1[1]}));
+      vrow[1][3] = __builtin_bit_cast(u32x4, Lo8x8ToBf16(u32x2{c1[2], c1[3]}));
+      continue;
+    }
     const std::uint16_t *base = (pl ? ap.qkv_lo : ap.qkv) + pos + vcol + dh;
     const u32x4 *r0 = reinterpret_cast<const u32x4 *>(base + (2 * kp) * ld);
     const u32x4 *r1 = reinterpret_cast<const u32x4 *>(base + (2 * kp + 1) * ld);
@@ -101,18 +113,26 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   // S^T = K Q^T operands: tile (t, q) holds keys 16 t + 4 g + r (rows) for
   // queries 16 q + fr (columns).
   const std::uint16_t *qh = ap.qkv + pos;
-  const std::uint16_t *ql = SPLIT ? ap.qkv_lo + pos : ap.qkv + pos;
+  const std::uint16_t *ql = SPLIT && !LO8_IN ? ap.qkv_lo + pos : ap.qkv + pos;
+  const std::uint8_t *q8 = LO8_IN ? ap.qkv_lo8 + pos : nullptr;
+  // Eight lo values of row `row` from column `col` (bf16 plane or codes).
+  auto load_lo = [&](size_t row, int col) {
+    if constexpr (LO8_IN)
+      return Lo8x8ToBf16(*reinterpret_cast<const u32x2 *>(q8 + row * ld + col));
+    else
+      return *reinterpret_cast<const bf16x8 *>(ql + row * ld + col);
+  };
   bf16x8 kf[4], kl[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     kf[i] = *reinterpret_cast<const bf16x8 *>(qh + (i * 16 + fr) * ld + kcol + g * 8);
     if constexpr (SPLIT)
-      kl[i] = *reinterpret_cast<const bf16x8 *>(ql + (i * 16 + fr) * ld + kcol + g * 8);
+      kl[i] = load_lo(i * 16 + fr, kcol + g * 8);
   }
   auto load_q = [&](int q, bf16x8 &hi, bf16x8 &lo) {
     hi = *reinterpret_cast<const bf16x8 *>(qh + (q * 16 + fr) * ld + qcol + g * 8);
     if constexpr (SPLIT)
-      lo = *reinterpret_cast<const bf16x8 *>(ql + (q * 16 + fr) * ld + qcol + g * 8);
+      lo = load_lo(q * 16 + fr, qcol + g * 8);
   };
   const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
   // Bias of query tile q for the lane's keys 16 t + 4 g .. + 3, t = 0..3.
@@ -320,9 +340,9 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
   }
 }
 
-template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32>
+template <bool SPLIT, bool SPLIT_OUT, bool BIAS_F32, bool LO8_IN = false>
 hipError_t Launch(const AttentionParams &ap, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((AttentionKernel<SPLIT, SPLIT_OUT, BIAS_F32>),
+  hipLaunchKernelGGL((AttentionKernel<SPLIT, SPLIT_OUT, BIAS_F32, LO8_IN>),
                      dim3(grid, 4 / ap.q_tiles), dim3(256), 0, stream, ap);
   return hipGetLastError();
 }
@@ -677,12 +697,14 @@ hipError_t LaunchAttentionSmolgen(const AttentionSmolgenParams &ap, hipStream_t 
 }
 
 hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::string *err) {
-  const bool split = ap.qkv_lo != nullptr;
+  const bool lo8_in = ap.qkv_lo8 != nullptr;
+  const bool split = ap.qkv_lo != nullptr || lo8_in;
   const bool split_out = ap.ctx_lo != nullptr || ap.ctx_lo8 != nullptr;
   if (ap.batch <= 0 || ap.heads <= 0 || ap.heads % kHeadsPerBlock || !ap.qkv || !ap.ctx ||
       Misaligned(ap.qkv, 16) || Misaligned(ap.ctx, 16) ||
       (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
-      (split && (!split_out || Misaligned(ap.qkv_lo, 16))) ||
+      (split && !split_out) || (ap.qkv_lo && Misaligned(ap.qkv_lo, 16)) ||
+      (lo8_in && (ap.qkv_lo || Misaligned(ap.qkv_lo8, 16))) ||
       (ap.ctx_lo && Misaligned(ap.ctx_lo, 16)) || (ap.ctx_lo && ap.ctx_lo8) ||
       (ap.ctx_lo8 && Misaligned(ap.ctx_lo8, 8))) {
     if (err)
@@ -703,6 +725,14 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::s
   // forward 1.36 -> 1.29 ms; batch 40 3.18 -> 3.15).
   if (a.q_tiles == 0)
     a.q_tiles = grid >= 512 ? 4 : grid >= 128 ? 2 : 1;
+  // e4m3 lo inputs (BF16X2_FP8LO): the fp32 bias of the split precision.
+  if (lo8_in && a.bias && !a.bias_f32) {
+    if (err)
+      *err = "attention: e4m3 lo inputs take an fp32 bias";
+    return hipErrorInvalidValue;
+  }
+  if (lo8_in)
+    return Launch<true, true, true, true>(a, grid, stream);
   if (split)
     return a.bias_f32 ? Launch<true, true, true>(a, grid, stream)
                       : Launch<true, true, false>(a, grid, stream);

@@ -84,6 +84,18 @@ __device__ __forceinline__ bf16x8 Fp8x8ToBf16(u32x2 q) {
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// Eight e4m3 lo codes (bytes of q, lowest first: e4m3(lo * 2^kLo8Shift)) as
+// the eight bf16 lo values; exact (an e4m3 value times a power of two is a
+// bf16 value), the conversion applying the power-of-two scale.
+__device__ __forceinline__ bf16x8 Lo8x8ToBf16(u32x2 q) {
+  constexpr float kInv = 1.0f / static_cast<float>(1 << kLo8Shift);
+  const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], kInv, false);
+  const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[0], kInv, true);
+  const auto c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], kInv, false);
+  const auto d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[1], kInv, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // e4m3 codes of four lo parts scaled by 2^kLo8Shift (the BF16X2_FP8LO
 // activation lo plane), round to nearest even, clamped to +-448 first.
 __device__ __forceinline__ unsigned Lo8Pack4(float a, float b, float c, float d) {

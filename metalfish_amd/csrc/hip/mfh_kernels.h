@@ -335,6 +335,9 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream,
 struct AttentionParams {
   const std::uint16_t *qkv = nullptr;
   const std::uint16_t *qkv_lo = nullptr;
+  // Alternatively the lo plane as e4m3 codes of lo * 2^kLo8Shift ([B*64][3E]
+  // bytes, BF16X2_FP8LO), converted exactly to bf16 as it loads.
+  const std::uint8_t *qkv_lo8 = nullptr;
   const void *bias = nullptr;
   int bias_f32 = 0;
   int batch = 0, heads = 0;
