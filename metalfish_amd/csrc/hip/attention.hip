@@ -135,25 +135,24 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       lo = load_lo(q * 16 + fr, qcol + g * 8);
   };
   const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
-  // Bias of query tile q for the lane's keys 16 t + 4 g .. + 3, t = 0..3.
+  // Bias of query tile q for the lane's keys 16 t + 4 g .. + 3, t = 0..3:
+  // SmolgenBiasIndex(16 q + fr, 16 t + 4 g) = (4 q + t) 256 + 4 lane.
   auto load_bias = [&](int q, float (&bb)[4][4]) {
-    const int query = q * 16 + fr;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int key0 = t * 16 + g * 4;
+      const size_t e = bias_off + (q * 4 + t) * 256 + lane * 4;
       if (!ap.bias) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           bb[t][r] = 0.f;
       } else if constexpr (BIAS_F32) {
-        const f32x4 x = *reinterpret_cast<const f32x4 *>(
-            static_cast<const float *>(ap.bias) + bias_off + query * kSq + key0);
+        const f32x4 x = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(ap.bias) + e);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           bb[t][r] = x[r];
       } else {
-        const u32x2 x = *reinterpret_cast<const u32x2 *>(
-            static_cast<const std::uint16_t *>(ap.bias) + bias_off + query * kSq + key0);
+        const u32x2 x =
+            *reinterpret_cast<const u32x2 *>(static_cast<const std::uint16_t *>(ap.bias) + e);
         bb[t][0] = __uint_as_float(x[0] << 16);
         bb[t][1] = __uint_as_float(x[0] & 0xFFFF0000u);
         bb[t][2] = __uint_as_float(x[1] << 16);

@@ -725,6 +725,18 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     const float *g = need("body.smolgen_w", static_cast<size_t>(S) * S * d.G);
     if (!g)
       return SetError(MFH_ERR_INVALID, ld.error);
+    // Output rows (query q, key k at row 64 q + k) in the order attention
+    // reads the bias tensor, so the projection writes that order; the
+    // in-kernel bias reads the rows in their own order.
+    std::vector<float> tiled;
+    if (!d.fused_bias) {
+      tiled.resize(static_cast<size_t>(S) * S * d.G);
+      for (int q = 0; q < S; ++q)
+        for (int k = 0; k < S; ++k)
+          std::memcpy(&tiled[static_cast<size_t>(mfh::SmolgenBiasIndex(q, k)) * d.G],
+                      g + static_cast<size_t>(q * S + k) * d.G, sizeof(float) * d.G);
+      g = tiled.data();
+    }
     SetW(net->global_w, AddGemmW(blob, net->fp8, {g}, {S * S}, d.G, d.G));
   }
   net->layers.resize(d.L);

@@ -328,10 +328,22 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream,
 
 // Multi-head 64x64 attention per (position, head), head depth 32:
 //   ctx = softmax(Q K^T / sqrt(32) + bias) V
-// qkv [B*64, 3E] bf16 (Q | K | V, head h at columns h*32..), bias [B,H,64,64]
-// (bf16, or fp32 when bias_f32) or null, ctx [B*64, E] bf16.  Split
+// qkv [B*64, 3E] bf16 (Q | K | V, head h at columns h*32..), bias [B,H,4096]
+// (bf16, or fp32 when bias_f32; each head's 64 x 64 in SmolgenBiasIndex
+// order) or null, ctx [B*64, E] bf16.  Split
 // precision inputs when qkv_lo is set (then ctx_lo is required); ctx_lo
 // alone splits only the output.
+// Element order of one (position, head)'s 64 x 64 smolgen bias in the
+// tensor attention reads: lane 16 g + f of a wave holds, for query tile q,
+// the four keys 16 t + 4 g .. + 3 of query 16 q + f in each key tile t, so
+// those four are contiguous and a wave's loads for one key tile cover 256
+// contiguous values.  The global projection's output rows are packed in
+// this order, so its GEMM writes the bias directly in it.
+constexpr int SmolgenBiasIndex(int query, int key) {
+  return ((query >> 4) * 4 + (key >> 4)) * 256 + ((((key >> 2) & 3) << 4) + (query & 15)) * 4 +
+         (key & 3);
+}
+
 struct AttentionParams {
   const std::uint16_t *qkv = nullptr;
   const std::uint16_t *qkv_lo = nullptr;
