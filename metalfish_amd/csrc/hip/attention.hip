@@ -33,6 +33,7 @@
 #include "mfh_kernels.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace mfh {
 namespace {
@@ -129,39 +130,71 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     if constexpr (SPLIT)
       kl[i] = load_lo(i * 16 + fr, kcol + g * 8);
   }
-  auto load_q = [&](int q, bf16x8 &hi, bf16x8 &lo) {
+  // A query tile's Q lo fragment as loaded (bf16, or e4m3 codes converted
+  // where the scores use them, so that the next tile's loads stay in flight
+  // while this one is processed).
+  using QLo = std::conditional_t<LO8_IN, u32x2, bf16x8>;
+  auto load_q = [&](int q, bf16x8 &hi, QLo &lo) {
     hi = *reinterpret_cast<const bf16x8 *>(qh + (q * 16 + fr) * ld + qcol + g * 8);
-    if constexpr (SPLIT)
+    if constexpr (LO8_IN)
+      lo = *reinterpret_cast<const u32x2 *>(q8 + (q * 16 + fr) * ld + qcol + g * 8);
+    else if constexpr (SPLIT)
       lo = load_lo(q * 16 + fr, qcol + g * 8);
+  };
+  auto q_lo = [&](const QLo &lo) -> bf16x8 {
+    if constexpr (LO8_IN)
+      return Lo8x8ToBf16(lo);
+    else
+      return lo;
   };
   const size_t bias_off = (static_cast<size_t>(b) * heads + h) * kSq * kSq;
   // Bias of query tile q for the lane's keys 16 t + 4 g .. + 3, t = 0..3:
-  // SmolgenBiasIndex(16 q + fr, 16 t + 4 g) = (4 q + t) 256 + 4 lane.
-  auto load_bias = [&](int q, float (&bb)[4][4]) {
+  // SmolgenBiasIndex(16 q + fr, 16 t + 4 g) = (4 q + t) 256 + 4 lane.  Kept
+  // as loaded (fp32, bf16 pairs, or bf16 pairs + e4m3 lo codes) until the
+  // scores use it, like Q's lo fragment.
+  struct BiasWords {
+    f32x4 f[4];
+    u32x2 h[4];
+    unsigned c[4];
+  };
+  auto load_bias = [&](int q, BiasWords &w) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const size_t e = bias_off + (q * 4 + t) * 256 + lane * 4;
-      if (!ap.bias) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          bb[t][r] = 0.f;
-      } else if constexpr (BIAS_F32) {
-        const f32x4 x = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(ap.bias) + e);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          bb[t][r] = x[r];
+      if constexpr (BIAS_F32) {
+        w.f[t] = ap.bias ? *reinterpret_cast<const f32x4 *>(static_cast<const float *>(ap.bias) + e)
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
       } else {
-        const u32x2 x =
-            *reinterpret_cast<const u32x2 *>(static_cast<const std::uint16_t *>(ap.bias) + e);
-        bb[t][0] = __uint_as_float(x[0] << 16);
-        bb[t][1] = __uint_as_float(x[0] & 0xFFFF0000u);
-        bb[t][2] = __uint_as_float(x[1] << 16);
-        bb[t][3] = __uint_as_float(x[1] & 0xFFFF0000u);
+        w.h[t] = ap.bias ? *reinterpret_cast<const u32x2 *>(
+                               static_cast<const std::uint16_t *>(ap.bias) + e)
+                         : u32x2{0u, 0u};
+        if constexpr (LO8_IN)
+          w.c[t] = ap.bias ? *reinterpret_cast<const unsigned *>(ap.bias_lo8 + e) : 0u;
       }
     }
   };
-  bf16x8 qcur, qlcur;
-  float bcur[4][4];
+  auto bias_tile = [&](const BiasWords &w, int t) -> f32x4 {
+    if constexpr (BIAS_F32) {
+      return w.f[t];
+    } else {
+      f32x4 x{__uint_as_float(w.h[t][0] << 16), __uint_as_float(w.h[t][0] & 0xFFFF0000u),
+              __uint_as_float(w.h[t][1] << 16), __uint_as_float(w.h[t][1] & 0xFFFF0000u)};
+      if constexpr (LO8_IN) {
+        // The e4m3 codes of the lo parts times 2^kLo8Shift (BF16X2_FP8LO).
+        constexpr float kInv = 1.0f / static_cast<float>(1 << kLo8Shift);
+        const auto l01 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w.c[t], kInv, false);
+        const auto l23 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w.c[t], kInv, true);
+        x[0] += l01[0];
+        x[1] += l01[1];
+        x[2] += l23[0];
+        x[3] += l23[1];
+      }
+      return x;
+    }
+  };
+  bf16x8 qcur;
+  QLo qlcur;
+  BiasWords bcur;
   load_q(q0, qcur, qlcur);
   load_bias(q0, bcur);
 
@@ -193,8 +226,9 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     if (qi >= qn)
       break;
     const int q = q0 + qi;
-    bf16x8 qnext, qlnext;
-    float bnext[4][4];
+    bf16x8 qnext;
+    QLo qlnext;
+    BiasWords bnext;
     if (qi + 1 < qn) {
       load_q(q + 1, qnext, qlnext);
       load_bias(q + 1, bnext);
@@ -204,16 +238,19 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     for (int t = 0; t < 4; ++t)
       s[t] = Mfma(kf[t], qcur, f32x4{0.f, 0.f, 0.f, 0.f});
     if constexpr (SPLIT) {
+      const bf16x8 ql_cur = q_lo(qlcur);
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        s[t] = Mfma(kl[t], qcur, Mfma(kf[t], qlcur, s[t]));
+        s[t] = Mfma(kl[t], qcur, Mfma(kf[t], ql_cur, s[t]));
     }
     float v[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4; ++t) {
+      const f32x4 bt = bias_tile(bcur, t);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        v[t][r] = s[t][r] * scale + bcur[t][r];
+        v[t][r] = s[t][r] * scale + bt[r];
+    }
     float m = v[0][0];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -330,11 +367,7 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     if (qi + 1 < qn) {
       qcur = qnext;
       qlcur = qlnext;
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          bcur[t][r] = bnext[t][r];
+      bcur = bnext;
     }
   }
 }
@@ -704,6 +737,7 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::s
       (ap.bias && Misaligned(ap.bias, ap.bias_f32 ? 16 : 8)) ||
       (split && !split_out) || (ap.qkv_lo && Misaligned(ap.qkv_lo, 16)) ||
       (lo8_in && (ap.qkv_lo || Misaligned(ap.qkv_lo8, 16))) ||
+      (ap.bias_lo8 && (!lo8_in || ap.bias_f32 || !ap.bias || Misaligned(ap.bias_lo8, 4))) ||
       (ap.ctx_lo && Misaligned(ap.ctx_lo, 16)) || (ap.ctx_lo && ap.ctx_lo8) ||
       (ap.ctx_lo8 && Misaligned(ap.ctx_lo8, 8))) {
     if (err)
@@ -724,12 +758,14 @@ hipError_t LaunchAttention(const AttentionParams &ap, hipStream_t stream, std::s
   // forward 1.36 -> 1.29 ms; batch 40 3.18 -> 3.15).
   if (a.q_tiles == 0)
     a.q_tiles = grid >= 512 ? 4 : grid >= 128 ? 2 : 1;
-  // e4m3 lo inputs (BF16X2_FP8LO): the fp32 bias of the split precision.
-  if (lo8_in && a.bias && !a.bias_f32) {
+  // e4m3 lo inputs (BF16X2_FP8LO): an fp32 bias, or bf16 hi + e4m3 lo.
+  if (lo8_in && a.bias && !a.bias_f32 && !a.bias_lo8) {
     if (err)
-      *err = "attention: e4m3 lo inputs take an fp32 bias";
+      *err = "attention: e4m3 lo inputs take an fp32 bias or a bf16 one with e4m3 lo codes";
     return hipErrorInvalidValue;
   }
+  if (lo8_in && a.bias_lo8)
+    return Launch<true, true, false, true>(a, grid, stream);
   if (lo8_in)
     return Launch<true, true, true, true>(a, grid, stream);
   if (split)

@@ -954,6 +954,7 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   if (d.lo8 && M >= static_cast<size_t>(kLo8MinRows)) {
     add("act_lo8", M * d.E);
     add("qkv_lo8", M * 3 * d.E);
+    add("bias_lo8", d.smolgen ? B * d.H * kSquares * kSquares : 256);
     add("ctx_lo8", M * d.E);
     add("hid_lo8", M * (hid ? hid : 1));
   }
@@ -1606,15 +1607,19 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       auto smolgen_global = [&](hipStream_t s) -> int {
         if (d.fused_bias)
           return MFH_OK;
-        // (A bf16 hi + e4m3 lo bias in BF16X2_FP8LO, 3 bytes instead of 4,
-        // made the global projection 9 % faster and attention 16 % slower:
-        // each lane's four-key pieces of hi and codes load as 8- and 4-byte
-        // pieces of sixteen rows.  The bias stays fp32.)
-        MFH_RUN(run(chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H, kSquares * kSquares,
-                               d.G, nullptr,
-                               d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
-                               ws.S<void>("bias"), nullptr, kSquares * kSquares),
-                    "smolgen_global", s));
+        mfh::GemmParams pg = chain_gemm("sg2n", d.G, net->global_w, d.G, B * d.H,
+                                        kSquares * kSquares, d.G, nullptr,
+                                        d.split_attn ? mfh::GEMM_OUT_F32 : mfh::GEMM_OUT_BF16,
+                                        ws.S<void>("bias"), nullptr, kSquares * kSquares);
+        if (qkv_codes) {
+          // BF16X2_FP8LO: the bias as bf16 hi plus the e4m3 codes of its lo
+          // parts (3 bytes instead of fp32's 4, written here and read by
+          // attention).
+          pg.out_mode = mfh::GEMM_OUT_BF16;
+          pg.C_lo8 = ws.S<std::uint8_t>("bias_lo8");
+          pg.ldc8 = kSquares * kSquares;
+        }
+        MFH_RUN(run(pg, "smolgen_global", s));
         return MFH_OK;
       };
       if (side_chain) {
@@ -1670,7 +1675,9 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     };
     if (L.smolgen && !d.fused_bias) {
       ap.bias = ws.S<void>("bias");
-      ap.bias_f32 = d.split_attn ? 1 : 0;
+      ap.bias_f32 = d.split_attn && !qkv_codes ? 1 : 0;
+      if (qkv_codes)
+        ap.bias_lo8 = ws.S<std::uint8_t>("bias_lo8");
     }
     if (L.smolgen && side_chain) {
       if (sg_stream != st) {
@@ -1738,11 +1745,12 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     } else {
       const double heads_total = static_cast<double>(B) * heads;
       const double flops = heads_total * 2.0 * (2.0 * kSquares * kSquares * 32);
-      const double bytes = 2.0 * (d.split_attn ? 2.0 : 1.0) * 3.0 * M * E +
-                           2.0 * plane_mult * M * E +
-                           (ap.bias ? heads_total * kSquares * kSquares *
-                                          (d.split_attn ? 4.0 : 2.0)
-                                    : 0.0);
+      // Bytes per element: bf16 planes 2 each, e4m3 lo codes 1, fp32 4.
+      const double in_b = ap.qkv_lo8 ? 3.0 : d.split_attn ? 4.0 : 2.0;
+      const double out_b = ap.ctx_lo8 ? 3.0 : 2.0 * plane_mult;
+      const double bias_b = ap.bias_lo8 ? 3.0 : ap.bias_f32 ? 4.0 : 2.0;
+      const double bytes = in_b * 3.0 * M * E + out_b * M * E +
+                           (ap.bias ? heads_total * kSquares * kSquares * bias_b : 0.0);
       StageTimer t(net, st, "attention", flops, bytes);
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
     }

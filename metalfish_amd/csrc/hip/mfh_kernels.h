@@ -352,6 +352,9 @@ struct AttentionParams {
   const std::uint8_t *qkv_lo8 = nullptr;
   const void *bias = nullptr;
   int bias_f32 = 0;
+  // With e4m3 lo inputs: the bias as bf16 hi (bias, bias_f32 0) plus the
+  // e4m3 codes of its lo parts times 2^kLo8Shift, in the same order.
+  const std::uint8_t *bias_lo8 = nullptr;
   int batch = 0, heads = 0;
   std::uint16_t *ctx = nullptr;
   std::uint16_t *ctx_lo = nullptr;
