@@ -314,12 +314,16 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     // Context of the tile into the staging buffer (lane: query fr, depths
     // 16 dt + 4 g .. + 3 of this wave's head = half of 16-byte chunk
     // 4 wave + 2 dt + g / 2), then one 16-byte store per plane and thread:
-    // thread t takes chunk t % 16 of query row t / 16.
+    // thread t takes chunk t % 16 of query row t / 16.  Rows 8-15 hold each
+    // chunk's two 8-byte halves swapped: the 16 lanes of one g (queries
+    // 0-15) then write distinct LDS banks (rows fr and fr + 8 share their
+    // chunk's banks, and now take its other half), and the reader swaps
+    // them back.
     std::uint16_t(*stage)[16 * kCtxCols] = ctx_lds[qi & 1];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       const int chunk = (4 * wave + 2 * dt + (g >> 1)) ^ fr;
-      const int off = fr * kCtxCols + chunk * 8 + (g & 1) * 4;
+      const int off = fr * kCtxCols + chunk * 8 + ((g & 1) ^ (fr >> 3)) * 4;
       std::uint16_t hi[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -345,9 +349,11 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       const int row = threadIdx.x >> 4, chunk = threadIdx.x & 15;
       const int src = row * kCtxCols + (chunk ^ row) * 8;
       const size_t idx = out_off + static_cast<size_t>(q * 16 + row) * E + chunk * 8;
-      *reinterpret_cast<u32x4 *>(ap.ctx + idx) = *reinterpret_cast<const u32x4 *>(stage[0] + src);
+      auto unswap = [&](u32x4 x) { return row >= 8 ? u32x4{x[2], x[3], x[0], x[1]} : x; };
+      *reinterpret_cast<u32x4 *>(ap.ctx + idx) =
+          unswap(*reinterpret_cast<const u32x4 *>(stage[0] + src));
       if constexpr (OUT_PLANES > 1) {
-        const u32x4 l = *reinterpret_cast<const u32x4 *>(stage[1] + src);
+        const u32x4 l = unswap(*reinterpret_cast<const u32x4 *>(stage[1] + src));
         if (ap.ctx_lo8) {
           // The lo plane as e4m3 codes of lo * 2^kLo8Shift (rounded from
           // its bf16 value).
