@@ -88,8 +88,11 @@ enum { MFH_WEIGHTS_BF16 = 0, MFH_WEIGHTS_FP8 = 1 };
  * power-of-two (bf16 weights) or its max|row| / 448 (fp8 weights) scale.
  * The lo product carries ~4 of lo's 8 bits; the product is ~2^-13 relative
  * instead of BF16X2's 2^-17, at three quarters of BF16X2's MFMA time.
- * Attention, smolgen, the residual stream and the heads are as in BF16X2;
- * below 8192 rows the whole forward is BF16X2. */
+ * Attention reads the lo parts of Q, K and V as the same e4m3 codes (its
+ * MFMAs stay bf16) and the smolgen bias as bf16 + e4m3 codes of its lo
+ * part; the residual stream and the heads are as in BF16X2.  Below 8192
+ * rows the whole forward is BF16X2.  The embedding and FFN widths must be
+ * multiples of 128 (mfh_net_create returns MFH_ERR_UNSUPPORTED otherwise). */
 enum {
   MFH_PRECISION_BF16 = 0,
   MFH_PRECISION_BF16X2 = 1,

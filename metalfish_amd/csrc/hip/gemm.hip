@@ -39,13 +39,21 @@ namespace mfh {
 namespace {
 
 // Element offset of 16-byte chunk `chunk` of LDS row `row` (rows of BK bf16).
-// BK = 64: 8 chunks per 128-byte row, XOR with row & 7.  BK = 32: two rows
-// per 128 bytes, XOR with (row >> 1) & 3, so rows r..r+7 cover all eight
-// 16-byte bank groups.
+// BK = 64: 8 chunks per 128-byte row, XOR with row & 7 and with 5 when bit 3
+// of the row is set.  Measured on MI355X (LDS bank-conflict cycles per
+// 16-byte read, fragment reads of 16 rows by 4 lane groups, every XOR-linear
+// swizzle of the row's 4 bits tried): row & 7 alone is conflict-free for the
+// bf16 reads (chunks c and 4 + c of lane group c) but costs 4 for the 8-bit
+// K-step reads (chunks 2c and 2c + 1); XOR 1 for bit 3 the reverse; XOR 5
+// none for both.  BK = 32: two rows per 128 bytes, XOR with (row >> 1) & 3,
+// so rows r..r+7 cover all eight 16-byte bank groups.
+__device__ __forceinline__ int Swz64Chunk(int row, int chunk) {
+  return chunk ^ (row & 7) ^ (((row >> 3) & 1) * 5);
+}
 template <int BK>
 __device__ __forceinline__ int Swz(int row, int chunk) {
   if constexpr (BK == 64)
-    return row * 64 + ((chunk ^ (row & 7)) << 3);
+    return row * 64 + (Swz64Chunk(row, chunk) << 3);
   else
     return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3);
 }
@@ -587,8 +595,9 @@ __device__ __forceinline__ void PipelinedLoop(const GemmParams &p, std::uint16_t
 // hi pass (PipelinedLoop) into the same accumulators: A_lo8 . W_lo8^T over
 // the whole K on v_mfma_f32_16x16x128_f8f6f4, 128-byte K steps.  A stage is
 // the BM activation code rows then the BN weight code rows, 128 bytes each,
-// their 16-byte chunks XOR-swizzled with row & 7 (the F8 path's layout);
-// ST2 stages of (BM + BN) * 128 bytes share the kernel's LDS ring.  Lane
+// their 16-byte chunks XOR-swizzled with row & 7 (the F8 path's layout) and
+// the bit 3 of the row as well; ST2 stages of (BM + BN) * 128 bytes share
+// the kernel's LDS ring.  Lane
 // (r, c) of a fragment feeds bytes 32 c .. 32 c + 31 of row r's K step
 // (chunks 2 c and 2 c + 1), for A and W alike.
 template <int BM, int BN, int WM, int WN, int ST2>
@@ -613,9 +622,13 @@ __device__ __forceinline__ void Lo8Loop(const GemmParams &p, std::uint16_t *lds,
   // scalar offset per wave-load and K step address them.  The resource
   // covers the operand's rows exactly: rows past M or N read zeros (they
   // only feed outputs that are never stored).  Lane l takes row l / 8 of a
-  // wave-load and its logical chunk (l % 8) ^ (row & 7), the same for all
-  // its wave-loads.
+  // wave-load and its logical chunk Swz64Chunk(row, l % 8): a wave's loads
+  // start at a multiple of 16 rows, so bit 3 of the row is the parity of
+  // the wave-load, and the odd ones flip bits 4 and 6 of the offset (the
+  // chunk's bits 0 and 2; the row offsets are multiples of 128 bytes:
+  // ld % 128 == 0).
   static_assert(BM % (8 * LPW) == 0, "a wave's loads stay inside one operand");
+  static_assert(LPW % 2 == 0 && BM % 16 == 0, "a wave's loads start at a multiple of 16 rows");
   const bool w_rows = wave * LPW * 8 >= BM;
   const int row0 = wave * LPW * 8 - (w_rows ? BM : 0);  // first row of the wave's loads
   const int ld = w_rows ? p.ldw8 : p.lda8;
@@ -623,13 +636,15 @@ __device__ __forceinline__ void Lo8Loop(const GemmParams &p, std::uint16_t *lds,
       const_cast<std::uint8_t *>(w_rows ? p.W_lo8 : p.A_lo8), 0,
       static_cast<int>((w_rows ? p.N : p.M) * static_cast<long>(ld)), 0x00020000);
   const unsigned goff =
-      static_cast<unsigned>((w_rows ? n0 : m0) + row0 + lane / 8) * ld + ((lane % 8) ^ (lane / 8)) * 16;
+      static_cast<unsigned>((w_rows ? n0 : m0) + row0 + lane / 8) * ld +
+      Swz64Chunk(lane / 8, lane % 8) * 16;
   const int ldsw = __builtin_amdgcn_readfirstlane(wave * LPW * 512);  // 16-bit units
   auto fill = [&](int s, int slot) {
     std::uint16_t *d = lds + slot * STAGE + ldsw;
 #pragma unroll
     for (int j = 0; j < LPW; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, MFH_LDS_PTR(d + j * 512), 16, goff,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, MFH_LDS_PTR(d + j * 512), 16,
+                                               (j & 1) ? goff ^ 80u : goff,
                                                s * 128 + j * 8 * ld, 0, 0);
   };
   // The hi pass's fragment reads of the ring are done before it is refilled.
@@ -759,7 +774,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     } else {
       const int row = L * RPL + lane / CPR;
       const int phys = lane % CPR;
-      const int chunk = BK == 64 ? (phys ^ (row & 7)) : (phys ^ ((row >> 1) & 3));
+      const int chunk = BK == 64 ? Swz64Chunk(row, phys) : (phys ^ ((row >> 1) & 3));
       const std::uint16_t *s16;
       if (row < BM) {
         s16 = p.A + static_cast<size_t>(min(m0 + row, p.M - 1)) * p.lda + k_begin + chunk * 8;
@@ -1017,12 +1032,28 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   // (fp32: two 16-byte stores per lane).  (The residual mode keeps the loop
   // below: requesting a chunk's residual rows ahead of the staging measured
   // slower.)
+  // 256-wide tiles (32 column groups per row): a wave's 64 lanes read two
+  // half rows of 16 groups each, lanes 16-31 the next row and lanes 32-63
+  // the right halves (a wave reading one whole row measured 4 LDS
+  // bank-conflict cycles per 16-byte read on MI355X; this order none).  A
+  // thread's group for index g (g % 64 its lane): row 2 (g / 64) + bit 4 of
+  // g, group (g % 16) + 16 (bit 5 of g).
+  auto group_of = [&](int g, int &rl, int &c8) {
+    if constexpr (GPR == 32) {
+      rl = 2 * (g >> 6) + ((g >> 4) & 1);
+      c8 = ((g & 15) + ((g >> 5) & 1) * 16) * 8;
+    } else {
+      rl = g / GPR;
+      c8 = (g % GPR) * 8;
+    }
+  };
   constexpr int THREADS = NWAVES * 64;
   if constexpr (MODE != GEMM_OUT_RESID_F32 && THREADS % GPR == 0 &&
                 (RB * GPR) % THREADS == 0) {
     constexpr int ITER = RB * GPR / THREADS;
     constexpr int RSTEP = THREADS / GPR;
-    const int c8 = (tid % GPR) * 8, r0 = tid / GPR;
+    int c8, r0;
+    group_of(tid, r0, c8);
     const int col = n0 + c8;
     if (p.vec8 && n0 + BN <= p.N && (n0 + BN <= p.split_n || n0 >= p.split_n)) {
       float b[8], sc[8];
@@ -1077,7 +1108,8 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   for (int pass = 0; pass < BM / RB; ++pass) {
     stage(pass);
     for (int g = tid; g < RB * GPR; g += NWAVES * 64) {
-      const int rl = g / GPR, c8 = (g % GPR) * 8;
+      int rl, c8;
+      group_of(g, rl, c8);
       const int row = m0 + pass * RB + rl, col = n0 + c8;
       if (row >= p.M || col >= p.N)
         continue;
@@ -1263,10 +1295,10 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   GemmParams p = p_in;
   const bool lo8 = p.A_lo8 != nullptr;
   if (lo8 && (!p.A || p.A_lo || !p.W || p.W8 || !p.wscale || !p.W_lo8 || p.A8 ||
-              p.k_splits != 1 || p.K % 128 || p.lda8 % 16 || p.ldw8 % 16 || p.lda8 < p.K ||
+              p.k_splits != 1 || p.K % 128 || p.lda8 % 128 || p.ldw8 % 128 || p.lda8 < p.K ||
               p.ldw8 < p.K || !Aligned(p.A_lo8, 16) || !Aligned(p.W_lo8, 16)))
     return fail("fp8 lo correction needs A (hi) + A_lo8 with W (bf16) + W_lo8 + wscale, "
-                "one K slice, K % 128 == 0, lda8 / ldw8 % 16 == 0 and 16-byte aligned codes");
+                "one K slice, K % 128 == 0, lda8 / ldw8 % 128 == 0 and 16-byte aligned codes");
   const bool f8 = p.A8 != nullptr;
   if (f8) {
     // fp8 activations x fp8 weights: the byte operands go through the bf16

@@ -629,6 +629,17 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // unless METALFISH_HIP_SKINNY=0, which keeps the split-K path at batch 1).
   const char *skinny_env = std::getenv("METALFISH_HIP_SKINNY");
   d.skinny = !(skinny_env && skinny_env[0] == '0');
+  // BF16X2_FP8LO: the lo pass of the encoder GEMMs takes 128-byte K steps
+  // over code rows laid out 128-byte aligned (K = the embedding and FFN
+  // widths, in the body, the input-embedding FFN and policy encoder layers).
+  if (d.lo8) {
+    for (const int w : {d.E, d.F, d.input_ffn ? d.Fi : d.E, d.PL ? d.PF : d.F}) {
+      if (w % 128)
+        return SetError(MFH_ERR_UNSUPPORTED,
+                        "the BF16X2_FP8LO precision needs embedding and FFN widths that "
+                        "are multiples of 128");
+    }
+  }
   // FP8 precision: the row quantiser takes rows of up to 2048 values and
   // the fp8 GEMM a K that is a multiple of 128 (the encoder GEMMs' inputs
   // are E and FFN wide, in the body and in policy encoder layers).

@@ -184,3 +184,15 @@ def test_forward_gates(positions, bt4_bench_oracle, weights_dtype, batch):
     print(f"bf16x2_fp8lo, {weights_dtype} weights, batch {batch}: policy max-abs {perr:.3e} "
           f"wdl max-abs {werr:.3e} top-1 {top1:.4f}", flush=True)
     assert perr <= POLICY_TOL and werr <= WDL_TOL and top1 >= TOP1_GATE
+
+
+def test_widths_not_multiple_of_128_rejected():
+    """The lo pass takes 128-byte K steps: a net whose FFN width is not a
+    multiple of 128 is refused at creation, not at its first forward (the
+    embedding width, 32 per head and heads a multiple of 4, always is)."""
+    spec = synth.NetSpec("ffn448", 256, 1, 8, 448, input_ffn=512, policy_dim=256)
+    weights = synth.make_weights(spec, seed=0)
+    with pytest.raises(RuntimeError, match="multiples of 128"):
+        backend.create_network(spec, weights, max_batch=8, device=0, precision="bf16x2_fp8lo")
+    net = backend.create_network(spec, weights, max_batch=8, device=0, precision="bf16x2")
+    net.close()
