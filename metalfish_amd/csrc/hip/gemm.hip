@@ -58,12 +58,66 @@ __device__ __forceinline__ int Swz(int row, int chunk) {
     return row * 32 + ((chunk ^ ((row >> 1) & 3)) << 3);
 }
 
+// mu and r = 1 / sqrt(var + eps) of row `row` of a folded LayerNorm from
+// its partial sums (width / kLnStatCols (sum x, sum x^2) pairs, added in
+// order), with the reference formula var = E[x^2] - mu^2 clamped at 0.
+__device__ __forceinline__ void RowLnStats(const float *stats, int width, float eps, int row,
+                                           float &mu, float &r) {
+  const int pairs2 = width / (2 * kLnStatCols);
+  const f32x4 *q = reinterpret_cast<const f32x4 *>(stats) + static_cast<size_t>(row) * pairs2;
+  // Up to 8 quads (width <= 2048), loaded together.
+  f32x4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < pairs2)
+      v[i] = q[i];
+  float s = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < pairs2) {
+      s += v[i][0];
+      s2 += v[i][1];
+      s += v[i][2];
+      s2 += v[i][3];
+    }
+  mu = s / static_cast<float>(width);
+  float var = s2 / static_cast<float>(width) - mu * mu;
+  var = var < 0.f ? 0.f : var;
+  r = 1.f / sqrtf(var + eps);
+}
+
+// Eight consecutive floats of a per-column vector.
+__device__ __forceinline__ void LoadVec8(const float *v, int col, float (&o)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(v + col);
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(v + col + 4);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    o[r] = a[r];
+    o[4 + r] = b[r];
+  }
+}
+
+// A consumer of a folded LayerNorm: v = r (v - mu fold_c) for the row.
+// (fold_c is loaded here, per row, from L1: holding it across the row loop
+// costs registers the 256 x 128 tiles do not have.)
+__device__ __forceinline__ void FoldLn8(const GemmParams &p, int row, int col, float (&v)[8]) {
+  float mu, rr;
+  RowLnStats(p.ln_stats, p.ln_width, p.ln_eps, row, mu, rr);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const f32x4 c = *reinterpret_cast<const f32x4 *>(p.fold_c + col + 4 * h);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      v[4 * h + r] = rr * (v[4 * h + r] - mu * c[r]);
+  }
+}
+
 // Epilogue for four consecutive outputs (row, col .. col + 3) of C, given
 // the fp32 accumulators and bias: bias + activation to bf16 (with the lo
 // plane and the split column) or fp32, or resid + alpha * (acc + bias).
 // Columns at or past N are skipped; vector stores when the whole group is
 // inside and the rows allow it (p.vec).
-template <int MODE, int ACT>
+template <int MODE, int ACT, bool LN = false>
 __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col, f32x4 acc,
                                           const float (&b)[4]) {
   const bool full = p.vec && col + 3 < p.N;
@@ -71,6 +125,14 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       acc[r] *= col + r < p.N ? p.wscale[col + r] : 0.f;
+  }
+  if (LN && p.fold_c) {
+    // Consumer of a folded LayerNorm (never in the residual mode).
+    float mu, rr;
+    RowLnStats(p.ln_stats, p.ln_width, p.ln_eps, row, mu, rr);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      acc[r] = rr * (acc[r] - mu * (col + r < p.N ? p.fold_c[col + r] : 0.f));
   }
   float v[4];
   if constexpr (MODE == GEMM_OUT_RESID_F32) {
@@ -285,7 +347,7 @@ __device__ __forceinline__ void LoadBiasScale8(const GemmParams &p, int col, flo
 // fp32 accumulator quads: one 16-byte store per output plane when the group
 // is whole, aligned (p.vec8) and on one side of split_n; otherwise two
 // four-column epilogues.
-template <int MODE, int ACT>
+template <int MODE, int ACT, bool LN = false>
 __device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col, f32x4 a0,
                                           f32x4 a1) {
   if (!(p.vec8 && col + 7 < p.N && (col >= p.split_n || col + 8 <= p.split_n))) {
@@ -293,12 +355,12 @@ __device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col,
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
-    Epilogue4<MODE, ACT>(p, row, col, a0, b);
+    Epilogue4<MODE, ACT, LN>(p, row, col, a0, b);
     if (col + 4 < p.N) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         b[r] = (p.bias && col + 4 + r < p.N) ? p.bias[col + 4 + r] : 0.f;
-      Epilogue4<MODE, ACT>(p, row, col + 4, a1, b);
+      Epilogue4<MODE, ACT, LN>(p, row, col + 4, a1, b);
     }
     return;
   }
@@ -309,9 +371,32 @@ __device__ __forceinline__ void Epilogue8(const GemmParams &p, int row, int col,
     v[r] = a0[r] * sc[r];
     v[4 + r] = a1[r] * sc[4 + r];
   }
+  if (LN && p.fold_c)
+    FoldLn8(p, row, col, v);
   if constexpr (MODE == GEMM_OUT_RESID_F32)
     LoadResid8(p, row, col, rv);
   Finish8<MODE, ACT>(p, row, col, v, b, rv);
+}
+
+// The folded-LayerNorm residual epilogue: a thread keeps one column group
+// for the tile (the threads are a multiple of the groups per row and every
+// thread runs the same rows) and each 128-column block of a row is 16
+// consecutive lanes (tiles 128 or 256 columns wide).
+// Rows per pass of the staged epilogue: the fp32 tile rows (BN + 4 floats
+// each) that fit the LDS ring of ST stages of STAGE_BYTES.
+template <int BM, int BN, int ST, int STAGE_BYTES>
+constexpr int StagedRows() {
+  constexpr int ring = ST * STAGE_BYTES / 4;
+  constexpr int pitch = BN + 4;
+  return ring >= BM * pitch    ? BM
+         : ring >= 128 * pitch ? 128
+         : ring >= 64 * pitch  ? 64
+         : ring >= 32 * pitch  ? 32
+                               : 16;
+}
+template <int BN, int THREADS, int RB>
+constexpr bool GemmLnEpilogueOk() {
+  return (BN == 128 || BN == 256) && THREADS % (BN / 8) == 0 && (RB * (BN / 8)) % THREADS == 0;
 }
 
 // fp8 weights (W8): the e4m3 rows go through the LDS ring as bytes (BK
@@ -692,8 +777,11 @@ __device__ __forceinline__ void Lo8Loop(const GemmParams &p, std::uint16_t *lds,
 #endif  // __HIP_DEVICE_COMPILE__
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8, bool F8 = false, bool PIPE = false, bool LO8 = false>
-__global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
+          bool W8, bool F8 = false, bool PIPE = false, bool LO8 = false, bool LN = false>
+// (The folded-LayerNorm 256 x 128 tiles are held to 128 VGPRs, two
+// workgroups per CU like the others of that shape.)
+__global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1) void GemmKernel(
+    GemmParams p) {
   constexpr int NWAVES = WM * WN;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 16, TN = WTN / 16;
@@ -948,8 +1036,8 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   }  // PIPE / lock-step loop
 
   // fp8 activations: each row's quantisation scale (the weight row scale
-  // follows in the epilogue).
-  if (p.ascale) {
+  // follows in the epilogue).  (Never with a folded LayerNorm.)
+  if (!LN && p.ascale) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = m0 + wm * WTM + i * 16 + (lane & 15);
@@ -963,7 +1051,7 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   // of its tile, columns n_base + 4 * (lane / 16) + r, r = 0..3.
   const int row_base = m0 + wm * WTM + (lane & 15);
   const int col_base = n0 + wn * WTN + (lane >> 4) * 4;
-  if (p.k_splits > 1) {
+  if (!LN && p.k_splits > 1) {
     float *part = static_cast<float *>(p.C) + static_cast<size_t>(blockIdx.y) * p.M * p.ldc;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -1000,19 +1088,109 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
   // lines of consecutive rows instead of pieces of sixteen rows.
   constexpr int PITCH = BN + 4;  // floats per staged row (+4: bank spread)
   constexpr int RING_FLOATS = ST * STAGE / 2;
-  constexpr int RB = RING_FLOATS >= BM * PITCH         ? BM
-                     : RING_FLOATS >= 128 * PITCH      ? 128
-                     : RING_FLOATS >= 64 * PITCH       ? 64
-                     : RING_FLOATS >= 32 * PITCH       ? 32
-                                                       : 16;
+  constexpr int RB = StagedRows<BM, BN, ST, STAGE_BYTES>();
   static_assert(RB * PITCH <= RING_FLOATS && BM % RB == 0 && RB % 16 == 0,
                 "staged epilogue rows must fit the LDS ring");
   constexpr int GPR = BN / 8;  // 8-column groups per row
   float *tile = reinterpret_cast<float *>(lds);
+  // Folded LayerNorm (LN instances): the tile's per-row mu and r (of the A
+  // rows' LayerNorm for a consumer, of the residual rows' for a residual
+  // GEMM) and per-column constants (fold_c; or the residual's gamma and beta
+  // and the output's gamma), fetched once per tile (rows: G lanes each, see
+  // ln_load; column t: thread t) and kept in the LDS ring behind the staged
+  // rows.
+  float *ln_row = tile + RB * PITCH;  // [BM][2]: mu, r
+  float *ln_col = ln_row + 2 * BM;    // [3][BN]
+  constexpr int THREADS = NWAVES * 64;
+  float ln_c0 = 0.f, ln_c1 = 0.f, ln_c2 = 0.f;
+  bool ln_on = false;
+  // Load rounds issued before the staging: on 256-wide tiles all of them
+  // for rows of up to 4 quads (width 1024), wider rows load the rest in the
+  // staging; 128-wide tiles load all there (their registers are full: the
+  // FFN1 forward at batch 256 measured 0.9-1.9 % faster so).
+  constexpr int kLnPre = LN && BN == 256 ? (BM * 4 + THREADS - 1) / THREADS : 0;
+  f32x4 ln_v[kLnPre > 0 ? kLnPre : 1] = {};
+  int ln_q = 0, ln_g = 1, ln_rounds = 0;
+  const float *st = nullptr;
+  // Round k of the row-stat loads: lane idx = k * THREADS + tid reads quad
+  // idx % G of tile row idx / G (zeros past the row's quads or the tile).
+  auto ln_load = [&](int k) {
+    const int idx = k * THREADS + tid, R = idx / ln_g, qd = idx % ln_g;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (k < ln_rounds && R < BM && qd < ln_q)
+      v = reinterpret_cast<const f32x4 *>(st)[static_cast<size_t>(min(m0 + R, p.M - 1)) * ln_q +
+                                              qd];
+    return v;
+  };
+  // Sums a round's quads over each row's G lanes (a fixed shuffle order)
+  // and stores the row's mu and r = 1 / sqrt(var + eps), with the reference
+  // formula var = E[x^2] - mu^2 clamped at 0.  Every lane takes part.
+  auto ln_reduce = [&](int k, f32x4 v, float eps) {
+    float a = v[0] + v[2], a2 = v[1] + v[3];
+    for (int m = 1; m < ln_g; m <<= 1) {
+      a += __shfl_xor(a, m, 64);
+      a2 += __shfl_xor(a2, m, 64);
+    }
+    const int idx = k * THREADS + tid, R = idx / ln_g;
+    if (R < BM && idx % ln_g == 0) {
+      const float mu = a / static_cast<float>(p.ln_width);
+      float var = a2 / static_cast<float>(p.ln_width) - mu * mu;
+      var = var < 0.f ? 0.f : var;
+      ln_row[2 * R] = mu;
+      ln_row[2 * R + 1] = 1.f / sqrtf(var + eps);
+    }
+  };
+  if constexpr (LN) {
+    static_assert(RB * PITCH + 2 * BM + 3 * BN <= RING_FLOATS && BN <= THREADS,
+                  "folded LayerNorm constants fit behind the staged rows");
+    st = p.fold_c ? p.ln_stats : p.res_stats;
+    ln_on = p.fold_c || p.res_stats || p.out_gamma;
+    // The rows' partial sums: G lanes per row (G = the row's quads of two
+    // (sum, sum^2) pairs, a power of two, 64 at most), the first kLnPre
+    // rounds of loads issued here so they are in flight during the staging.
+    if (st) {
+      ln_q = p.ln_width / (2 * kLnStatCols);
+      ln_g = 1;
+      while (ln_g < ln_q)
+        ln_g <<= 1;
+      ln_rounds = (BM * ln_g + THREADS - 1) / THREADS;
+#pragma unroll
+      for (int k = 0; k < kLnPre; ++k)
+        ln_v[k] = ln_load(k);
+    }
+    if (tid < BN) {
+      const int col = min(n0 + tid, p.N - 1);
+      if (p.fold_c) {
+        ln_c0 = p.fold_c[col];
+      } else if (p.res_stats) {
+        ln_c0 = p.res_gamma[col];
+        ln_c1 = p.res_beta[col];
+      }
+      if (p.out_gamma)
+        ln_c2 = p.out_gamma[col];
+    }
+  }
   // Rows pass * RB .. + RB of the accumulator tile into the ring.
   auto stage = [&](int pass) {
     // The ring is no longer read (first pass) / the previous chunk is stored.
     __syncthreads();
+    if constexpr (LN) {
+      if (pass == 0 && ln_on) {
+        if (st) {
+          const float eps = p.fold_c ? p.ln_eps : p.res_eps;
+#pragma unroll
+          for (int k = 0; k < kLnPre; ++k)
+            ln_reduce(k, ln_v[k], eps);
+          for (int k = kLnPre; k < ln_rounds; ++k)
+            ln_reduce(k, ln_load(k), eps);
+        }
+        if (tid < BN) {
+          ln_col[tid] = ln_c0;
+          ln_col[BN + tid] = ln_c1;
+          ln_col[2 * BN + tid] = ln_c2;
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int rl = wm * WTM + i * 16 + (lane & 15);
@@ -1047,7 +1225,6 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       c8 = (g % GPR) * 8;
     }
   };
-  constexpr int THREADS = NWAVES * 64;
   if constexpr (MODE != GEMM_OUT_RESID_F32 && THREADS % GPR == 0 &&
                 (RB * GPR) % THREADS == 0) {
     constexpr int ITER = RB * GPR / THREADS;
@@ -1055,9 +1232,13 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
     int c8, r0;
     group_of(tid, r0, c8);
     const int col = n0 + c8;
-    if (p.vec8 && n0 + BN <= p.N && (n0 + BN <= p.split_n || n0 >= p.split_n)) {
+    // (The pipelined LN instances take only whole tiles with fold_c, which
+    // the launcher checks: their other epilogue paths are not compiled.)
+    if ((LN && PIPE) ||
+        (p.vec8 && n0 + BN <= p.N && (n0 + BN <= p.split_n || n0 >= p.split_n))) {
       float b[8], sc[8];
       LoadBiasScale8(p, col, b, sc);
+      const bool fold = LN && (PIPE || p.fold_c != nullptr);
 #pragma unroll 1
       for (int pass = 0; pass < BM / RB; ++pass) {
         const float none[8] = {};
@@ -1075,6 +1256,14 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
             for (int r = 0; r < 4; ++r) {
               v[r] = a0[r] * sc[r];
               v[4 + r] = a1[r] * sc[4 + r];
+            }
+            if (fold) {
+              // r (v - mu fold_c) from the tile's LDS constants.
+              const int rt = pass * RB + rl;
+              const float mu = ln_row[2 * rt], rr = ln_row[2 * rt + 1];
+#pragma unroll
+              for (int r = 0; r < 8; ++r)
+                v[r] = rr * (v[r] - mu * ln_col[c8 + r]);
             }
             Finish8<MODE, ACT>(p, row, col, v, b, none);
           }
@@ -1099,23 +1288,104 @@ __global__ __launch_bounds__(WM *WN * 64) void GemmKernel(GemmParams p) {
       for (int i = 0; i < TM; ++i) {
         const int row = row_base + i * 16;
         if (row < p.M)
-          Epilogue4<MODE, ACT>(p, row, col, acc[i][j], b);
+          Epilogue4<MODE, ACT, LN>(p, row, col, acc[i][j], b);
       }
     }
     return;
   }
+  if constexpr (LN && MODE == GEMM_OUT_RESID_F32 && BN == 256 &&
+                GemmLnEpilogueOk<BN, THREADS, RB>()) {
+    if (PIPE || p.out_gamma || p.res_stats) {
+      // Residual mode with a folded LayerNorm on either side (whole tiles,
+      // checked by the launcher): the residual is LN(x) of x o gamma rows
+      // (res_stats), and/or the result x = resid + alpha (acc + b) leaves
+      // as x o out_gamma in bf16 hi + lo (+ e4m3 codes) with the partial
+      // sums of x over each 128-column block: a block is 16 consecutive
+      // lanes of one row (8 columns each), summed by shuffles in a fixed
+      // order.  A thread keeps one column group for the whole tile.
+      int c8, r0;
+      group_of(tid, r0, c8);
+      const int col = n0 + c8;
+      float b[8], sc[8];
+      LoadBiasScale8(p, col, b, sc);
+      const int parts = p.ln_width / kLnStatCols;
 #pragma unroll 1
-  for (int pass = 0; pass < BM / RB; ++pass) {
-    stage(pass);
-    for (int g = tid; g < RB * GPR; g += NWAVES * 64) {
-      int rl, c8;
-      group_of(g, rl, c8);
-      const int row = m0 + pass * RB + rl, col = n0 + c8;
-      if (row >= p.M || col >= p.N)
-        continue;
-      const float *src = tile + rl * PITCH + c8;
-      Epilogue8<MODE, ACT>(p, row, col, *reinterpret_cast<const f32x4 *>(src),
-                           *reinterpret_cast<const f32x4 *>(src + 4));
+      for (int pass = 0; pass < BM / RB; ++pass) {
+        stage(pass);
+        for (int g = tid; g < RB * GPR; g += THREADS) {
+          int rl, cc;  // cc == c8: g % 64 is the thread's lane
+          group_of(g, rl, cc);
+          (void)cc;
+          const int row = m0 + pass * RB + rl;
+          const bool valid = row < p.M;
+          const float *src = tile + rl * PITCH + c8;
+          const f32x4 a0 = *reinterpret_cast<const f32x4 *>(src);
+          const f32x4 a1 = *reinterpret_cast<const f32x4 *>(src + 4);
+          float x[8], rv[8];
+          if (valid) {
+            LoadResid8(p, row, col, rv);
+            if (p.res_stats) {
+              // LN of the residual row: r (x o gamma - mu gamma) + beta.
+              const int rt = pass * RB + rl;
+              const float mu = ln_row[2 * rt], rr = ln_row[2 * rt + 1];
+#pragma unroll
+              for (int r = 0; r < 8; ++r)
+                rv[r] = rr * (rv[r] - mu * ln_col[c8 + r]) + ln_col[BN + c8 + r];
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            x[r] = valid ? rv[r] + p.alpha * (a0[r] * sc[r] + b[r]) : 0.f;
+            x[4 + r] = valid ? rv[4 + r] + p.alpha * (a1[r] * sc[4 + r] + b[4 + r]) : 0.f;
+          }
+          if (!p.out_gamma) {
+            if (valid) {
+              float *c = static_cast<float *>(p.C) + static_cast<size_t>(row) * p.ldc + col;
+              *reinterpret_cast<f32x4 *>(c) = f32x4{x[0], x[1], x[2], x[3]};
+              *reinterpret_cast<f32x4 *>(c + 4) = f32x4{x[4], x[5], x[6], x[7]};
+            }
+            continue;
+          }
+          float s = 0.f, s2 = 0.f;
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            s += x[r];
+            s2 += x[r] * x[r];
+          }
+#pragma unroll
+          for (int m = 1; m < 16; m <<= 1) {
+            s += __shfl_xor(s, m, 64);
+            s2 += __shfl_xor(s2, m, 64);
+          }
+          if (!valid)
+            continue;
+          if ((lane & 15) == 0)
+            *reinterpret_cast<f32x2 *>(p.out_stats + (static_cast<size_t>(row) * parts +
+                                                      col / kLnStatCols) * 2) = f32x2{s, s2};
+          float y[8], none[8] = {};
+#pragma unroll
+          for (int r = 0; r < 8; ++r)
+            y[r] = x[r] * ln_col[2 * BN + c8 + r];
+          Finish8<GEMM_OUT_BF16, ACT_NONE>(p, row, col, y, none, none);
+        }
+      }
+      return;
+    }
+  }
+  if constexpr (!(LN && PIPE)) {
+#pragma unroll 1
+    for (int pass = 0; pass < BM / RB; ++pass) {
+      stage(pass);
+      for (int g = tid; g < RB * GPR; g += NWAVES * 64) {
+        int rl, c8;
+        group_of(g, rl, c8);
+        const int row = m0 + pass * RB + rl, col = n0 + c8;
+        if (row >= p.M || col >= p.N)
+          continue;
+        const float *src = tile + rl * PITCH + c8;
+        Epilogue8<MODE, ACT, LN>(p, row, col, *reinterpret_cast<const f32x4 *>(src),
+                                 *reinterpret_cast<const f32x4 *>(src + 4));
+      }
     }
   }
 }
@@ -1151,7 +1421,7 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
-          bool W8 = false, bool F8 = false, bool PIPE = false, bool LO8 = false>
+          bool W8 = false, bool F8 = false, bool PIPE = false, bool LO8 = false, bool LN = false>
 hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   // The LDS ring: ST stages of the main loop, or two stages of the fp8 lo
   // pass's 128-byte rows when larger.
@@ -1159,7 +1429,25 @@ hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
       static_cast<size_t>(ST) * GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>();
   constexpr size_t kLo8Ring = LO8 ? static_cast<size_t>(2) * (BM + BN) * 128 : 0;
   constexpr size_t kLds = kRing > kLo8Ring ? kRing : kLo8Ring;
-  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8, PIPE, LO8>;
+  auto kernel = GemmKernel<BM, BN, BK, ST, WM, WN, SPLIT, MODE, ACT, W8, F8, PIPE, LO8, LN>;
+  constexpr int kRb = StagedRows<BM, BN, ST, GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>()>();
+  if constexpr (MODE == GEMM_OUT_RESID_F32) {
+    // The folded-LayerNorm residual epilogue takes whole 256-wide tiles.
+    if ((p.out_gamma || p.res_stats) &&
+        !(LN && BN == 256 && GemmLnEpilogueOk<BN, WM * WN * 64, kRb>() && p.vec8 &&
+          p.N % BN == 0))
+      return hipErrorInvalidValue;
+    if (LN && PIPE && !p.out_gamma && !p.res_stats)
+      return hipErrorInvalidValue;
+  } else if constexpr (LN && PIPE) {
+    // The pipelined consumer instances compile only the whole-tile epilogue.
+    constexpr int kGpr = BN / 8, kThreads = WM * WN * 64;
+    if (!p.fold_c || !p.vec8 || p.N % BN || (p.split_n < p.N && p.split_n % BN) ||
+        kThreads % kGpr || (kRb * kGpr) % kThreads)
+      return hipErrorInvalidValue;
+  }
+  if (LN && (p.ascale || p.k_splits != 1))
+    return hipErrorInvalidValue;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [&]() {
@@ -1201,6 +1489,30 @@ hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, bool W8, bool F8 = false,
           bool PIPE = false, bool LO8 = false>
 hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
+  // A folded LayerNorm (GemmParams::fold_c / out_gamma / res_stats): its
+  // epilogue code is compiled only into the tiles that take it (LnFoldTile:
+  // the pipelined split-precision and BF16X2_FP8LO tiles of the large
+  // batches, and the small-LDS split 64 x 64 tile of the smolgen
+  // compression beside Q|K|V), bf16 outputs and the residual mode.
+  constexpr bool kLn = !W8 && !F8 && (SPLIT || LO8) &&
+                       (PIPE || (BM == 64 && BN == 64 && BK == 32));
+  if (p.fold_c || p.out_gamma || p.res_stats) {
+    if constexpr (kLn) {
+      if (p.k_splits == 1 && p.out_mode == GEMM_OUT_RESID_F32)
+        return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_RESID_F32, ACT_NONE, W8, F8,
+                             PIPE, LO8, true>(p, stream);
+      if (p.k_splits == 1 && p.out_mode == GEMM_OUT_BF16 && p.act == ACT_NONE)
+        return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_NONE, W8, F8,
+                             PIPE, LO8, true>(p, stream);
+      if (p.k_splits == 1 && p.out_mode == GEMM_OUT_BF16 && p.act == ACT_MISH)
+        return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_MISH, W8, F8,
+                             PIPE, LO8, true>(p, stream);
+      if (p.k_splits == 1 && p.out_mode == GEMM_OUT_BF16)
+        return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_BF16, ACT_RUNTIME, W8, F8,
+                             PIPE, LO8, true>(p, stream);
+    }
+    return hipErrorInvalidValue;
+  }
   if (p.k_splits > 1 || (p.out_mode == GEMM_OUT_F32 && p.act == ACT_NONE))
     return LaunchVariant<BM, BN, BK, ST, WM, WN, SPLIT, GEMM_OUT_F32, ACT_NONE, W8, F8, PIPE, LO8>(p, stream);
   if (p.out_mode == GEMM_OUT_RESID_F32)
@@ -1246,6 +1558,39 @@ bool GemmWholeRoundTiles(const GemmParams &p) {
   const long big_tiles = static_cast<long>((p.M + 255) / 256) * ((p.N + 255) / 256);
   return p.M >= kLargeRows && p.N >= 128 && p.k_splits == 1 && big_tiles % 256 == 0 && !p.A8;
 }
+
+namespace {
+
+// The instances that compile a folded LayerNorm's epilogue, and the one a
+// GEMM with a folded LayerNorm runs on (the tiles the same shapes take
+// without it, where those are among them): split precision (bf16 hi + lo
+// activations, or the BF16X2_FP8LO codes), bf16 weights, one K slice.
+enum class LnTile { kNone, kLo8, k256, k256Beside, k256x128, k64 };
+
+LnTile LnFoldTile(const GemmParams &p) {
+  const bool res = p.out_mode == GEMM_OUT_RESID_F32;
+  if ((!p.A_lo && !p.A_lo8) || p.W8 || p.A8 || p.k_splits != 1 || p.K % 64)
+    return LnTile::kNone;
+  if (!res && p.out_mode != GEMM_OUT_BF16)
+    return LnTile::kNone;
+  // 256-wide whole tiles (the residual side always; a consumer's epilogue
+  // on the pipelined tiles too).
+  if (p.A_lo8)
+    return p.N % 256 == 0 ? LnTile::kLo8 : LnTile::kNone;
+  if (p.N % 256 == 0 && (res || GemmWholeRoundTiles(p)))
+    return p.beside_chain && !res ? LnTile::k256Beside : LnTile::k256;
+  if (res)
+    return LnTile::kNone;
+  // Consumers: the small-LDS 64 x 64 tiles beside Q|K|V (any width), else
+  // 256 x 128 pipelined tiles.
+  if (p.small_lds)
+    return LnTile::k64;
+  return p.N % 128 == 0 ? LnTile::k256x128 : LnTile::kNone;
+}
+
+}  // namespace
+
+bool GemmLnFoldOk(const GemmParams &p) { return LnFoldTile(p) != LnTile::kNone; }
 
 // Split-K at few positions (64 x 64 tiles, K in 64-wide steps).  A GEMM
 // kernel here costs ~5 us however short its K loop, and a separate reduce
@@ -1348,13 +1693,35 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
     return fail("split output needs lo planes for both parts or neither");
   if (p.ldc < (p.split_n < p.N ? p.split_n : p.N))
     return fail("ldc too small");
-  if (p.C_lo8 && (p.out_mode != GEMM_OUT_BF16 || p.C_lo || p.split_n < p.N || p.k_splits != 1 ||
-                  p.ldc8 < p.N || p.ldc8 % 8 || !Aligned(p.C_lo8, 8)))
+  // Folded LayerNorm (see GemmParams): consumer and residual sides.
+  const bool ln_res = p.out_mode == GEMM_OUT_RESID_F32 && (p.out_gamma || p.res_stats);
+  if (p.fold_c && (!p.ln_stats || p.out_mode == GEMM_OUT_RESID_F32 || p.ln_width != p.K ||
+                   p.K % (2 * kLnStatCols) || p.K > 128 * kLnStatCols ||
+                   !Aligned(p.fold_c, 16) ||
+                   !Aligned(p.ln_stats, 16) || p.k_splits != 1))
+    return fail("folded LayerNorm consumer: ln_stats, fold_c (16-byte aligned), K = ln_width "
+                "a multiple of 256 up to 16384, one K slice, not the residual mode");
+  if ((p.out_gamma || p.res_stats) && !ln_res)
+    return fail("folded LayerNorm output / residual: residual mode only");
+  if (ln_res && (!p.resid16 || p.k_splits != 1 || p.ln_width != p.N ||
+                 p.N % (2 * kLnStatCols) || p.N > 128 * kLnStatCols ||
+                 (p.res_stats && (!p.res_gamma || !p.res_beta || !Aligned(p.res_stats, 16) ||
+                                  !Aligned(p.res_gamma, 16) || !Aligned(p.res_beta, 16))) ||
+                 (p.out_gamma && (!p.out_stats || !Aligned(p.out_gamma, 16) ||
+                                  !Aligned(p.out_stats, 8) || !p.C_lo))))
+    return fail("folded LayerNorm residual: split residual, one K slice, N = ln_width a "
+                "multiple of 256 up to 16384, gamma / beta / stats 16-byte aligned, a bf16 lo output "
+                "plane with out_gamma");
+  if (p.C_lo8 && !(p.out_mode == GEMM_OUT_RESID_F32 && p.out_gamma) &&
+      (p.out_mode != GEMM_OUT_BF16 || p.C_lo || p.split_n < p.N || p.k_splits != 1 ||
+       p.ldc8 < p.N || p.ldc8 % 8 || !Aligned(p.C_lo8, 8)))
     return fail("e4m3 lo output: bf16 mode, one output, no bf16 lo plane, ldc8 >= N, "
                 "ldc8 % 8 == 0, 8-byte aligned");
+  if (p.C_lo8 && p.out_gamma && (p.ldc8 < p.N || p.ldc8 % 8 || !Aligned(p.C_lo8, 8)))
+    return fail("e4m3 lo output: ldc8 >= N, ldc8 % 8 == 0, 8-byte aligned");
   // Vector (4-column) stores need every output row start aligned to 4
   // elements' width; otherwise the epilogue stores element by element.
-  const bool f32 = p.out_mode != GEMM_OUT_BF16 || p.k_splits > 1;
+  const bool f32 = (p.out_mode != GEMM_OUT_BF16 && !p.out_gamma) || p.k_splits > 1;
   const std::uintptr_t vb = f32 ? 16 : 8;
   p.vec = Aligned(p.C, vb) && p.ldc % 4 == 0 && (!p.C_lo || Aligned(p.C_lo, vb)) &&
           (p.split_n >= p.N ||
@@ -1363,7 +1730,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
            (p.ldr % 4 == 0 && (p.resid16 ? Aligned(p.resid16, 8) && Aligned(p.resid16_lo, 8)
                                           : Aligned(p.resid, 16))));
   // Eight-column groups with 16-byte accesses (staged epilogue).
-  const bool out_bf16 = p.out_mode == GEMM_OUT_BF16;
+  const bool out_bf16 = p.out_mode == GEMM_OUT_BF16 || p.out_gamma;
   const int gcols = out_bf16 ? 8 : 4;  // elements per 16 bytes
   p.vec8 = p.vec && Aligned(p.C, 16) && p.ldc % gcols == 0 &&
            (!p.C_lo || Aligned(p.C_lo, 16)) &&
@@ -1376,6 +1743,25 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   // fp8 lo correction: 256 x 256 tiles of eight waves, the hi pass on the
   // four-stage single-bf16 pipelined ring (128 KiB), then the lo pass on two
   // 64 KiB stages of code rows.
+  // A folded LayerNorm: only the instances that compile its epilogue.
+  if (p.fold_c || ln_res) {
+    switch (LnFoldTile(p)) {
+    case LnTile::kLo8:
+      return LaunchW<256, 256, 32, 4, 4, 2, false, false, false, true, true>(p, stream);
+    case LnTile::k256Beside:
+      return LaunchW<256, 256, 32, 2, 4, 2, true, false, false, true>(p, stream);
+    case LnTile::k256:
+      return LaunchW<256, 256, 32, 3, 4, 2, true, false, false, true>(p, stream);
+    case LnTile::k256x128:
+      return LaunchW<256, 128, 32, 2, 4, 2, true, false, false, true>(p, stream);
+    case LnTile::k64:
+      return LaunchW<64, 64, 32, 2, 2, 2, true, false>(p, stream);
+    default:
+      return fail("folded LayerNorm: split-precision activations, bf16 weights, one K slice, "
+                  "K % 64 == 0 and N a multiple of 256 (residual, BF16X2_FP8LO codes) or "
+                  "128 (or small-LDS tiles)");
+    }
+  }
   if (lo8)
     return LaunchW<256, 256, 32, 4, 4, 2, false, false, false, true, true>(p, stream);
   const bool split = p.A_lo != nullptr;
@@ -1385,7 +1771,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   // partials to p.partials through a three-stage ring and sums them in
   // slice order in a second kernel that applies the epilogue.  The split depends on the shape
   // only: a batch size always takes the same path and gives the same bits.
-  if (!large && p.k_splits == 1 && p.partials && Aligned(p.partials, 16) && p.vec &&
+  if (!large && !ln_res && p.k_splits == 1 && p.partials && Aligned(p.partials, 16) && p.vec &&
       p.N % 4 == 0) {
     const int splits = GemmAutoSplits(p);
     if (splits > 1) {

@@ -105,6 +105,12 @@ constexpr int kSmolgenSideRows = 1088;
 // BF16X2_FP8LO: the fp8 lo correction runs from this many token rows (128
 // positions); below, the forward is the BF16X2 one.
 constexpr int kLo8MinRows = 8192;
+// From this many token rows (256 positions) the body's residual LayerNorms
+// are folded into the GEMMs around them (GemmParams: the residual GEMMs write
+// x o gamma with per-row partial sums, Q|K|V, the compression and FFN1 take
+// the LayerNorm in their epilogue, the next residual rebuilds it), where
+// the residual GEMMs (N = E) take whole rounds of 256 x 256 tiles.
+constexpr long kFoldRows = 16384;
 
 std::uint16_t ToBf16(float f) {
   std::uint32_t u;
@@ -203,6 +209,9 @@ struct Layer {
   bool smolgen = false;
   size_t sg_d1_b, sg_ln1_g, sg_ln1_b, sg_d2_b, sg_ln2_g, sg_ln2_b;
   size_t sg_d1_w[2], sg_d2_w[2];
+  // Folded LayerNorms (see kFoldRows): {fold_c, bias'} of the Q|K|V (+
+  // compression) rows over the previous layer's LN2, and of FFN1 over LN1.
+  size_t qkv_fold[2] = {0, 0}, ffn1_fold[2] = {0, 0};
 };
 
 struct Dims {
@@ -255,6 +264,8 @@ struct mfh_net {
   // BF16X2_FP8LO: offset of a dense weight's W' (bf16, with column scales) ->
   // offset of its e4m3 codes.
   std::map<size_t, size_t> lo8_codes;
+  // The body's fold constants were packed (Layer::qkv_fold / ffn1_fold).
+  bool has_fold = false;
   size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
   size_t head_w[2], qk_w[2], val1_w[2];
   size_t mov_b = 0, mov1_b = 0, mov2_w = 0, mov2_b = 0;  // moves-left head
@@ -662,6 +673,50 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   return MFH_OK;
 }
 
+// The value the GPU multiplies for row n, column k of a packed GEMM
+// weight: bf16, an e4m3 code times its row scale, or (BF16X2_FP8LO) W'
+// times the column scale.
+double PackedWeight(const Blob &blob, const size_t (&w)[2], bool fp8, bool lo8, int ld, int n,
+                    int k) {
+  const size_t i = static_cast<size_t>(n) * ld + k;
+  float scale = 1.f;
+  if (fp8 || lo8)
+    std::memcpy(&scale, blob.bytes.data() + w[1] + 4 * static_cast<size_t>(n), 4);
+  if (fp8 && !lo8)
+    return static_cast<double>(DecodeE4m3(blob.bytes[w[0] + i])) * scale;
+  std::uint16_t b;
+  std::memcpy(&b, blob.bytes.data() + w[0] + 2 * i, 2);
+  const std::uint32_t u = static_cast<std::uint32_t>(b) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return static_cast<double>(f) * scale;
+}
+
+// A LayerNorm (gamma, beta) folded into the GEMM that reads its output:
+// fold_c[n] = sum_k gamma_k W[n][k] and bias'[n] = bias[n] + sum_k beta_k
+// W[n][k] over the weights as the GPU holds them, summed in double.
+// Returns {fold_c, bias'} blob offsets.
+void AddLnFold(Blob &blob, const size_t (&w)[2], bool fp8, bool lo8, int rows, int K,
+               size_t gamma, size_t beta, size_t bias, size_t (&out)[2]) {
+  std::vector<float> c(rows), b(rows);
+  std::vector<float> g(K), be(K), bi(rows);
+  std::memcpy(g.data(), blob.bytes.data() + gamma, 4 * static_cast<size_t>(K));
+  std::memcpy(be.data(), blob.bytes.data() + beta, 4 * static_cast<size_t>(K));
+  std::memcpy(bi.data(), blob.bytes.data() + bias, 4 * static_cast<size_t>(rows));
+  for (int n = 0; n < rows; ++n) {
+    double sc = 0.0, sb = 0.0;
+    for (int k = 0; k < K; ++k) {
+      const double x = PackedWeight(blob, w, fp8, lo8, K, n, k);
+      sc += g[k] * x;
+      sb += be[k] * x;
+    }
+    c[n] = static_cast<float>(sc);
+    b[n] = static_cast<float>(bi[n] + sb);
+  }
+  out[0] = blob.Add(c.data(), c.size() * 4);
+  out[1] = blob.Add(b.data(), b.size() * 4);
+}
+
 void SetW(size_t (&dst)[2], const GemmW &g) {
   dst[0] = g.w;
   dst[1] = g.s;
@@ -810,6 +865,26 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
     const int rc = pack_layer("body.encoder." + std::to_string(i), net->layers[i], d.F, d.smolgen);
     if (rc != MFH_OK)
       return rc;
+  }
+  // Folded residual LayerNorms of the body (split precisions, nets sized
+  // for kFoldRows token rows): Q|K|V (+ compression) of layer i > 0 over
+  // layer i - 1's LN2, FFN1 of every layer over its LN1.
+  if (d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
+      static_cast<long>(net->max_batch) * kSquares >= kFoldRows) {
+    const int qrows = 3 * E + (d.smolgen ? d.C : 0);
+    for (int i = 0; i < d.L; ++i) {
+      Layer &L = net->layers[i];
+      const bool qlo8 = net->lo8_codes.count(L.qkv_w[0]) > 0;
+      const bool flo8 = net->lo8_codes.count(L.ffn1_w[0]) > 0;
+      if (i > 0) {
+        const Layer &P = net->layers[i - 1];
+        AddLnFold(blob, L.qkv_w, net->fp8, qlo8, qrows, E, P.ln2_g, P.ln2_b, L.qkv_b,
+                  L.qkv_fold);
+      }
+      AddLnFold(blob, L.ffn1_w, net->fp8, flo8, d.F, E, L.ln1_g, L.ln1_b, L.ffn1_b,
+                L.ffn1_fold);
+    }
+    net->has_fold = true;
   }
   // Policy encoder layers (weights.cpp:188-203), no smolgen.
   net->pol_layers.resize(d.PL);
@@ -962,6 +1037,13 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   }
   // e4m3 lo parts of the encoder GEMM inputs (BF16X2_FP8LO), at the batches
   // whose forward uses them.
+  if (d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
+      M >= static_cast<size_t>(kFoldRows)) {
+    // Per-row partial sums of the folded LayerNorms' rows (LN2: "st_act",
+    // LN1: "st_mid").
+    add("st_act", M * (d.E / mfh::kLnStatCols) * 2 * 4);
+    add("st_mid", M * (d.E / mfh::kLnStatCols) * 2 * 4);
+  }
   if (d.lo8 && M >= static_cast<size_t>(kLo8MinRows)) {
     add("act_lo8", M * d.E);
     add("qkv_lo8", M * 3 * d.E);
@@ -1202,6 +1284,14 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   };
   const bool lo8_act =
       lo8 && (whole_round(M, 3 * E) || whole_round(M, d.F) || (d.input_ffn && whole_round(M, d.Fi)));
+  // The body's residual LayerNorms folded into the GEMMs around them (see
+  // kFoldRows): the whole forward (a single debug layer keeps them), where
+  // the residual GEMMs take whole rounds of 256 x 256 tiles.
+  // (Checked below: every GEMM around them must have a tile that compiles
+  // the folded epilogue.)
+  bool fold = net->has_fold && full && ws.Has("st_act") && whole_round(M, E) &&
+              M >= kSmolgenSideRows;
+  float *st_act = nullptr, *st_mid = nullptr;
   auto ln = [&](const float *x, int rows, int width, float eps, const float *g, const float *b,
                 float *y32, const std::string &y16) {
     mfh::LayerNormParams lp;
@@ -1328,6 +1418,51 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // workgroup; at small batches the LayerNorm kernel sums the GEMM's split-K
   // partials with the bias and residual; otherwise the tiled GEMM writes the
   // pre-LayerNorm rows to `pre` for the LayerNorm kernel.
+  // A residual GEMM beside folded LayerNorms (kFoldRows): the residual is
+  // the "act" planes, LN(x) of folded rows x o gamma when res_st is set
+  // (rg / rb / res_eps that LayerNorm's); the sum x = resid + alpha (A.W^T +
+  // b) leaves folded, as x o og onto "act" with its partial sums in out_st
+  // (og set), or in fp32 to `pre` for the LayerNorm kernel (g / b / eps,
+  // y32 as in residual_ln).
+  auto residual_fold = [&](const std::string &a, int k, const size_t (&w_off)[2],
+                           const float *bias, const char *role, float alpha, const float *res_st,
+                           const float *rg, const float *rb, float res_eps, const float *og,
+                           float *out_st, float eps, const float *g, const float *b,
+                           float *y32) -> int {
+    mfh::GemmParams p = gemm(a, k, w_off, k, M, E, k, bias, mfh::ACT_NONE,
+                             mfh::GEMM_OUT_RESID_F32, pre, nullptr, E);
+    use_lo8(p, a, w_off);
+    p.partials = nullptr;
+    p.resid16 = ws.S<std::uint16_t>("act");
+    p.resid16_lo = ws.Lo("act");
+    p.ldr = E;
+    p.alpha = alpha;
+    p.ln_width = E;
+    if (res_st) {
+      p.res_stats = res_st;
+      p.res_gamma = rg;
+      p.res_beta = rb;
+      p.res_eps = res_eps;
+    }
+    if (og) {
+      // In place: each output element is read (as the residual) and then
+      // written by the same thread.
+      p.out_gamma = og;
+      p.out_stats = out_st;
+      p.C = ws.S<std::uint16_t>("act");
+      p.C_lo = ws.Lo("act");
+      p.ldc = E;
+      if (lo8_act) {
+        p.C_lo8 = ws.S<std::uint8_t>("act_lo8");
+        p.ldc8 = E;
+      }
+      MFH_RUN(run(p, role));
+      return MFH_OK;
+    }
+    MFH_RUN(run(p, role));
+    MFH_RUN(run_ln(ln(pre, M, E, eps, g, b, y32, "act")));
+    return MFH_OK;
+  };
   auto residual_ln = [&](const std::string &a, int k, const size_t (&w_off)[2],
                          const float *bias, const char *role, float alpha, float eps,
                          const float *g, const float *b, float *y32, bool f8 = false) -> int {
@@ -1537,6 +1672,35 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // One encoder layer (cpu_network.cpp:1027-1266, 1318-1457) on resid/act:
   // `heads` attention heads, FFN width `ffn`, LayerNorm epsilons after the
   // attention and the FFN, residual scale alpha.
+  // The GEMMs around the folded LayerNorms of every body layer, as the
+  // layer below sets them up (operands, lo8 codes, tiles beside the smolgen
+  // chain), must each have a tile that compiles the folded epilogue.
+  for (int li = 0; fold && li < d.L; ++li) {
+    const Layer &L = net->layers[li];
+    const int bf16 = mfh::GEMM_OUT_BF16, res = mfh::GEMM_OUT_RESID_F32;
+    mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M, 3 * E, E, nullptr, mfh::ACT_NONE, bf16,
+                              nullptr, nullptr, 3 * E);
+    use_lo8(pq, "act", L.qkv_w);
+    pq.beside_chain = L.smolgen && ws.Has("splitk_sg") && mfh::GemmWholeRoundTiles(pq);
+    mfh::GemmParams pc = gemm("act", E, L.qkv_w, E, M, d.C, E, nullptr, mfh::ACT_NONE, bf16,
+                              nullptr, nullptr, d.C);
+    pc.small_lds = pq.beside_chain;
+    mfh::GemmParams pf = gemm("act", E, L.ffn1_w, E, M, d.F, E, nullptr, d.act_ffn, bf16,
+                              nullptr, nullptr, d.F);
+    use_lo8(pf, "act", L.ffn1_w);
+    mfh::GemmParams po = gemm("ctx", E, L.out_w, E, M, E, E, nullptr, mfh::ACT_NONE, res,
+                              nullptr, nullptr, E);
+    use_lo8(po, "ctx", L.out_w);
+    mfh::GemmParams p2 = gemm("hid", d.F, L.ffn2_w, d.F, M, E, d.F, nullptr, mfh::ACT_NONE, res,
+                              nullptr, nullptr, E);
+    use_lo8(p2, "hid", L.ffn2_w);
+    fold = (li == 0 || mfh::GemmLnFoldOk(pq)) && (li == 0 || !L.smolgen || mfh::GemmLnFoldOk(pc)) &&
+           mfh::GemmLnFoldOk(pf) && mfh::GemmLnFoldOk(po) && mfh::GemmLnFoldOk(p2);
+  }
+  if (fold) {
+    st_act = ws.S<float>("st_act");
+    st_mid = ws.S<float>("st_mid");
+  }
   auto encoder_layer = [&](const Layer &L, int heads, int ffn, float eps_attn, float eps_ffn,
                            float alpha, bool body_out) -> int {
     // The smolgen chain (compression, dense1, LayerNorm, dense2, LayerNorm,
@@ -1551,6 +1715,24 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // stream so each launch is timed alone.
     const int li = layer_index++;
     const bool side_chain = M >= kSmolgenSideRows;
+    // Folded LayerNorms (body layers): LN1 always; the layer input is the
+    // previous layer's folded LN2 from layer 1 on; LN2 is folded except
+    // after the last layer, whose LayerNorm the heads read.
+    const bool body = li < d.L;
+    const bool fold_mid = fold && body;
+    const bool fold_in = fold_mid && li > 0;
+    const bool fold_out = fold_mid && !body_out;
+    const Layer *prev = fold_in ? &net->layers[li - 1] : nullptr;
+    // A GEMM reading LN(x) of folded rows (x o gamma with stats st): the
+    // LayerNorm in its epilogue with the fold constants {fold_c, bias'}.
+    auto fold_consumer = [&](mfh::GemmParams &p, const float *st, float eps,
+                             const size_t (&fc)[2], size_t skip) {
+      p.ln_stats = st;
+      p.ln_width = E;
+      p.ln_eps = eps;
+      p.fold_c = net->W<float>(fc[0]) + skip;
+      p.bias = net->W<float>(fc[1]) + skip;
+    };
     // FP8 precision from 2048 rows: Q|K|V, out-projection and FFN GEMMs on
     // per-row e4m3 copies of their inputs (the smolgen chain stays bf16).
     const bool f8 = d.fp8_act && M >= 2048;
@@ -1646,6 +1828,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
           if (pc.wscale)  // BF16X2_FP8LO column scales
             pc.wscale += skip;
         }
+        if (fold_in)
+          fold_consumer(pc, st_act, eps_ffn, L.qkv_fold, skip);
         MFH_RUN(run(pc, "smolgen_compress", on));
       }
       if (few_row_dense) {
@@ -1713,6 +1897,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
         pq.ldc8 = 3 * E;
       }
     }
+    if (fold_in)
+      fold_consumer(pq, st_act, eps_ffn, L.qkv_fold, 0);
     MFH_RUN(run(pq, "qkv"));
     if (L.smolgen && !side_chain) {
       const int rc = smolgen_chain(st);
@@ -1765,8 +1951,16 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
       StageTimer t(net, st, "attention", flops, bytes);
       MFH_RUN(mfh::LaunchAttention(ap, st, &err_));
     }
-    int rc = residual_ln("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha, eps_attn,
-                         net->W<float>(L.ln1_g), net->W<float>(L.ln1_b), res32, f8);
+    int rc = fold_mid
+                 ? residual_fold("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha,
+                                 fold_in ? st_act : nullptr,
+                                 fold_in ? net->W<float>(prev->ln2_g) : nullptr,
+                                 fold_in ? net->W<float>(prev->ln2_b) : nullptr, eps_ffn,
+                                 net->W<float>(L.ln1_g), st_mid, eps_attn, nullptr, nullptr,
+                                 nullptr)
+                 : residual_ln("ctx", E, L.out_w, net->W<float>(L.out_b), "out", alpha,
+                               eps_attn, net->W<float>(L.ln1_g), net->W<float>(L.ln1_b), res32,
+                               f8);
     if (rc != MFH_OK)
       return rc;
     mfh::GemmParams pf = gemm("act", E, L.ffn1_w, E, M, ffn, E, net->W<float>(L.ffn1_b),
@@ -1784,7 +1978,15 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
         pf.ldc8 = ffn;
       }
     }
+    if (fold_mid)
+      fold_consumer(pf, st_mid, eps_attn, L.ffn1_fold, 0);
     MFH_RUN(run(pf, "ffn1"));
+    if (fold_mid)
+      return residual_fold("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, st_mid,
+                           net->W<float>(L.ln1_g), net->W<float>(L.ln1_b), eps_attn,
+                           fold_out ? net->W<float>(L.ln2_g) : nullptr, st_act, eps_ffn,
+                           net->W<float>(L.ln2_g), net->W<float>(L.ln2_b),
+                           body_out ? resid : res32);
     rc = residual_ln("hid", ffn, L.ffn2_w, net->W<float>(L.ffn2_b), "ffn2", alpha, eps_ffn,
                      net->W<float>(L.ln2_g), net->W<float>(L.ln2_b), body_out ? resid : res32,
                      f8);

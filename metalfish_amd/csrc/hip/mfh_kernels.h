@@ -19,6 +19,10 @@ namespace mfh {
 // under 2^-20.
 constexpr int kLo8Shift = 10;
 
+// Column block of the per-row partial sums of a LayerNorm folded into GEMM
+// epilogues (GemmParams::ln_stats / out_stats).
+constexpr int kLnStatCols = 128;
+
 // Activation ids used by kernel epilogues (the C ABI maps the
 // reference's ActivationFunction values onto these).
 enum Act : int {
@@ -103,6 +107,31 @@ struct GemmParams {
   // (instead of the bf16 C_lo plane), the A_lo8 of a following GEMM.
   std::uint8_t *C_lo8 = nullptr;
   int ldc8 = 0;
+  // A LayerNorm folded into the GEMMs around it (the LayerNorm kernel then
+  // does not run).  The rows x it normalises, y = LN(x) = (x - mu) r gamma +
+  // beta with r = 1 / sqrt(E[x^2] - mu^2 + eps), are stored as x o gamma
+  // (bf16 hi + lo planes) with per-row partial sums (sum x, sum x^2) over
+  // blocks of kLnStatCols columns (ln_width / kLnStatCols pairs per row):
+  // * producer (residual mode, out_gamma set): x = resid + alpha (acc + b) is
+  //   written as x o out_gamma to C / C_lo (bf16 planes, C_lo8 codes) and
+  //   its partial sums to out_stats, instead of x in fp32;
+  // * consumer of y as the A operand (fold_c set): A holds x o gamma,
+  //   fold_c[n] = sum_k gamma_k W[n][k] and the bias is b + W beta, so
+  //   out = act(r (acc - mu fold_c[n]) + bias[n]) with the stats ln_stats;
+  // * residual y (res_stats set): resid16 / resid16_lo hold x o gamma, and
+  //   resid = r (x o gamma - mu res_gamma) + res_beta.
+  // Residual modes with out_gamma or res_stats take whole tiles at least
+  // kLnStatCols wide (LaunchGemm rejects other shapes).
+  const float *ln_stats = nullptr;
+  const float *fold_c = nullptr;
+  float ln_eps = 0.f;
+  const float *res_stats = nullptr;
+  const float *res_gamma = nullptr;
+  const float *res_beta = nullptr;
+  float res_eps = 0.f;
+  const float *out_gamma = nullptr;
+  float *out_stats = nullptr;
+  int ln_width = 0;  // width of the normalised rows (K for ln_stats, N otherwise)
   // Tiles that leave room for a concurrent launch on another stream (bf16
   // weights).  beside_chain (split precision): whole-round 256 x 256 tiles
   // take two LDS stages (96 KiB) instead of three (144 KiB).  small_lds:
@@ -136,6 +165,12 @@ constexpr long kSplitPairMaxGroups = 384;
 // Whether LaunchGemm runs `p` (bf16 activations) on 256 x 256 tiles that
 // fill whole rounds of 256 workgroups.
 bool GemmWholeRoundTiles(const GemmParams &p);
+
+// Whether LaunchGemm can run `p` with a folded LayerNorm (fold_c as a
+// consumer in the bf16 mode, out_gamma / res_stats in the residual mode):
+// a tile whose instance compiles that epilogue exists for its shape and
+// operands.  (The pointers and widths are checked at the launch.)
+bool GemmLnFoldOk(const GemmParams &p);
 
 // Row-panel GEMM: one workgroup of eight waves owns 64 whole output rows
 // and a panel of 128 * TN columns (TN = 2, 4, 6 or 8), so a row's outputs

@@ -199,6 +199,54 @@ def test_bt4_batch_256_whole_round_tiles():
         assert np.abs(wdl - small["wdl"][:hi - lo]).max() <= 1e-5
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("embedding,heads,ffn,gen,batches", [(768, 24, 1024, 256, (1024, 1000)),
+                                                             (2048, 64, 1536, 64, (256, 255, 252))])
+def test_folded_layernorm_row_widths(embedding, heads, ffn, gen, batches):
+    """The body's residual LayerNorms folded into the GEMMs around them
+    (batches whose N = E residual GEMMs fill whole rounds of 256 x 256
+    tiles) at widths other than the BT4 net's 1024: 768 (three quads of
+    per-row partial sums, each row's four-lane group one lane short) and
+    2048 (eight quads: the load rounds past the two prefetched ones run in
+    the staging), two layers with smolgen (the compression GEMM takes the
+    folded rows too); FFN1 takes 256 x 256 tiles at 768 and 256 x 128 tiles
+    at 2048.  Batch 255 folds with a partial last row tile; batches 1000
+    and 252 are no whole rounds and keep the LayerNorm kernels: the folded
+    forwards run 2L - 1 = 3 fewer LayerNorm launches than those.  Every
+    position meets the gates against the oracle, and the folded and
+    unfolded forwards agree to summation-order noise.  (The 2048-wide net's
+    smolgen makes 64 values per head: its dense2 row, heads x gen, stays
+    within the LayerNorm kernel's 8192.)"""
+    spec = synth.NetSpec(f"fold{embedding}", embedding, 2, heads, ffn, input_ffn=512,
+                         smolgen_compress=32, smolgen_hidden=256, smolgen_gen=gen,
+                         policy_dim=embedding)
+    weights = synth.make_weights(spec, seed=5)
+    n = 8
+    planes, legal = synth.playout_positions(n, seed=5)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=heads), weights).evaluate_batch(planes)
+    net = backend.create_network(spec, weights, max_batch=batches[0], device=0)
+    net.set_profiling(True)
+    outs, lns = {}, {}
+    for b in batches:
+        idx = np.arange(b) % n
+        net.profile_reset()
+        outs[b] = net.evaluate_batch(planes[idx])
+        lns[b] = net.profile().get("layernorm", {"launches": 0})["launches"]
+        pol, wdl = outs[b]["policy"], outs[b]["wdl"]
+        perr = np.abs(pol - ref["policy"][idx]).max()
+        werr = np.abs(wdl - ref["wdl"][idx]).max()
+        top1 = _top1_agreement(pol, ref["policy"][idx], legal[idx])
+        print(f"E={embedding} batch {b}: {lns[b]} LayerNorm launches, policy max-abs "
+              f"{perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}", flush=True)
+        assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
+    net.close()
+    unfolded = batches[-1]
+    for b in batches[:-1]:
+        assert lns[b] == lns[unfolded] - 3, (b, lns)
+        assert np.abs(outs[b]["policy"][:n] - outs[unfolded]["policy"][:n]).max() <= 1e-4
+        assert np.abs(outs[b]["wdl"][:n] - outs[unfolded]["wdl"][:n]).max() <= 1e-5
+
+
 @pytest.mark.parametrize("embedding,heads,batch", [(512, 16, 4), (2048, 64, 4), (512, 16, 40)])
 def test_wide_embedding_layernorm_groups(embedding, heads, batch):
     """One-layer nets of embedding width 512 and 2048 (head depth 32): their
