@@ -1100,7 +1100,22 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
   // ln_load; column t: thread t) and kept in the LDS ring behind the staged
   // rows.
   float *ln_row = tile + RB * PITCH;  // [BM][2]: mu, r
-  float *ln_col = ln_row + 2 * BM;    // [3][BN]
+  float *ln_col = ln_row + 2 * BM;    // [3][BN], see ln_col8
+  // The eight constants of column group c8 / 8 of plane `plane`: each
+  // plane holds the groups' first four columns, then their last four, so a
+  // wave's 16-byte reads of consecutive groups are consecutive (each lane's
+  // eight in one run had lanes 32 bytes apart: 0.2-0.4 bank-conflict
+  // cycles per LDS instruction in the folded epilogues).
+  auto ln_col8 = [&](int plane, int c8, float (&o)[8]) {
+    const float *b = ln_col + plane * BN + (c8 >> 3) * 4;
+    const f32x4 lo = *reinterpret_cast<const f32x4 *>(b);
+    const f32x4 hi = *reinterpret_cast<const f32x4 *>(b + BN / 2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      o[r] = lo[r];
+      o[4 + r] = hi[r];
+    }
+  };
   constexpr int THREADS = NWAVES * 64;
   float ln_c0 = 0.f, ln_c1 = 0.f, ln_c2 = 0.f;
   bool ln_on = false;
@@ -1185,9 +1200,10 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
             ln_reduce(k, ln_load(k), eps);
         }
         if (tid < BN) {
-          ln_col[tid] = ln_c0;
-          ln_col[BN + tid] = ln_c1;
-          ln_col[2 * BN + tid] = ln_c2;
+          const int cs = ((tid & 7) >> 2) * (BN / 2) + (tid >> 3) * 4 + (tid & 3);
+          ln_col[cs] = ln_c0;
+          ln_col[BN + cs] = ln_c1;
+          ln_col[2 * BN + cs] = ln_c2;
         }
       }
     }
@@ -1261,9 +1277,11 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
               // r (v - mu fold_c) from the tile's LDS constants.
               const int rt = pass * RB + rl;
               const float mu = ln_row[2 * rt], rr = ln_row[2 * rt + 1];
+              float fc[8];
+              ln_col8(0, c8, fc);
 #pragma unroll
               for (int r = 0; r < 8; ++r)
-                v[r] = rr * (v[r] - mu * ln_col[c8 + r]);
+                v[r] = rr * (v[r] - mu * fc[r]);
             }
             Finish8<MODE, ACT>(p, row, col, v, b, none);
           }
@@ -1328,9 +1346,12 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
               // LN of the residual row: r (x o gamma - mu gamma) + beta.
               const int rt = pass * RB + rl;
               const float mu = ln_row[2 * rt], rr = ln_row[2 * rt + 1];
+              float g[8], be[8];
+              ln_col8(0, c8, g);
+              ln_col8(1, c8, be);
 #pragma unroll
               for (int r = 0; r < 8; ++r)
-                rv[r] = rr * (rv[r] - mu * ln_col[c8 + r]) + ln_col[BN + c8 + r];
+                rv[r] = rr * (rv[r] - mu * g[r]) + be[r];
             }
           }
 #pragma unroll
@@ -1362,10 +1383,11 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
           if ((lane & 15) == 0)
             *reinterpret_cast<f32x2 *>(p.out_stats + (static_cast<size_t>(row) * parts +
                                                       col / kLnStatCols) * 2) = f32x2{s, s2};
-          float y[8], none[8] = {};
+          float y[8], og[8], none[8] = {};
+          ln_col8(2, c8, og);
 #pragma unroll
           for (int r = 0; r < 8; ++r)
-            y[r] = x[r] * ln_col[2 * BN + c8 + r];
+            y[r] = x[r] * og[r];
           Finish8<GEMM_OUT_BF16, ACT_NONE>(p, row, col, y, none, none);
         }
       }
