@@ -1174,15 +1174,18 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
         ln_v[k] = ln_load(k);
     }
     if (tid < BN) {
+      // (A consumer, the bf16 mode, has fold_c only.)
       const int col = min(n0 + tid, p.N - 1);
-      if (p.fold_c) {
+      if constexpr (MODE != GEMM_OUT_RESID_F32) {
         ln_c0 = p.fold_c[col];
-      } else if (p.res_stats) {
-        ln_c0 = p.res_gamma[col];
-        ln_c1 = p.res_beta[col];
+      } else {
+        if (p.res_stats) {
+          ln_c0 = p.res_gamma[col];
+          ln_c1 = p.res_beta[col];
+        }
+        if (p.out_gamma)
+          ln_c2 = p.out_gamma[col];
       }
-      if (p.out_gamma)
-        ln_c2 = p.out_gamma[col];
     }
   }
   // Rows pass * RB .. + RB of the accumulator tile into the ring.
@@ -1202,8 +1205,10 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
         if (tid < BN) {
           const int cs = ((tid & 7) >> 2) * (BN / 2) + (tid >> 3) * 4 + (tid & 3);
           ln_col[cs] = ln_c0;
-          ln_col[BN + cs] = ln_c1;
-          ln_col[2 * BN + cs] = ln_c2;
+          if constexpr (MODE == GEMM_OUT_RESID_F32) {
+            ln_col[BN + cs] = ln_c1;
+            ln_col[2 * BN + cs] = ln_c2;
+          }
         }
       }
     }
