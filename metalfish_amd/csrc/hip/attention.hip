@@ -281,11 +281,10 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
       for (int j = 0; j < 8; j += 2) {
         const float p0 = v[2 * u + j / 4][j % 4] * inv;
         const float p1 = v[2 * u + j / 4][j % 4 + 1] * inv;
-        const std::uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
-        hw[j / 2] = h0 | (static_cast<std::uint32_t>(h1) << 16);
         if constexpr (SPLIT)
-          lw[j / 2] = f32_to_bf16(p0 - bf16_to_f32(h0)) |
-                      (static_cast<std::uint32_t>(f32_to_bf16(p1 - bf16_to_f32(h1))) << 16);
+          split_bf16x2(p0, p1, hw[j / 2], lw[j / 2]);
+        else
+          hw[j / 2] = pack_bf16x2(p0, p1);
       }
       pf[u] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
       if constexpr (SPLIT)
@@ -324,23 +323,17 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionParams ap) {
     for (int dt = 0; dt < 2; ++dt) {
       const int chunk = (4 * wave + 2 * dt + (g >> 1)) ^ fr;
       const int off = fr * kCtxCols + chunk * 8 + ((g & 1) ^ (fr >> 3)) * 4;
-      std::uint16_t hi[4];
+      std::uint32_t hw[2], lw[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        hi[r] = f32_to_bf16(o[dt][r]);
-      *reinterpret_cast<u32x2 *>(stage[0] + off) =
-          u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
-                hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
-      if constexpr (SPLIT_OUT) {
-        std::uint32_t lw[2];
-#pragma unroll
-        for (int r = 0; r < 4; r += 2)
-          lw[r / 2] = f32_to_bf16(o[dt][r] - bf16_to_f32(hi[r])) |
-                      (static_cast<std::uint32_t>(
-                           f32_to_bf16(o[dt][r + 1] - bf16_to_f32(hi[r + 1])))
-                       << 16);
-        *reinterpret_cast<u32x2 *>(stage[1] + off) = u32x2{lw[0], lw[1]};
+      for (int r = 0; r < 4; r += 2) {
+        if constexpr (SPLIT_OUT)
+          split_bf16x2(o[dt][r], o[dt][r + 1], hw[r / 2], lw[r / 2]);
+        else
+          hw[r / 2] = pack_bf16x2(o[dt][r], o[dt][r + 1]);
       }
+      *reinterpret_cast<u32x2 *>(stage[0] + off) = u32x2{hw[0], hw[1]};
+      if constexpr (SPLIT_OUT)
+        *reinterpret_cast<u32x2 *>(stage[1] + off) = u32x2{lw[0], lw[1]};
     }
     // Two staging buffers: the barrier of a tile also orders every read of
     // the previous tile's buffer before the next tile overwrites it.
@@ -620,11 +613,10 @@ __global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenP
       for (int j = 0; j < 8; j += 2) {
         const float p0 = v[2 * u + j / 4][j % 4] * inv;
         const float p1 = v[2 * u + j / 4][j % 4 + 1] * inv;
-        const std::uint16_t h0 = f32_to_bf16(p0), h1 = f32_to_bf16(p1);
-        hw[j / 2] = h0 | (static_cast<std::uint32_t>(h1) << 16);
         if constexpr (SPLIT)
-          lw[j / 2] = f32_to_bf16(p0 - bf16_to_f32(h0)) |
-                      (static_cast<std::uint32_t>(f32_to_bf16(p1 - bf16_to_f32(h1))) << 16);
+          split_bf16x2(p0, p1, hw[j / 2], lw[j / 2]);
+        else
+          hw[j / 2] = pack_bf16x2(p0, p1);
       }
       pf[u] = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
       if constexpr (SPLIT)
@@ -644,23 +636,17 @@ __global__ __launch_bounds__(1024) void AttentionSmolgenKernel(AttentionSmolgenP
       const size_t off = (out_row0 + qt * 16 + fr) * E + h * kDepth + 4 * g;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        std::uint16_t hi[4];
+        std::uint32_t hw[2], lw[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          hi[r] = f32_to_bf16(o[dt][r]);
-        *reinterpret_cast<u32x2 *>(ap.ctx + off + 16 * dt) =
-            u32x2{hi[0] | (static_cast<std::uint32_t>(hi[1]) << 16),
-                  hi[2] | (static_cast<std::uint32_t>(hi[3]) << 16)};
-        if constexpr (SPLIT_OUT) {
-          std::uint32_t lw[2];
-#pragma unroll
-          for (int r = 0; r < 4; r += 2)
-            lw[r / 2] = f32_to_bf16(o[dt][r] - bf16_to_f32(hi[r])) |
-                        (static_cast<std::uint32_t>(
-                             f32_to_bf16(o[dt][r + 1] - bf16_to_f32(hi[r + 1])))
-                         << 16);
-          *reinterpret_cast<u32x2 *>(ap.ctx_lo + off + 16 * dt) = u32x2{lw[0], lw[1]};
+        for (int r = 0; r < 4; r += 2) {
+          if constexpr (SPLIT_OUT)
+            split_bf16x2(o[dt][r], o[dt][r + 1], hw[r / 2], lw[r / 2]);
+          else
+            hw[r / 2] = pack_bf16x2(o[dt][r], o[dt][r + 1]);
         }
+        *reinterpret_cast<u32x2 *>(ap.ctx + off + 16 * dt) = u32x2{hw[0], hw[1]};
+        if constexpr (SPLIT_OUT)
+          *reinterpret_cast<u32x2 *>(ap.ctx_lo + off + 16 * dt) = u32x2{lw[0], lw[1]};
       }
     }
   }

@@ -267,10 +267,10 @@ __device__ __forceinline__ void Finish8(const GemmParams &p, int row, int col, f
       u32x4 hi, lo;
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
-        const std::uint16_t h0 = f32_to_bf16(v[2 * h]), h1 = f32_to_bf16(v[2 * h + 1]);
-        hi[h] = h0 | (static_cast<unsigned>(h1) << 16);
-        lo[h] = f32_to_bf16(v[2 * h] - bf16_to_f32(h0)) |
-                (static_cast<unsigned>(f32_to_bf16(v[2 * h + 1] - bf16_to_f32(h1))) << 16);
+        std::uint32_t hw, lw;
+        split_bf16x2(v[2 * h], v[2 * h + 1], hw, lw);
+        hi[h] = hw;
+        lo[h] = lw;
       }
       *reinterpret_cast<u32x4 *>(c) = hi;
       if (c_lo)

@@ -206,10 +206,7 @@ __global__ __launch_bounds__(kWaves * 64) void PanelGemmKernel(PanelGemmParams p
         for (int h = 0; h < 2; ++h) {
           const float v0 = Act<ACT>(acc[i][j][2 * h] + bias[j][2 * h], p.act);
           const float v1 = Act<ACT>(acc[i][j][2 * h + 1] + bias[j][2 * h + 1], p.act);
-          const std::uint16_t h0 = f32_to_bf16(v0), h1 = f32_to_bf16(v1);
-          hi[h] = h0 | (static_cast<std::uint32_t>(h1) << 16);
-          lo[h] = f32_to_bf16(v0 - bf16_to_f32(h0)) |
-                  (static_cast<std::uint32_t>(f32_to_bf16(v1 - bf16_to_f32(h1))) << 16);
+          split_bf16x2(v0, v1, hi[h], lo[h]);
         }
         *reinterpret_cast<u32x2 *>(p.C + off) = u32x2{hi[0], hi[1]};
         if (p.C_lo)
@@ -300,11 +297,7 @@ __global__ __launch_bounds__(kWaves * 64) void PanelGemmKernel(PanelGemmParams p
         std::uint32_t hi[2], lo[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const std::uint16_t h0 = f32_to_bf16(y[2 * h]), h1 = f32_to_bf16(y[2 * h + 1]);
-          hi[h] = h0 | (static_cast<std::uint32_t>(h1) << 16);
-          lo[h] = f32_to_bf16(y[2 * h] - bf16_to_f32(h0)) |
-                  (static_cast<std::uint32_t>(f32_to_bf16(y[2 * h + 1] - bf16_to_f32(h1)))
-                   << 16);
+          split_bf16x2(y[2 * h], y[2 * h + 1], hi[h], lo[h]);
         }
         *reinterpret_cast<u32x2 *>(p.C + off) = u32x2{hi[0], hi[1]};
         if (p.C_lo)

@@ -115,6 +115,44 @@ def test_panel_bias_activation_against_fp64(m, n, k, split, w8, act):
     assert err <= 1e-4 * max(1.0, np.abs(y).max())
 
 
+def _rounding_cases(rng, n):
+    """float32 values whose bf16 rounding the split must get right: random
+    magnitudes over the whole range, exact ties (low half 0x8000, even and
+    odd kept bits), denormals and denormal ties, both signs, zeros."""
+    sign = rng.integers(0, 2, n, dtype=np.uint32) << 31
+    hi16 = rng.integers(0, 0x7F7F, n, dtype=np.uint32)
+    kinds = [
+        (hi16 << 16) | rng.integers(0, 1 << 16, n, dtype=np.uint32),   # anything finite
+        (hi16 << 16) | 0x8000,                                           # ties
+        rng.integers(1, 1 << 23, n, dtype=np.uint32),                    # denormals
+        (rng.integers(0, 0x80, n, dtype=np.uint32) << 16) | 0x8000,      # denormal ties
+    ]
+    bits = np.concatenate([k | sign for k in kinds])
+    bits[:4] = [0, 0x80000000, 0x00008000, 0x7F7F7FFF]
+    return bits.view(np.float32)
+
+
+def test_bf16_split_rounding_bit_exact():
+    """The epilogues' bf16 hi + lo split (hi = bf16(v), lo = bf16(v - hi),
+    round to nearest even on gfx950's v_cvt_pk_bf16_f32) against the integer
+    rounding on the host, bit for bit: a zero product plus a bias of crafted
+    values, through the row-panel GEMM's bias epilogue (the helper the tiled
+    GEMM, attention and the panel share)."""
+    rng = np.random.default_rng(11)
+    vals = _rounding_cases(rng, 3072)
+    a = np.zeros((64, 128), np.uint16)
+    w = np.zeros((3072, 128), np.uint16)
+    for c in range(0, vals.size, 3072):
+        bias = vals[c:c + 3072]
+        hi, lo = backend.panel_gemm(a, w_bits=w, bias=bias)
+        y = np.float32(0) + bias
+        want_hi, want_lo = _split(y)
+        bad = np.flatnonzero((hi != want_hi[None, :]).any(0) | (lo != want_lo[None, :]).any(0))
+        assert bad.size == 0, [(hex(int(y.view(np.uint32)[i])), hex(int(hi[0, i])),
+                                hex(int(want_hi[i])), hex(int(lo[0, i])), hex(int(want_lo[i])))
+                               for i in bad[:8]]
+
+
 def test_panel_rejects_bad_shapes():
     a = np.zeros((64, 256), np.uint16)
     w = np.zeros((320, 256), np.uint16)  # 320 columns: no panel width
