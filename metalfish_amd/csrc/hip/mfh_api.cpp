@@ -228,6 +228,7 @@ struct Dims {
   bool fused_ln = false;    // residual GEMM + LayerNorm as one row-panel launch
   bool fused_bias = false;  // smolgen bias generated inside the attention kernel
   bool skinny = true;       // few-row GEMMs for single-position forwards
+  bool fold_ln = true;      // the body's residual LayerNorms folded (kFoldRows)
   bool fp8_act = false;     // e4m3 activations on the fp8 MFMA (FP8 precision)
   bool lo8 = false;         // BF16X2_FP8LO: e4m3 lo parts on the fp8 MFMA
   int act_default = mfh::ACT_MISH, act_ffn = mfh::ACT_MISH, act_smolgen = mfh::ACT_SWISH;
@@ -640,6 +641,13 @@ int Infer(const mfh_net_desc &desc, Loader &ld, Dims &d) {
   // unless METALFISH_HIP_SKINNY=0, which keeps the split-K path at batch 1).
   const char *skinny_env = std::getenv("METALFISH_HIP_SKINNY");
   d.skinny = !(skinny_env && skinny_env[0] == '0');
+  // The body's residual LayerNorms folded into the GEMMs around them from
+  // kFoldRows (on unless METALFISH_HIP_FOLD_LN=0).  The folded GEMMs work on
+  // x o gamma and subtract mu (W . gamma) after the product, so the rounding
+  // of the stored rows counts relative to |x| rather than to |x - mu|: a
+  // row whose mean is large against its spread loses that factor.
+  const char *fold_env = std::getenv("METALFISH_HIP_FOLD_LN");
+  d.fold_ln = !(fold_env && fold_env[0] == '0');
   // BF16X2_FP8LO: the lo pass of the encoder GEMMs takes 128-byte K steps
   // over code rows laid out 128-byte aligned (K = the embedding and FFN
   // widths, in the body, the input-embedding FFN and policy encoder layers).
@@ -869,7 +877,7 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   // Folded residual LayerNorms of the body (split precisions, nets sized
   // for kFoldRows token rows): Q|K|V (+ compression) of layer i > 0 over
   // layer i - 1's LN2, FFN1 of every layer over its LN1.
-  if (d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
+  if (d.fold_ln && d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
       static_cast<long>(net->max_batch) * kSquares >= kFoldRows) {
     const int qrows = 3 * E + (d.smolgen ? d.C : 0);
     for (int i = 0; i < d.L; ++i) {
@@ -1037,8 +1045,8 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   }
   // e4m3 lo parts of the encoder GEMM inputs (BF16X2_FP8LO), at the batches
   // whose forward uses them.
-  if (d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
-      M >= static_cast<size_t>(kFoldRows)) {
+  if (d.fold_ln && d.split && !d.fp8_act && !d.fused_ln &&
+      d.E % (2 * mfh::kLnStatCols) == 0 && M >= static_cast<size_t>(kFoldRows)) {
     // Per-row partial sums of the folded LayerNorms' rows (LN2: "st_act",
     // LN1: "st_mid").
     add("st_act", M * (d.E / mfh::kLnStatCols) * 2 * 4);

@@ -247,6 +247,30 @@ def test_folded_layernorm_row_widths(embedding, heads, ffn, gen, batches):
         assert np.abs(outs[b]["wdl"][:n] - outs[unfolded]["wdl"][:n]).max() <= 1e-5
 
 
+def test_folded_layernorm_switch(monkeypatch):
+    """METALFISH_HIP_FOLD_LN=0 at net creation keeps the LayerNorm kernels at
+    a folding batch: 2L - 1 = 3 more LayerNorm launches than the folded
+    forward of the same net, the same outputs to summation-order noise."""
+    spec = synth.NetSpec("fold768", 768, 2, 24, 1024, input_ffn=512, smolgen_compress=32,
+                         smolgen_hidden=256, smolgen_gen=256, policy_dim=768)
+    weights = synth.make_weights(spec, seed=5)
+    planes, _ = synth.playout_positions(8, seed=5)
+    idx = np.arange(1024) % 8
+    outs, lns = {}, {}
+    for env in ("1", "0"):
+        monkeypatch.setenv("METALFISH_HIP_FOLD_LN", env)
+        net = backend.create_network(spec, weights, max_batch=1024, device=0)
+        net.set_profiling(True)
+        net.profile_reset()
+        outs[env] = net.evaluate_batch(planes[idx])
+        lns[env] = net.profile().get("layernorm", {"launches": 0})["launches"]
+        net.close()
+    print(f"LayerNorm launches folded {lns['1']}, switched off {lns['0']}", flush=True)
+    assert lns["0"] == lns["1"] + 3
+    assert np.abs(outs["1"]["policy"] - outs["0"]["policy"]).max() <= 1e-4
+    assert np.abs(outs["1"]["wdl"] - outs["0"]["wdl"]).max() <= 1e-5
+
+
 @pytest.mark.parametrize("embedding,heads,batch", [(512, 16, 4), (2048, 64, 4), (512, 16, 40)])
 def test_wide_embedding_layernorm_groups(embedding, heads, batch):
     """One-layer nets of embedding width 512 and 2048 (head depth 32): their
