@@ -172,27 +172,31 @@ def test_bt4_large_batch_tiles(precision, n):
         assert top1 >= 0.995
 
 
-def test_bt4_batch_256_whole_round_tiles():
+@pytest.mark.parametrize("batch", [256, 512])
+def test_bt4_batch_256_whole_round_tiles(batch):
     """Batch 256 (16384 token rows, the benchmark batch): the dense layers
     whose tile count fills whole rounds of 256 workgroups (out-projection,
     FFN2, smolgen global) take the 256 x 256 eight-wave tiles, which no
-    smaller batch reaches.  The 40 oracle-checked positions fill the batch
+    smaller batch reaches, and the body's residual LayerNorms are folded
+    into the GEMMs around them; at batch 512 FFN1 takes whole-round 256 x
+    256 tiles too.  The 40 oracle-checked positions fill the batch
     cyclically; each copy meets the bf16x2 gates against the oracle and agrees
-    with the batch-40 run (other tile shapes) to summation-order noise."""
+    with the batch-40 run (other tile shapes, no fold) to summation-order
+    noise."""
     spec = synth.SPECS["bt4"]
     weights, planes, legal, ref = _reference("bt4", 40, 0, 0)
-    idx = np.arange(256) % 40
-    net = backend.create_network(spec, weights, max_batch=256, device=0)
+    idx = np.arange(batch) % 40
+    net = backend.create_network(spec, weights, max_batch=batch, device=0)
     big = net.evaluate_batch(planes[idx])
     small = net.evaluate_batch(planes)
     net.close()
-    for lo in range(0, 256, 40):
-        hi = min(lo + 40, 256)
+    for lo in range(0, batch, 40):
+        hi = min(lo + 40, batch)
         pol, wdl = big["policy"][lo:hi], big["wdl"][lo:hi]
         perr = np.abs(pol - ref["policy"][:hi - lo]).max()
         werr = np.abs(wdl - ref["wdl"][:hi - lo]).max()
         top1 = _top1_agreement(pol, ref["policy"][:hi - lo], legal[:hi - lo])
-        print(f"bt4 x256 rows {lo}..{hi}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} "
+        print(f"bt4 x{batch} rows {lo}..{hi}: policy max-abs {perr:.3e} wdl max-abs {werr:.3e} "
               f"top1 {top1:.3f}")
         assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
         assert np.abs(pol - small["policy"][:hi - lo]).max() <= 1e-4
