@@ -350,6 +350,8 @@ struct LayerNormParams {
   int rows = 0, width = 0;
   float eps = 1e-3f;
   const float *gamma = nullptr, *beta = nullptr;
+  // Embedding gates (square rows): [64][width], square-major, 16-byte
+  // aligned; y = y * mult_gate[sq][c] + add_gate[sq][c], sq = row % 64.
   const float *mult_gate = nullptr, *add_gate = nullptr;
   float *y_f32 = nullptr;
   std::uint16_t *y_bf16 = nullptr;

@@ -216,12 +216,21 @@ __global__ __launch_bounds__(T > 256 ? T : 256) void LayerNormKernel(LayerNormPa
       const int c = c0 + 4 * q;
       f32x4 y;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 4; ++e)
         y[e] = (v[i][q][e] - mean) * inv_std * gm[i][q][e] + bt[i][q][e];
-        if (lp.mult_gate)
-          y[e] = y[e] * lp.mult_gate[static_cast<size_t>(c + e) * kSquares + sq];
-        if (lp.add_gate)
-          y[e] = y[e] + lp.add_gate[static_cast<size_t>(c + e) * kSquares + sq];
+      // Gates [64][width], square-major: four consecutive channels.
+      const size_t goff = static_cast<size_t>(sq) * width + c;
+      if (lp.mult_gate) {
+        const f32x4 m = *reinterpret_cast<const f32x4 *>(lp.mult_gate + goff);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = y[e] * m[e];
+      }
+      if (lp.add_gate) {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(lp.add_gate + goff);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = y[e] + a[e];
       }
       if (lp.y_f32)
         *reinterpret_cast<f32x4 *>(lp.y_f32 + row_off + c) = y;
@@ -438,7 +447,8 @@ hipError_t LaunchLayerNorm(const LayerNormParams &lp, hipStream_t stream, std::s
       (lp.y_bf16 && !aligned(lp.y_bf16, 8)) || (lp.y_bf16_lo && !aligned(lp.y_bf16_lo, 8)) ||
       (lp.y_lo8 && (!lp.y_bf16 || !aligned(lp.y_lo8, 8))) ||
       (lp.resid && !aligned(lp.resid, 16)) ||
-      (lp.resid16 && (!aligned(lp.resid16, 8) || !aligned(lp.resid16_lo, 8)))) {
+      (lp.resid16 && (!aligned(lp.resid16, 8) || !aligned(lp.resid16_lo, 8))) ||
+      (lp.mult_gate && !aligned(lp.mult_gate, 16)) || (lp.add_gate && !aligned(lp.add_gate, 16))) {
     Fail(err, "layernorm: width % 4 == 0 and 16-byte aligned rows required");
     return hipErrorInvalidValue;
   }
