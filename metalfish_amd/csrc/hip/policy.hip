@@ -2,15 +2,18 @@
 // promotion logits and the gather into the 1858-move policy
 // (reference src/nn/cpu/cpu_network.cpp:892-1025, gather table 91-103).
 //
-// One workgroup of 16 waves per position.  Wave w computes query rows
-// 16 (w % 4) .. + 15 of Q K^T over the interleaved quarter of the Dp
-// dimension starting at 32 (w / 4), with v_mfma_f32_16x16x32_bf16 straight
-// from global memory (Q and K rows are K-contiguous); the four partial 64x64
+// One workgroup of 16 waves per position, or up to 64 positions four, one
+// per block of 16 query rows (a single position's Q K^T on one workgroup
+// waited on that CU's loads: 45 us at batch 1).  A wave computes 16 query
+// rows against all 64 keys over an interleaved quarter (one workgroup) or
+// sixteenth (four) of the Dp dimension, with v_mfma_f32_16x16x32_bf16
+// straight from global memory (Q and K rows are K-contiguous); the partial
 // blocks go to LDS and are summed in a fixed order, then scaled by
 // 1 / sqrt(Dp).  The promotion logit for p in [0,192) is, as in the
 // reference,
 //   raw[48 + (p%64)/8][56 + (p%64)%8] + K[56 + (p%24)/3] . (promo[p%3] + promo[3]).
-// The 24 promotion-offset dot products are formed once per position.
+// The 24 promotion-offset dot products are formed once per position, by the
+// workgroup of query rows 48-63.
 // Split precision: Q and K arrive as hi + lo planes and each fragment product
 // takes three MFMAs (hi.hi + hi.lo + lo.hi).
 #include "mfh_device.h"
@@ -23,18 +26,22 @@ constexpr int kSq = 64;
 constexpr int kOutputs = 1858;
 constexpr int kMaxMoves = 256;
 
-template <bool SPLIT>
+template <bool SPLIT, int NQB>
 __global__ __launch_bounds__(1024) void PolicyMapKernel(
     const std::uint16_t *__restrict__ qk, const std::uint16_t *__restrict__ qk_lo, int dp,
     float scale, const float *__restrict__ promo, const std::int16_t *__restrict__ gather,
     float *__restrict__ policy) {
-  __shared__ float part[4][kSq * kSq];
+  // NQB workgroups per position; each takes QBW blocks of 16 query rows,
+  // its waves DC interleaved parts of the depth.
+  constexpr int QBW = 4 / NQB, DC = 16 / QBW;
+  __shared__ float part[DC][QBW * 16 * kSq];
   __shared__ float pk_term[24];
   __shared__ float pk_wave[16][24];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int qb = wave & 3, dc = wave >> 2;
-  const int b = blockIdx.x;
+  const int qbl = wave % QBW, dc = wave / QBW;
+  const int qb = blockIdx.x * QBW + qbl, b = blockIdx.y;
+  const int row0 = 16 * QBW * blockIdx.x;  // the workgroup's first query row
   const size_t ld = static_cast<size_t>(2) * dp;
   const size_t pos = static_cast<size_t>(b) * kSq * ld;
   const std::uint16_t *base = qk + pos;
@@ -46,7 +53,7 @@ __global__ __launch_bounds__(1024) void PolicyMapKernel(
     acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const size_t qoff = (qb * 16 + fr) * ld + fc;
 #pragma unroll 2
-  for (int k0 = dc * 32; k0 < dp; k0 += 128) {
+  for (int k0 = dc * 32; k0 < dp; k0 += 32 * DC) {
     const bf16x8 a = *reinterpret_cast<const bf16x8 *>(base + qoff + k0);
     bf16x8 kb[4];
 #pragma unroll
@@ -66,46 +73,50 @@ __global__ __launch_bounds__(1024) void PolicyMapKernel(
       }
     }
   }
+  // Query row q of the workgroup at (q - row0) * 64.
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      part[dc][(qb * 16 + (lane >> 4) * 4 + r) * kSq + j * 16 + fr] = acc[j][r];
+      part[dc][(qbl * 16 + (lane >> 4) * 4 + r) * kSq + j * 16 + fr] = acc[j][r];
 
-  // Promotion offsets: term[t][tf] = K[56+tf] . (promo[t] + promo[3]).
-  // Thread c takes depth c (c, c + 1024, ...) of all 24 products, so every
-  // load is issued before any sum waits on one (a single position is
-  // latency-bound here); then one wave sum per product and a fixed-order
-  // sum over the 16 waves.
-  float term[24];
+  // Promotion offsets (the workgroup of query rows 48-63 only; the branch
+  // is uniform over the workgroup): term[t][tf] = K[56+tf] . (promo[t] +
+  // promo[3]).  Thread c takes depth c (c, c + 1024, ...) of all 24
+  // products, so every load is issued before any sum waits on one; then one
+  // wave sum per product and a fixed-order sum over the 16 waves.
+  const bool promos = blockIdx.x == NQB - 1;
+  if (promos) {
+    float term[24];
 #pragma unroll
-  for (int d = 0; d < 24; ++d)
-    term[d] = 0.f;
-  for (int c = threadIdx.x; c < dp; c += 1024) {
-    float pr[3];
-    const float p3 = promo[static_cast<size_t>(3) * dp + c];
-#pragma unroll
-    for (int t = 0; t < 3; ++t)
-      pr[t] = promo[static_cast<size_t>(t) * dp + c] + p3;
-#pragma unroll
-    for (int tf = 0; tf < 8; ++tf) {
-      const size_t koff = (56 + tf) * ld + dp + c;
-      float kv = bf16_to_f32(base[koff]);
-      if constexpr (SPLIT)
-        kv += bf16_to_f32(qk_lo[pos + koff]);
+    for (int d = 0; d < 24; ++d)
+      term[d] = 0.f;
+    for (int c = threadIdx.x; c < dp; c += 1024) {
+      float pr[3];
+      const float p3 = promo[static_cast<size_t>(3) * dp + c];
 #pragma unroll
       for (int t = 0; t < 3; ++t)
-        term[t * 8 + tf] += kv * pr[t];
+        pr[t] = promo[static_cast<size_t>(t) * dp + c] + p3;
+#pragma unroll
+      for (int tf = 0; tf < 8; ++tf) {
+        const size_t koff = (56 + tf) * ld + dp + c;
+        float kv = bf16_to_f32(base[koff]);
+        if constexpr (SPLIT)
+          kv += bf16_to_f32(qk_lo[pos + koff]);
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+          term[t * 8 + tf] += kv * pr[t];
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < 24; ++d) {
+      const float w = wave_sum(term[d]);
+      if (lane == 0)
+        pk_wave[wave][d] = w;
     }
   }
-#pragma unroll
-  for (int d = 0; d < 24; ++d) {
-    const float w = wave_sum(term[d]);
-    if (lane == 0)
-      pk_wave[wave][d] = w;
-  }
   __syncthreads();
-  if (threadIdx.x < 24) {
+  if (promos && threadIdx.x < 24) {
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < 16; ++w)
@@ -114,19 +125,32 @@ __global__ __launch_bounds__(1024) void PolicyMapKernel(
   }
   __syncthreads();
 
+  // Each workgroup writes the outputs whose logit lies in its query rows
+  // (the first also the ones with no logit; the last the promotions,
+  // queries 48-55).
   float *out = policy + static_cast<size_t>(b) * kOutputs;
-  auto raw = [&](int i) { return (((part[0][i] + part[1][i]) + part[2][i]) + part[3][i]) * scale; };
+  auto raw = [&](int q, int k) {
+    const int i = (q - row0) * kSq + k;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < DC; ++w)
+      v += part[w][i];
+    return v * scale;
+  };
   for (int i = threadIdx.x; i < kOutputs; i += 1024) {
     const int r = gather[i];
-    float v = 0.f;
     if (r >= 0 && r < kSq * kSq) {
-      v = raw(r);
+      if (r / kSq / (16 * QBW) == static_cast<int>(blockIdx.x))
+        out[i] = raw(r / kSq, r % kSq);
     } else if (r >= kSq * kSq) {
-      const int p = r - kSq * kSq;
-      const int pair = p % kSq;
-      v = raw((48 + pair / 8) * kSq + 56 + pair % 8) + pk_term[(p % 3) * 8 + (p % 24) / 3];
+      if (promos) {
+        const int p = r - kSq * kSq;
+        const int pair = p % kSq;
+        out[i] = raw(48 + pair / 8, 56 + pair % 8) + pk_term[(p % 3) * 8 + (p % 24) / 3];
+      }
+    } else if (blockIdx.x == 0) {
+      out[i] = 0.f;
     }
-    out[i] = v;
   }
 }
 
@@ -223,19 +247,30 @@ hipError_t LaunchPolicyPriors(const float *policy, const std::int32_t *offsets,
 hipError_t LaunchPolicyMap(const std::uint16_t *qk, const std::uint16_t *qk_lo, int batch,
                            int dp, const float *promo, const std::int16_t *gather,
                            float *policy, hipStream_t stream, std::string *err) {
-  if (batch <= 0 || dp <= 0 || dp % 32 || !qk || !promo || !gather || !policy ||
+  if (batch <= 0 || batch > 65535 || dp <= 0 || dp % 32 || !qk || !promo || !gather || !policy ||
       (reinterpret_cast<std::uintptr_t>(qk) & 15u) ||
       (qk_lo && (reinterpret_cast<std::uintptr_t>(qk_lo) & 15u))) {
     if (err)
-      *err = "policy_map: needs batch > 0, Dp % 32 == 0 and 16-byte aligned Q|K";
+      *err = "policy_map: needs 0 < batch <= 65535, Dp % 32 == 0 and 16-byte aligned Q|K";
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(dp));
-  if (qk_lo)
-    hipLaunchKernelGGL(PolicyMapKernel<true>, dim3(batch), dim3(1024), 0, stream, qk, qk_lo, dp,
+  // Four workgroups per position while they fit on the CUs at once (up to
+  // 64 positions: batch 1 1.179 -> 1.150 ms, batch 32 +1.1 %), one above
+  // (four at batch 256 were 0.4 % slower: K read by every workgroup).
+  const bool four = batch <= 64;
+  const dim3 grid(four ? 4 : 1, batch);
+  if (qk_lo && four)
+    hipLaunchKernelGGL((PolicyMapKernel<true, 4>), grid, dim3(1024), 0, stream, qk, qk_lo, dp,
+                       scale, promo, gather, policy);
+  else if (qk_lo)
+    hipLaunchKernelGGL((PolicyMapKernel<true, 1>), grid, dim3(1024), 0, stream, qk, qk_lo, dp,
+                       scale, promo, gather, policy);
+  else if (four)
+    hipLaunchKernelGGL((PolicyMapKernel<false, 4>), grid, dim3(1024), 0, stream, qk, qk_lo, dp,
                        scale, promo, gather, policy);
   else
-    hipLaunchKernelGGL(PolicyMapKernel<false>, dim3(batch), dim3(1024), 0, stream, qk, qk_lo, dp,
+    hipLaunchKernelGGL((PolicyMapKernel<false, 1>), grid, dim3(1024), 0, stream, qk, qk_lo, dp,
                        scale, promo, gather, policy);
   return hipGetLastError();
 }
