@@ -59,27 +59,29 @@ __device__ __forceinline__ int Swz(int row, int chunk) {
 }
 
 // mu and r = 1 / sqrt(var + eps) of row `row` of a folded LayerNorm from
-// its partial sums (width / kLnStatCols (sum x, sum x^2) pairs, added in
-// order), with the reference formula var = E[x^2] - mu^2 clamped at 0.
-__device__ __forceinline__ void RowLnStats(const float *stats, int width, float eps, int row,
-                                           float &mu, float &r) {
-  const int pairs2 = width / (2 * kLnStatCols);
+// its partial sums (width / part (sum x, sum x^2) pairs, added in order),
+// with the reference formula var = E[x^2] - mu^2 clamped at 0.
+__device__ __forceinline__ void RowLnStats(const float *stats, int width, int part, float eps,
+                                           int row, float &mu, float &r) {
+  const int pairs2 = width / (2 * part);
   const f32x4 *q = reinterpret_cast<const f32x4 *>(stats) + static_cast<size_t>(row) * pairs2;
-  // Up to 8 quads (width <= 2048), loaded together.
-  f32x4 v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < pairs2)
-      v[i] = q[i];
   float s = 0.f, s2 = 0.f;
+  // Eight quads at a time, loaded together.
+  for (int i0 = 0; i0 < pairs2; i0 += 8) {
+    f32x4 v[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    if (i < pairs2) {
-      s += v[i][0];
-      s2 += v[i][1];
-      s += v[i][2];
-      s2 += v[i][3];
-    }
+    for (int i = 0; i < 8; ++i)
+      if (i0 + i < pairs2)
+        v[i] = q[i0 + i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i0 + i < pairs2) {
+        s += v[i][0];
+        s2 += v[i][1];
+        s += v[i][2];
+        s2 += v[i][3];
+      }
+  }
   mu = s / static_cast<float>(width);
   float var = s2 / static_cast<float>(width) - mu * mu;
   var = var < 0.f ? 0.f : var;
@@ -102,7 +104,7 @@ __device__ __forceinline__ void LoadVec8(const float *v, int col, float (&o)[8])
 // costs registers the 256 x 128 tiles do not have.)
 __device__ __forceinline__ void FoldLn8(const GemmParams &p, int row, int col, float (&v)[8]) {
   float mu, rr;
-  RowLnStats(p.ln_stats, p.ln_width, p.ln_eps, row, mu, rr);
+  RowLnStats(p.ln_stats, p.ln_width, p.ln_part, p.ln_eps, row, mu, rr);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const f32x4 c = *reinterpret_cast<const f32x4 *>(p.fold_c + col + 4 * h);
@@ -129,7 +131,7 @@ __device__ __forceinline__ void Epilogue4(const GemmParams &p, int row, int col,
   if (LN && p.fold_c) {
     // Consumer of a folded LayerNorm (never in the residual mode).
     float mu, rr;
-    RowLnStats(p.ln_stats, p.ln_width, p.ln_eps, row, mu, rr);
+    RowLnStats(p.ln_stats, p.ln_width, p.ln_part, p.ln_eps, row, mu, rr);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       acc[r] = rr * (acc[r] - mu * (col + r < p.N ? p.fold_c[col + r] : 0.f));
@@ -396,7 +398,8 @@ constexpr int StagedRows() {
 }
 template <int BN, int THREADS, int RB>
 constexpr bool GemmLnEpilogueOk() {
-  return (BN == 128 || BN == 256) && THREADS % (BN / 8) == 0 && (RB * (BN / 8)) % THREADS == 0;
+  return (BN == 64 || BN == 128 || BN == 256) && THREADS % (BN / 8) == 0 &&
+         (RB * (BN / 8)) % THREADS == 0;
 }
 
 // fp8 weights (W8): the e4m3 rows go through the LDS ring as bytes (BK
@@ -1164,7 +1167,7 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
     // (sum, sum^2) pairs, a power of two, 64 at most), the first kLnPre
     // rounds of loads issued here so they are in flight during the staging.
     if (st) {
-      ln_q = p.ln_width / (2 * kLnStatCols);
+      ln_q = p.ln_width / (2 * p.ln_part);
       ln_g = 1;
       while (ln_g < ln_q)
         ln_g <<= 1;
@@ -1316,22 +1319,24 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
     }
     return;
   }
-  if constexpr (LN && MODE == GEMM_OUT_RESID_F32 && BN == 256 &&
+  if constexpr (LN && MODE == GEMM_OUT_RESID_F32 && (BN == 256 || BN == 64) &&
                 GemmLnEpilogueOk<BN, THREADS, RB>()) {
     if (PIPE || p.out_gamma || p.res_stats) {
       // Residual mode with a folded LayerNorm on either side (whole tiles,
       // checked by the launcher): the residual is LN(x) of x o gamma rows
       // (res_stats), and/or the result x = resid + alpha (acc + b) leaves
       // as x o out_gamma in bf16 hi + lo (+ e4m3 codes) with the partial
-      // sums of x over each 128-column block: a block is 16 consecutive
-      // lanes of one row (8 columns each), summed by shuffles in a fixed
-      // order.  A thread keeps one column group for the whole tile.
+      // sums of x over each block of kPart columns (128 on 256-wide tiles,
+      // 64 on 64-wide ones): a block is kPart / 8 consecutive lanes of one
+      // row (8 columns each), summed by shuffles in a fixed order.  A
+      // thread keeps one column group for the whole tile.
+      constexpr int kPartLanes = BN == 64 ? 8 : 16, kPart = 8 * kPartLanes;
       int c8, r0;
       group_of(tid, r0, c8);
       const int col = n0 + c8;
       float b[8], sc[8];
       LoadBiasScale8(p, col, b, sc);
-      const int parts = p.ln_width / kLnStatCols;
+      const int parts = p.ln_width / kPart;
 #pragma unroll 1
       for (int pass = 0; pass < BM / RB; ++pass) {
         stage(pass);
@@ -1379,15 +1384,15 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
             s2 += x[r] * x[r];
           }
 #pragma unroll
-          for (int m = 1; m < 16; m <<= 1) {
+          for (int m = 1; m < kPartLanes; m <<= 1) {
             s += __shfl_xor(s, m, 64);
             s2 += __shfl_xor(s2, m, 64);
           }
           if (!valid)
             continue;
-          if ((lane & 15) == 0)
+          if ((lane & (kPartLanes - 1)) == 0)
             *reinterpret_cast<f32x2 *>(p.out_stats + (static_cast<size_t>(row) * parts +
-                                                      col / kLnStatCols) * 2) = f32x2{s, s2};
+                                                      col / kPart) * 2) = f32x2{s, s2};
           float y[8], og[8], none[8] = {};
           ln_col8(2, c8, og);
 #pragma unroll
@@ -1460,9 +1465,10 @@ hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   constexpr int kRb = StagedRows<BM, BN, ST, GemmStageBytes<BM, BN, BK, WM, WN, SPLIT, W8>()>();
   if constexpr (MODE == GEMM_OUT_RESID_F32) {
     // The folded-LayerNorm residual epilogue takes whole 256-wide tiles.
+    // (Partial sums per 128 columns on 256-wide tiles, per 64 on 64-wide.)
     if ((p.out_gamma || p.res_stats) &&
-        !(LN && BN == 256 && GemmLnEpilogueOk<BN, WM * WN * 64, kRb>() && p.vec8 &&
-          p.N % BN == 0))
+        !(LN && (BN == 256 || BN == 64) && GemmLnEpilogueOk<BN, WM * WN * 64, kRb>() &&
+          p.vec8 && p.N % BN == 0 && p.ln_part == (BN == 64 ? 64 : 128)))
       return hipErrorInvalidValue;
     if (LN && PIPE && !p.out_gamma && !p.res_stats)
       return hipErrorInvalidValue;
@@ -1519,10 +1525,10 @@ hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
   // A folded LayerNorm (GemmParams::fold_c / out_gamma / res_stats): its
   // epilogue code is compiled only into the tiles that take it (LnFoldTile:
   // the pipelined split-precision and BF16X2_FP8LO tiles of the large
-  // batches, and the small-LDS split 64 x 64 tile of the smolgen
-  // compression beside Q|K|V), bf16 outputs and the residual mode.
-  constexpr bool kLn = !W8 && !F8 && (SPLIT || LO8) &&
-                       (PIPE || (BM == 64 && BN == 64 && BK == 32));
+  // batches, the small-LDS split 64 x 64 tile of the smolgen compression
+  // beside Q|K|V, and the split 64 x 64 tiles of 24-63 positions), bf16
+  // outputs and the residual mode.
+  constexpr bool kLn = !W8 && !F8 && (SPLIT || LO8) && (PIPE || (BM == 64 && BN == 64));
   if (p.fold_c || p.out_gamma || p.res_stats) {
     if constexpr (kLn) {
       if (p.k_splits == 1 && p.out_mode == GEMM_OUT_RESID_F32)
@@ -1592,7 +1598,7 @@ namespace {
 // GEMM with a folded LayerNorm runs on (the tiles the same shapes take
 // without it, where those are among them): split precision (bf16 hi + lo
 // activations, or the BF16X2_FP8LO codes), bf16 weights, one K slice.
-enum class LnTile { kNone, kLo8, k256, k256Beside, k256x128, k64 };
+enum class LnTile { kNone, kLo8, k256, k256Beside, k256x128, k64, k64x64 };
 
 LnTile LnFoldTile(const GemmParams &p) {
   const bool res = p.out_mode == GEMM_OUT_RESID_F32;
@@ -1600,12 +1606,16 @@ LnTile LnFoldTile(const GemmParams &p) {
     return LnTile::kNone;
   if (!res && p.out_mode != GEMM_OUT_BF16)
     return LnTile::kNone;
-  // 256-wide whole tiles (the residual side always; a consumer's epilogue
-  // on the pipelined tiles too).
+  // Whole rounds of 256-wide whole tiles.
   if (p.A_lo8)
     return p.N % 256 == 0 ? LnTile::kLo8 : LnTile::kNone;
-  if (p.N % 256 == 0 && (res || GemmWholeRoundTiles(p)))
+  if (p.N % 256 == 0 && GemmWholeRoundTiles(p))
     return p.beside_chain && !res ? LnTile::k256Beside : LnTile::k256;
+  // Fewer 128 x 128 tiles than CUs (24-63 positions at the BT4 widths): the
+  // 64 x 64 tiles over the whole K that these shapes take without the fold.
+  const long tiles128 = static_cast<long>((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (p.M >= kLargeRows && p.N >= 128 && tiles128 < 256 && p.N % 64 == 0)
+    return LnTile::k64x64;
   if (res)
     return LnTile::kNone;
   // Consumers: the small-LDS 64 x 64 tiles beside Q|K|V (any width), else
@@ -1723,22 +1733,25 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
   // Folded LayerNorm (see GemmParams): consumer and residual sides.
   const bool ln_res = p.out_mode == GEMM_OUT_RESID_F32 && (p.out_gamma || p.res_stats);
   if (p.fold_c && (!p.ln_stats || p.out_mode == GEMM_OUT_RESID_F32 || p.ln_width != p.K ||
-                   p.K % (2 * kLnStatCols) || p.K > 128 * kLnStatCols ||
+                   (p.ln_part != 64 && p.ln_part != 128) || p.K % (2 * p.ln_part) ||
+                   p.K > 128 * p.ln_part ||
                    !Aligned(p.fold_c, 16) ||
                    !Aligned(p.ln_stats, 16) || p.k_splits != 1))
-    return fail("folded LayerNorm consumer: ln_stats, fold_c (16-byte aligned), K = ln_width "
-                "a multiple of 256 up to 16384, one K slice, not the residual mode");
+    return fail("folded LayerNorm consumer: ln_stats, fold_c (16-byte aligned), ln_part 64 or "
+                "128, K = ln_width a multiple of 2 ln_part up to 128 ln_part, one K slice, not "
+                "the residual mode");
   if ((p.out_gamma || p.res_stats) && !ln_res)
     return fail("folded LayerNorm output / residual: residual mode only");
   if (ln_res && (!p.resid16 || p.k_splits != 1 || p.ln_width != p.N ||
-                 p.N % (2 * kLnStatCols) || p.N > 128 * kLnStatCols ||
+                 (p.ln_part != 64 && p.ln_part != 128) || p.N % (2 * p.ln_part) ||
+                 p.N > 128 * p.ln_part ||
                  (p.res_stats && (!p.res_gamma || !p.res_beta || !Aligned(p.res_stats, 16) ||
                                   !Aligned(p.res_gamma, 16) || !Aligned(p.res_beta, 16))) ||
                  (p.out_gamma && (!p.out_stats || !Aligned(p.out_gamma, 16) ||
                                   !Aligned(p.out_stats, 8) || !p.C_lo))))
-    return fail("folded LayerNorm residual: split residual, one K slice, N = ln_width a "
-                "multiple of 256 up to 16384, gamma / beta / stats 16-byte aligned, a bf16 lo output "
-                "plane with out_gamma");
+    return fail("folded LayerNorm residual: split residual, one K slice, ln_part 64 or 128, "
+                "N = ln_width a multiple of 2 ln_part up to 128 ln_part, gamma / beta / stats "
+                "16-byte aligned, a bf16 lo output plane with out_gamma");
   if (p.C_lo8 && !(p.out_mode == GEMM_OUT_RESID_F32 && p.out_gamma) &&
       (p.out_mode != GEMM_OUT_BF16 || p.C_lo || p.split_n < p.N || p.k_splits != 1 ||
        p.ldc8 < p.N || p.ldc8 % 8 || !Aligned(p.C_lo8, 8)))
@@ -1783,6 +1796,8 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       return LaunchW<256, 128, 32, 2, 4, 2, true, false, false, true>(p, stream);
     case LnTile::k64:
       return LaunchW<64, 64, 32, 2, 2, 2, true, false>(p, stream);
+    case LnTile::k64x64:
+      return LaunchW<64, 64, 64, 2, 2, 2, true, false>(p, stream);
     default:
       return fail("folded LayerNorm: split-precision activations, bf16 weights, one K slice, "
                   "K % 64 == 0 and N a multiple of 256 (residual, BF16X2_FP8LO codes) or "

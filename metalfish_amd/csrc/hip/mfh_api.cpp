@@ -111,6 +111,10 @@ constexpr int kLo8MinRows = 8192;
 // the LayerNorm in their epilogue, the next residual rebuilds it), where
 // the residual GEMMs (N = E) take whole rounds of 256 x 256 tiles.
 constexpr long kFoldRows = 16384;
+// From this many token rows (24 positions), where the residual GEMMs take 64
+// x 64 tiles over the whole K, LN1 alone is folded (out-projection -> FFN1
+// and FFN2); the 64-wide residual tiles write partial sums per 64 columns.
+constexpr long kFoldLn1Rows = 1536;
 
 std::uint16_t ToBf16(float f) {
   std::uint32_t u;
@@ -265,8 +269,9 @@ struct mfh_net {
   // BF16X2_FP8LO: offset of a dense weight's W' (bf16, with column scales) ->
   // offset of its e4m3 codes.
   std::map<size_t, size_t> lo8_codes;
-  // The body's fold constants were packed (Layer::qkv_fold / ffn1_fold).
-  bool has_fold = false;
+  // The body's fold constants were packed (Layer::qkv_fold / ffn1_fold;
+  // ffn1_fold alone for has_fold1).
+  bool has_fold = false, has_fold1 = false;
   size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
   size_t head_w[2], qk_w[2], val1_w[2];
   size_t mov_b = 0, mov1_b = 0, mov2_w = 0, mov2_b = 0;  // moves-left head
@@ -889,14 +894,16 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
   // Folded residual LayerNorms of the body (split precisions, nets sized
   // for kFoldRows token rows): Q|K|V (+ compression) of layer i > 0 over
   // layer i - 1's LN2, FFN1 of every layer over its LN1.
+  // (FFN1 over LN1 alone for nets sized for kFoldLn1Rows.)
+  const long net_rows = static_cast<long>(net->max_batch) * kSquares;
   if (d.fold_ln && d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
-      static_cast<long>(net->max_batch) * kSquares >= kFoldRows) {
+      net_rows >= kFoldLn1Rows) {
     const int qrows = 3 * E + (d.smolgen ? d.C : 0);
     for (int i = 0; i < d.L; ++i) {
       Layer &L = net->layers[i];
       const bool qlo8 = net->lo8_codes.count(L.qkv_w[0]) > 0;
       const bool flo8 = net->lo8_codes.count(L.ffn1_w[0]) > 0;
-      if (i > 0) {
+      if (i > 0 && net_rows >= kFoldRows) {
         const Layer &P = net->layers[i - 1];
         AddLnFold(blob, L.qkv_w, net->fp8, qlo8, qrows, E, P.ln2_g, P.ln2_b, L.qkv_b,
                   L.qkv_fold);
@@ -904,7 +911,8 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       AddLnFold(blob, L.ffn1_w, net->fp8, flo8, d.F, E, L.ln1_g, L.ln1_b, L.ffn1_b,
                 L.ffn1_fold);
     }
-    net->has_fold = true;
+    net->has_fold = net_rows >= kFoldRows;
+    net->has_fold1 = true;
   }
   // Policy encoder layers (weights.cpp:188-203), no smolgen.
   net->pol_layers.resize(d.PL);
@@ -1058,11 +1066,12 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
   // e4m3 lo parts of the encoder GEMM inputs (BF16X2_FP8LO), at the batches
   // whose forward uses them.
   if (d.fold_ln && d.split && !d.fp8_act && !d.fused_ln &&
-      d.E % (2 * mfh::kLnStatCols) == 0 && M >= static_cast<size_t>(kFoldRows)) {
+      d.E % (2 * mfh::kLnStatCols) == 0 && M >= static_cast<size_t>(kFoldLn1Rows)) {
     // Per-row partial sums of the folded LayerNorms' rows (LN2: "st_act",
-    // LN1: "st_mid").
-    add("st_act", M * (d.E / mfh::kLnStatCols) * 2 * 4);
-    add("st_mid", M * (d.E / mfh::kLnStatCols) * 2 * 4);
+    // LN1: "st_mid"), per 64 columns at most.
+    if (M >= static_cast<size_t>(kFoldRows))
+      add("st_act", M * (d.E / 64) * 2 * 4);
+    add("st_mid", M * (d.E / 64) * 2 * 4);
   }
   if (d.lo8 && M >= static_cast<size_t>(kLo8MinRows)) {
     add("act_lo8", M * d.E);
@@ -1311,7 +1320,13 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // the folded epilogue.)
   bool fold = net->has_fold && full && ws.Has("st_act") && whole_round(M, E) &&
               M >= kSmolgenSideRows;
+  // Below whole rounds (kFoldLn1Rows on): LN1 alone, on the 64 x 64
+  // residual tiles (partial sums per 64 columns).
+  bool fold1 = !fold && net->has_fold1 && full && ws.Has("st_mid") && M >= kFoldLn1Rows;
   float *st_act = nullptr, *st_mid = nullptr;
+  // Columns per partial sum: 128 on the whole-round 256-wide tiles, 64 on
+  // the 64-wide ones (set with the fold below).
+  int ln_part = 128;
   auto ln = [&](const float *x, int rows, int width, float eps, const float *g, const float *b,
                 float *y32, const std::string &y16) {
     mfh::LayerNormParams lp;
@@ -1458,6 +1473,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     p.ldr = E;
     p.alpha = alpha;
     p.ln_width = E;
+    p.ln_part = ln_part;
     if (res_st) {
       p.res_stats = res_st;
       p.res_gamma = rg;
@@ -1717,10 +1733,32 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     fold = (li == 0 || mfh::GemmLnFoldOk(pq)) && (li == 0 || !L.smolgen || mfh::GemmLnFoldOk(pc)) &&
            mfh::GemmLnFoldOk(pf) && mfh::GemmLnFoldOk(po) && mfh::GemmLnFoldOk(p2);
   }
+  // LN1 alone: the out-projection (writing x o gamma1 with its sums), FFN1
+  // (its consumer) and FFN2 (rebuilding the residual) on 64-wide tiles.
+  for (int li = 0; fold1 && li < d.L; ++li) {
+    const Layer &L = net->layers[li];
+    const int bf16 = mfh::GEMM_OUT_BF16, res = mfh::GEMM_OUT_RESID_F32;
+    mfh::GemmParams pf = gemm("act", E, L.ffn1_w, E, M, d.F, E, nullptr, d.act_ffn, bf16,
+                              nullptr, nullptr, d.F);
+    mfh::GemmParams po = gemm("ctx", E, L.out_w, E, M, E, E, nullptr, mfh::ACT_NONE, res,
+                              nullptr, nullptr, E);
+    mfh::GemmParams p2 = gemm("hid", d.F, L.ffn2_w, d.F, M, E, d.F, nullptr, mfh::ACT_NONE, res,
+                              nullptr, nullptr, E);
+    const mfh::GemmParams *ps[3] = {&pf, &po, &p2};
+    for (const mfh::GemmParams *q : ps)
+      fold1 = fold1 && !q->A_lo8 && mfh::GemmLnFoldOk(*q);
+    // (The residual tiles must be the 64-wide ones their sums assume, and
+    // FFN1 keeps the 64-wide tiles it takes without the fold.)
+    auto t128 = [&](int n) { return static_cast<long>((M + 127) / 128) * ((n + 127) / 128); };
+    fold1 = fold1 && t128(E) < 256 && t128(d.F) < 256;
+  }
   if (fold) {
     st_act = ws.S<float>("st_act");
     st_mid = ws.S<float>("st_mid");
+  } else if (fold1) {
+    st_mid = ws.S<float>("st_mid");
   }
+  ln_part = fold ? 128 : 64;
   auto encoder_layer = [&](const Layer &L, int heads, int ffn, float eps_attn, float eps_ffn,
                            float alpha, bool body_out) -> int {
     // The smolgen chain (compression, dense1, LayerNorm, dense2, LayerNorm,
@@ -1739,9 +1777,9 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // previous layer's folded LN2 from layer 1 on; LN2 is folded except
     // after the last layer, whose LayerNorm the heads read.
     const bool body = li < d.L;
-    const bool fold_mid = fold && body;
-    const bool fold_in = fold_mid && li > 0;
-    const bool fold_out = fold_mid && !body_out;
+    const bool fold_mid = (fold || fold1) && body;
+    const bool fold_in = fold && body && li > 0;
+    const bool fold_out = fold && body && !body_out;
     const Layer *prev = fold_in ? &net->layers[li - 1] : nullptr;
     // A GEMM reading LN(x) of folded rows (x o gamma with stats st): the
     // LayerNorm in its epilogue with the fold constants {fold_c, bias'}.
@@ -1749,6 +1787,7 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
                              const size_t (&fc)[2], size_t skip) {
       p.ln_stats = st;
       p.ln_width = E;
+      p.ln_part = ln_part;
       p.ln_eps = eps;
       p.fold_c = net->W<float>(fc[0]) + skip;
       p.bias = net->W<float>(fc[1]) + skip;

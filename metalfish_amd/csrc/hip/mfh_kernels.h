@@ -20,7 +20,8 @@ namespace mfh {
 constexpr int kLo8Shift = 10;
 
 // Column block of the per-row partial sums of a LayerNorm folded into GEMM
-// epilogues (GemmParams::ln_stats / out_stats).
+// epilogues (GemmParams::ln_stats / out_stats): 128 columns, or 64 where
+// the residual GEMMs take 64-wide tiles (GemmParams::ln_part).
 constexpr int kLnStatCols = 128;
 
 // Activation ids used by kernel epilogues (the C ABI maps the
@@ -111,7 +112,7 @@ struct GemmParams {
   // does not run).  The rows x it normalises, y = LN(x) = (x - mu) r gamma +
   // beta with r = 1 / sqrt(E[x^2] - mu^2 + eps), are stored as x o gamma
   // (bf16 hi + lo planes) with per-row partial sums (sum x, sum x^2) over
-  // blocks of kLnStatCols columns (ln_width / kLnStatCols pairs per row):
+  // blocks of ln_part columns (ln_width / ln_part pairs per row):
   // * producer (residual mode, out_gamma set): x = resid + alpha (acc + b) is
   //   written as x o out_gamma to C / C_lo (bf16 planes, C_lo8 codes) and
   //   its partial sums to out_stats, instead of x in fp32;
@@ -120,8 +121,8 @@ struct GemmParams {
   //   out = act(r (acc - mu fold_c[n]) + bias[n]) with the stats ln_stats;
   // * residual y (res_stats set): resid16 / resid16_lo hold x o gamma, and
   //   resid = r (x o gamma - mu res_gamma) + res_beta.
-  // Residual modes with out_gamma or res_stats take whole tiles at least
-  // kLnStatCols wide (LaunchGemm rejects other shapes).
+  // Residual modes with out_gamma or res_stats take whole tiles of 256 or
+  // (ln_part 64) 64 columns (LaunchGemm rejects other shapes).
   const float *ln_stats = nullptr;
   const float *fold_c = nullptr;
   float ln_eps = 0.f;
@@ -132,6 +133,7 @@ struct GemmParams {
   const float *out_gamma = nullptr;
   float *out_stats = nullptr;
   int ln_width = 0;  // width of the normalised rows (K for ln_stats, N otherwise)
+  int ln_part = kLnStatCols;  // columns per partial-sum block: 128 or 64
   // Tiles that leave room for a concurrent launch on another stream (bf16
   // weights).  beside_chain (split precision): whole-round 256 x 256 tiles
   // take two LDS stages (96 KiB) instead of three (144 KiB).  small_lds:

@@ -275,6 +275,42 @@ def test_folded_layernorm_switch(monkeypatch):
     assert np.abs(outs["1"]["wdl"] - outs["0"]["wdl"]).max() <= 1e-5
 
 
+@pytest.mark.parametrize("batch", [24, 32])
+def test_folded_ln1_small_batch(batch, monkeypatch):
+    """From 24 positions, below whole rounds, LN1 alone is folded: the
+    out-projection (64 x 64 tiles) writes x o gamma1 with partial sums per 64
+    columns, FFN1 applies the LayerNorm in its epilogue and FFN2 rebuilds
+    its residual.  One LayerNorm launch per layer fewer than with
+    METALFISH_HIP_FOLD_LN=0, the same outputs to summation-order noise, and
+    the gates against the oracle."""
+    spec = synth.NetSpec("fold768", 768, 2, 24, 1024, input_ffn=512, smolgen_compress=32,
+                         smolgen_hidden=256, smolgen_gen=256, policy_dim=768)
+    weights = synth.make_weights(spec, seed=5)
+    n = 8
+    planes, legal = synth.playout_positions(n, seed=5)
+    ref = oracle.OracleNet(oracle.NetFormat(body_heads=24), weights).evaluate_batch(planes)
+    idx = np.arange(batch) % n
+    outs, lns = {}, {}
+    for env in ("1", "0"):
+        monkeypatch.setenv("METALFISH_HIP_FOLD_LN", env)
+        net = backend.create_network(spec, weights, max_batch=batch, device=0)
+        net.set_profiling(True)
+        net.profile_reset()
+        outs[env] = net.evaluate_batch(planes[idx])
+        lns[env] = net.profile().get("layernorm", {"launches": 0})["launches"]
+        net.close()
+    pol, wdl = outs["1"]["policy"], outs["1"]["wdl"]
+    perr = np.abs(pol - ref["policy"][idx]).max()
+    werr = np.abs(wdl - ref["wdl"][idx]).max()
+    top1 = _top1_agreement(pol, ref["policy"][idx], legal[idx])
+    print(f"batch {batch}: LayerNorm launches folded {lns['1']}, unfolded {lns['0']}; "
+          f"policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}", flush=True)
+    assert lns["0"] == lns["1"] + spec.layers
+    assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
+    assert np.abs(pol - outs["0"]["policy"]).max() <= 1e-4
+    assert np.abs(wdl - outs["0"]["wdl"]).max() <= 1e-5
+
+
 @pytest.mark.parametrize("embedding,heads,batch", [(512, 16, 4), (2048, 64, 4), (512, 16, 40)])
 def test_wide_embedding_layernorm_groups(embedding, heads, batch):
     """One-layer nets of embedding width 512 and 2048 (head depth 32): their
