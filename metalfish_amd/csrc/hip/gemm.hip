@@ -1423,8 +1423,10 @@ __global__ __launch_bounds__(WM *WN * 64, (LN && BM == 256 && BN == 128) ? 4 : 1
 }
 
 // Sums the k_splits fp32 partial tiles of a split-K launch in slice order
-// and applies the epilogue: one thread per four consecutive outputs.
-template <int MODE, int ACT>
+// and applies the epilogue: one thread per four consecutive outputs.  With
+// LN, the GEMM read folded rows (x o gamma) and the epilogue applies their
+// LayerNorm (p.fold_c, p.ln_stats) before the bias.
+template <int MODE, int ACT, bool LN = false>
 __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const float *part,
                                                             int splits) {
   const int groups = (p.N + 3) / 4;
@@ -1449,7 +1451,7 @@ __global__ __launch_bounds__(256) void ReduceEpilogueKernel(GemmParams p, const 
 #pragma unroll
   for (int r = 0; r < 4; ++r)
     b[r] = (p.bias && col + r < p.N) ? p.bias[col + r] : 0.f;
-  Epilogue4<MODE, ACT>(p, row, col, a, b);
+  Epilogue4<MODE, ACT, LN>(p, row, col, a, b);
 }
 
 template <int BM, int BN, int BK, int ST, int WM, int WN, bool SPLIT, int MODE, int ACT,
@@ -1495,16 +1497,24 @@ hipError_t LaunchVariant(const GemmParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int MODE, int ACT>
+template <int MODE, int ACT, bool LN = false>
 hipError_t LaunchReduce(const GemmParams &p, const float *part, int splits,
                         hipStream_t stream) {
   const long threads = static_cast<long>(p.M) * ((p.N + 3) / 4);
-  hipLaunchKernelGGL((ReduceEpilogueKernel<MODE, ACT>), dim3((threads + 255) / 256), dim3(256),
-                     0, stream, p, part, splits);
+  hipLaunchKernelGGL((ReduceEpilogueKernel<MODE, ACT, LN>), dim3((threads + 255) / 256),
+                     dim3(256), 0, stream, p, part, splits);
   return hipGetLastError();
 }
 
 hipError_t Reduce(const GemmParams &p, const float *part, int splits, hipStream_t stream) {
+  if (p.fold_c) {
+    // A folded LayerNorm's consumer (bf16 output only).
+    if (p.out_mode != GEMM_OUT_BF16 || !p.ln_stats)
+      return hipErrorInvalidValue;
+    return p.act == ACT_NONE
+               ? LaunchReduce<GEMM_OUT_BF16, ACT_NONE, true>(p, part, splits, stream)
+               : LaunchReduce<GEMM_OUT_BF16, ACT_RUNTIME, true>(p, part, splits, stream);
+  }
   if (p.out_mode == GEMM_OUT_RESID_F32)
     return LaunchReduce<GEMM_OUT_RESID_F32, ACT_NONE>(p, part, splits, stream);
   if (p.out_mode == GEMM_OUT_F32)
@@ -1598,7 +1608,7 @@ namespace {
 // GEMM with a folded LayerNorm runs on (the tiles the same shapes take
 // without it, where those are among them): split precision (bf16 hi + lo
 // activations, or the BF16X2_FP8LO codes), bf16 weights, one K slice.
-enum class LnTile { kNone, kLo8, k256, k256Beside, k256x128, k64, k64x64 };
+enum class LnTile { kNone, kLo8, k256, k256Beside, k256x128, k64, k64x64, kSplitK };
 
 LnTile LnFoldTile(const GemmParams &p) {
   const bool res = p.out_mode == GEMM_OUT_RESID_F32;
@@ -1618,10 +1628,15 @@ LnTile LnFoldTile(const GemmParams &p) {
     return LnTile::k64x64;
   if (res)
     return LnTile::kNone;
-  // Consumers: the small-LDS 64 x 64 tiles beside Q|K|V (any width), else
-  // 256 x 128 pipelined tiles.
+  // Consumers: the small-LDS 64 x 64 tiles beside Q|K|V (any width); narrow
+  // ones (the smolgen compression at 24-63 positions) split over K where
+  // the launcher splits them (the split GEMM sums x o gamma and the reduce
+  // kernel applies the LayerNorm before the bias), else on those 64 x 64
+  // tiles; else 256 x 128 pipelined tiles.
   if (p.small_lds)
     return LnTile::k64;
+  if (p.N < 128)
+    return GemmAutoSplits(p) > 1 ? LnTile::kSplitK : LnTile::k64;
   return p.N % 128 == 0 ? LnTile::k256x128 : LnTile::kNone;
 }
 
@@ -1798,6 +1813,10 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       return LaunchW<64, 64, 32, 2, 2, 2, true, false>(p, stream);
     case LnTile::k64x64:
       return LaunchW<64, 64, 64, 2, 2, 2, true, false>(p, stream);
+    case LnTile::kSplitK:
+      if (!Aligned(p.partials, 16) || !p.vec || p.N % 4)
+        return fail("folded LayerNorm split over K: 16-byte aligned partials, vector stores");
+      break;  // the split-K launch below, its reduce applying the LayerNorm
     default:
       return fail("folded LayerNorm: split-precision activations, bf16 weights, one K slice, "
                   "K % 64 == 0 and N a multiple of 256 (residual, BF16X2_FP8LO codes) or "
@@ -1826,6 +1845,7 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       q.ldc = p.N;
       q.split_n = 1 << 30;
       q.resid = nullptr;
+      q.fold_c = q.ln_stats = nullptr;  // plain sums of x o gamma
       q.k_splits = splits;
       q.vec = true;
       const bool small = p.small_lds && !p.W8;
@@ -1841,6 +1861,8 @@ hipError_t LaunchGemm(const GemmParams &p_in, hipStream_t stream, std::string *e
       return Reduce(r, p.partials, splits, stream);
     }
   }
+  if (p.fold_c)
+    return fail("folded LayerNorm: no tile for this shape");
   const int kslice = p.K / p.k_splits;
   // Tile choice measured on MI355X at the BT4 body shapes (M = 16384): for
   // K <= 1024, eight waves per workgroup on BK = 32 steps (split precision

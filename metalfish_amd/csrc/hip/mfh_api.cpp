@@ -112,8 +112,10 @@ constexpr int kLo8MinRows = 8192;
 // the residual GEMMs (N = E) take whole rounds of 256 x 256 tiles.
 constexpr long kFoldRows = 16384;
 // From this many token rows (24 positions), where the residual GEMMs take 64
-// x 64 tiles over the whole K, LN1 alone is folded (out-projection -> FFN1
-// and FFN2); the 64-wide residual tiles write partial sums per 64 columns.
+// x 64 tiles over the whole K, the same folds run on those tiles (partial
+// sums per 64 columns): LN1 (out-projection -> FFN1 and FFN2) and LN2 (FFN2
+// -> Q|K|V on 256 x 128 tiles, the compression split over K with the
+// LayerNorm applied by its reduce, and the next out-projection).
 constexpr long kFoldLn1Rows = 1536;
 
 std::uint16_t ToBf16(float f) {
@@ -269,8 +271,8 @@ struct mfh_net {
   // BF16X2_FP8LO: offset of a dense weight's W' (bf16, with column scales) ->
   // offset of its e4m3 codes.
   std::map<size_t, size_t> lo8_codes;
-  // The body's fold constants were packed (Layer::qkv_fold / ffn1_fold;
-  // ffn1_fold alone for has_fold1).
+  // The body's fold constants were packed (Layer::qkv_fold / ffn1_fold),
+  // for kFoldRows (has_fold) or kFoldLn1Rows (has_fold1) token rows.
   bool has_fold = false, has_fold1 = false;
   size_t head_b, qk_b, promo, val1_b, val2_w, val2_b, gather;
   size_t head_w[2], qk_w[2], val1_w[2];
@@ -892,9 +894,8 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       return rc;
   }
   // Folded residual LayerNorms of the body (split precisions, nets sized
-  // for kFoldRows token rows): Q|K|V (+ compression) of layer i > 0 over
+  // for kFoldLn1Rows token rows): Q|K|V (+ compression) of layer i > 0 over
   // layer i - 1's LN2, FFN1 of every layer over its LN1.
-  // (FFN1 over LN1 alone for nets sized for kFoldLn1Rows.)
   const long net_rows = static_cast<long>(net->max_batch) * kSquares;
   if (d.fold_ln && d.split && !d.fp8_act && !d.fused_ln && d.E % (2 * mfh::kLnStatCols) == 0 &&
       net_rows >= kFoldLn1Rows) {
@@ -903,7 +904,7 @@ int Pack(mfh_net *net, Loader &ld, Blob &blob) {
       Layer &L = net->layers[i];
       const bool qlo8 = net->lo8_codes.count(L.qkv_w[0]) > 0;
       const bool flo8 = net->lo8_codes.count(L.ffn1_w[0]) > 0;
-      if (i > 0 && net_rows >= kFoldRows) {
+      if (i > 0) {
         const Layer &P = net->layers[i - 1];
         AddLnFold(blob, L.qkv_w, net->fp8, qlo8, qrows, E, P.ln2_g, P.ln2_b, L.qkv_b,
                   L.qkv_fold);
@@ -1069,8 +1070,7 @@ size_t PlanLayout(const Dims &d, int batch, size_t splitk_floats, bool side,
       d.E % (2 * mfh::kLnStatCols) == 0 && M >= static_cast<size_t>(kFoldLn1Rows)) {
     // Per-row partial sums of the folded LayerNorms' rows (LN2: "st_act",
     // LN1: "st_mid"), per 64 columns at most.
-    if (M >= static_cast<size_t>(kFoldRows))
-      add("st_act", M * (d.E / 64) * 2 * 4);
+    add("st_act", M * (d.E / 64) * 2 * 4);
     add("st_mid", M * (d.E / 64) * 2 * 4);
   }
   if (d.lo8 && M >= static_cast<size_t>(kLo8MinRows)) {
@@ -1320,9 +1320,11 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
   // the folded epilogue.)
   bool fold = net->has_fold && full && ws.Has("st_act") && whole_round(M, E) &&
               M >= kSmolgenSideRows;
-  // Below whole rounds (kFoldLn1Rows on): LN1 alone, on the 64 x 64
-  // residual tiles (partial sums per 64 columns).
+  // Below whole rounds (kFoldLn1Rows on): LN1 on the 64 x 64 residual
+  // tiles (partial sums per 64 columns), and LN2 too where its consumers
+  // have tiles that fold it (fold2).
   bool fold1 = !fold && net->has_fold1 && full && ws.Has("st_mid") && M >= kFoldLn1Rows;
+  bool fold2 = fold1 && ws.Has("st_act") && M >= kSmolgenSideRows;
   float *st_act = nullptr, *st_mid = nullptr;
   // Columns per partial sum: 128 on the whole-round 256-wide tiles, 64 on
   // the 64-wide ones (set with the fold below).
@@ -1733,8 +1735,10 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     fold = (li == 0 || mfh::GemmLnFoldOk(pq)) && (li == 0 || !L.smolgen || mfh::GemmLnFoldOk(pc)) &&
            mfh::GemmLnFoldOk(pf) && mfh::GemmLnFoldOk(po) && mfh::GemmLnFoldOk(p2);
   }
-  // LN1 alone: the out-projection (writing x o gamma1 with its sums), FFN1
-  // (its consumer) and FFN2 (rebuilding the residual) on 64-wide tiles.
+  // LN1: the out-projection (writing x o gamma1 with its sums), FFN1 (its
+  // consumer) and FFN2 (rebuilding the residual) on 64-wide tiles.  LN2:
+  // FFN2 writing x o gamma2, Q|K|V and the compression (beside Q|K|V on
+  // the side stream) of the next layer as its consumers.
   for (int li = 0; fold1 && li < d.L; ++li) {
     const Layer &L = net->layers[li];
     const int bf16 = mfh::GEMM_OUT_BF16, res = mfh::GEMM_OUT_RESID_F32;
@@ -1751,8 +1755,16 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // FFN1 keeps the 64-wide tiles it takes without the fold.)
     auto t128 = [&](int n) { return static_cast<long>((M + 127) / 128) * ((n + 127) / 128); };
     fold1 = fold1 && t128(E) < 256 && t128(d.F) < 256;
+    if (li > 0 && fold2) {
+      mfh::GemmParams pq = gemm("act", E, L.qkv_w, E, M, 3 * E, E, nullptr, mfh::ACT_NONE, bf16,
+                                nullptr, nullptr, 3 * E);
+      mfh::GemmParams pc = gemm("act", E, L.qkv_w, E, M, d.C, E, nullptr, mfh::ACT_NONE, bf16,
+                                nullptr, nullptr, d.C);
+      fold2 = !pq.A_lo8 && mfh::GemmLnFoldOk(pq) && (!L.smolgen || mfh::GemmLnFoldOk(pc));
+    }
   }
-  if (fold) {
+  fold2 = fold2 && fold1;
+  if (fold || fold2) {
     st_act = ws.S<float>("st_act");
     st_mid = ws.S<float>("st_mid");
   } else if (fold1) {
@@ -1778,8 +1790,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     // after the last layer, whose LayerNorm the heads read.
     const bool body = li < d.L;
     const bool fold_mid = (fold || fold1) && body;
-    const bool fold_in = fold && body && li > 0;
-    const bool fold_out = fold && body && !body_out;
+    const bool fold_in = (fold || fold2) && body && li > 0;
+    const bool fold_out = (fold || fold2) && body && !body_out;
     const Layer *prev = fold_in ? &net->layers[li - 1] : nullptr;
     // A GEMM reading LN(x) of folded rows (x o gamma with stats st): the
     // LayerNorm in its epilogue with the fold constants {fold_c, bias'}.

@@ -277,12 +277,16 @@ def test_folded_layernorm_switch(monkeypatch):
 
 @pytest.mark.parametrize("batch", [24, 32])
 def test_folded_ln1_small_batch(batch, monkeypatch):
-    """From 24 positions, below whole rounds, LN1 alone is folded: the
-    out-projection (64 x 64 tiles) writes x o gamma1 with partial sums per 64
-    columns, FFN1 applies the LayerNorm in its epilogue and FFN2 rebuilds
-    its residual.  One LayerNorm launch per layer fewer than with
-    METALFISH_HIP_FOLD_LN=0, the same outputs to summation-order noise, and
-    the gates against the oracle."""
+    """From 24 positions, below whole rounds, both residual LayerNorms are
+    folded on the 64 x 64 residual tiles (partial sums per 64 columns): the
+    out-projection writes x o gamma1, FFN1 applies LN1 in its epilogue and
+    FFN2 rebuilds its residual from it; FFN2 writes x o gamma2, the next
+    layer's Q|K|V (256 x 128 tiles) applies LN2 in its epilogue, the
+    smolgen compression (split over K) in its reduce kernel, and the next
+    out-projection rebuilds its residual.  2L - 1 = 3 LayerNorm launches
+    fewer than with METALFISH_HIP_FOLD_LN=0 (the last layer's LN2 feeds the
+    heads), the same outputs to summation-order noise, and the gates against
+    the oracle."""
     spec = synth.NetSpec("fold768", 768, 2, 24, 1024, input_ffn=512, smolgen_compress=32,
                          smolgen_hidden=256, smolgen_gen=256, policy_dim=768)
     weights = synth.make_weights(spec, seed=5)
@@ -305,7 +309,7 @@ def test_folded_ln1_small_batch(batch, monkeypatch):
     top1 = _top1_agreement(pol, ref["policy"][idx], legal[idx])
     print(f"batch {batch}: LayerNorm launches folded {lns['1']}, unfolded {lns['0']}; "
           f"policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}", flush=True)
-    assert lns["0"] == lns["1"] + spec.layers
+    assert lns["0"] == lns["1"] + 2 * spec.layers - 1
     assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
     assert np.abs(pol - outs["0"]["policy"]).max() <= 1e-4
     assert np.abs(wdl - outs["0"]["wdl"]).max() <= 1e-5
