@@ -276,7 +276,7 @@ def test_folded_layernorm_switch(monkeypatch):
 
 
 @pytest.mark.parametrize("batch", [24, 32])
-def test_folded_ln1_small_batch(batch, monkeypatch):
+def test_folded_layernorms_small_batch(batch, monkeypatch):
     """From 24 positions, below whole rounds, both residual LayerNorms are
     folded on the 64 x 64 residual tiles (partial sums per 64 columns): the
     out-projection writes x o gamma1, FFN1 applies LN1 in its epilogue and
