@@ -315,6 +315,39 @@ def test_folded_layernorms_small_batch(batch, monkeypatch):
     assert np.abs(wdl - outs["0"]["wdl"]).max() <= 1e-5
 
 
+@pytest.mark.parametrize("batch", [48, 56])
+def test_bt4_folded_layernorms_wide_ffn1(batch, monkeypatch):
+    """43-62 positions at the BT4 widths: the residual GEMMs still take 64 x
+    64 tiles (fewer than 256 128 x 128 tiles), FFN1 (N = 1536) no longer
+    does, and both LayerNorms stay folded, FFN1 applying LN1 on 256 x 128
+    tiles with partial sums per 64 columns.  The 40 oracle-checked positions
+    fill the batch cyclically; each copy meets the bf16x2 gates, the forward
+    agrees with the unfolded one (METALFISH_HIP_FOLD_LN=0) to
+    summation-order noise, and it makes 2L - 1 LayerNorm launches fewer."""
+    spec = synth.SPECS["bt4"]
+    weights, planes, legal, ref = _reference("bt4", 40, 0, 0)
+    idx = np.arange(batch) % 40
+    outs, lns = {}, {}
+    for env in ("1", "0"):
+        monkeypatch.setenv("METALFISH_HIP_FOLD_LN", env)
+        net = backend.create_network(spec, weights, max_batch=batch, device=0)
+        net.set_profiling(True)
+        net.profile_reset()
+        outs[env] = net.evaluate_batch(planes[idx])
+        lns[env] = net.profile().get("layernorm", {"launches": 0})["launches"]
+        net.close()
+    pol, wdl = outs["1"]["policy"], outs["1"]["wdl"]
+    perr = np.abs(pol - ref["policy"][idx]).max()
+    werr = np.abs(wdl - ref["wdl"][idx]).max()
+    top1 = _top1_agreement(pol, ref["policy"][idx], legal[idx])
+    print(f"bt4 x{batch}: LayerNorm launches folded {lns['1']}, unfolded {lns['0']}; "
+          f"policy max-abs {perr:.3e} wdl max-abs {werr:.3e} top1 {top1:.3f}", flush=True)
+    assert lns["0"] == lns["1"] + 2 * spec.layers - 1
+    assert perr <= 1e-3 and werr <= 1e-4 and top1 >= 0.995
+    assert np.abs(pol - outs["0"]["policy"]).max() <= 1e-4
+    assert np.abs(wdl - outs["0"]["wdl"]).max() <= 1e-5
+
+
 @pytest.mark.parametrize("embedding,heads,batch", [(512, 16, 4), (2048, 64, 4), (512, 16, 40)])
 def test_wide_embedding_layernorm_groups(embedding, heads, batch):
     """One-layer nets of embedding width 512 and 2048 (head depth 32): their
