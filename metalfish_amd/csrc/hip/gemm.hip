@@ -1623,8 +1623,12 @@ LnTile LnFoldTile(const GemmParams &p) {
     return p.beside_chain && !res ? LnTile::k256Beside : LnTile::k256;
   // Fewer 128 x 128 tiles than CUs (24-63 positions at the BT4 widths): the
   // 64 x 64 tiles over the whole K that these shapes take without the fold.
+  // Consumers up to 2048 wide also up to two rounds of them (FFN1 at 43-62
+  // positions, 128 x 128 tiles without the fold; on 256 x 128 ones with it
+  // the forward was 3.4 % slower at batch 48, 0.5 % at 56).
   const long tiles128 = static_cast<long>((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (p.M >= kLargeRows && p.N >= 128 && tiles128 < 256 && p.N % 64 == 0)
+  if (p.M >= kLargeRows && p.N >= 128 && p.N % 64 == 0 &&
+      (tiles128 < 256 || (!res && p.N <= 2048 && tiles128 < 512)))
     return LnTile::k64x64;
   if (res)
     return LnTile::kNone;

@@ -1752,9 +1752,8 @@ int Forward(mfh_net *net, const WsView &ws, int B, const std::uint64_t *masks,
     for (const mfh::GemmParams *q : ps)
       fold1 = fold1 && !q->A_lo8 && mfh::GemmLnFoldOk(*q);
     // (The residual tiles must be the 64-wide ones their sums assume.  FFN1
-    // takes 64 x 64 tiles up to 42 positions at the BT4 widths, and 256 x
-    // 128 ones with the fold above, where it takes 128 x 128 tiles without
-    // it: batch 48 +4.1 %, 56 +1.3 % against no fold there.)
+    // takes 64 x 64 tiles with the fold, also above 42 positions at the BT4
+    // widths, where it takes 128 x 128 ones without it.)
     auto t128 = [&](int n) { return static_cast<long>((M + 127) / 128) * ((n + 127) / 128); };
     fold1 = fold1 && t128(E) < 256;
     if (li > 0 && fold2) {

@@ -318,9 +318,10 @@ def test_folded_layernorms_small_batch(batch, monkeypatch):
 @pytest.mark.parametrize("batch", [48, 56])
 def test_bt4_folded_layernorms_wide_ffn1(batch, monkeypatch):
     """43-62 positions at the BT4 widths: the residual GEMMs still take 64 x
-    64 tiles (fewer than 256 128 x 128 tiles), FFN1 (N = 1536) no longer
-    does, and both LayerNorms stay folded, FFN1 applying LN1 on 256 x 128
-    tiles with partial sums per 64 columns.  The 40 oracle-checked positions
+    64 tiles (fewer than 256 128 x 128 tiles), FFN1 (N = 1536) takes 128 x
+    128 tiles without the fold, and both LayerNorms stay folded, FFN1
+    applying LN1 on up to two rounds of 64 x 64 tiles (partial sums per 64
+    columns).  The 40 oracle-checked positions
     fill the batch cyclically; each copy meets the bf16x2 gates, the forward
     agrees with the unfolded one (METALFISH_HIP_FOLD_LN=0) to
     summation-order noise, and it makes 2L - 1 LayerNorm launches fewer."""
