@@ -1536,8 +1536,9 @@ hipError_t LaunchW(const GemmParams &p, hipStream_t stream) {
   // epilogue code is compiled only into the tiles that take it (LnFoldTile:
   // the pipelined split-precision and BF16X2_FP8LO tiles of the large
   // batches, the small-LDS split 64 x 64 tile of the smolgen compression
-  // beside Q|K|V, and the split 64 x 64 tiles of 24-63 positions), bf16
-  // outputs and the residual mode.
+  // beside Q|K|V and at 24-62 positions where its K is not split, and the
+  // split 64 x 64 tiles of 24-62 positions), bf16 outputs and the residual
+  // mode; the split-K reduce applies it for split consumers.
   constexpr bool kLn = !W8 && !F8 && (SPLIT || LO8) && (PIPE || (BM == 64 && BN == 64));
   if (p.fold_c || p.out_gamma || p.res_stats) {
     if constexpr (kLn) {
@@ -1621,7 +1622,7 @@ LnTile LnFoldTile(const GemmParams &p) {
     return p.N % 256 == 0 ? LnTile::kLo8 : LnTile::kNone;
   if (p.N % 256 == 0 && GemmWholeRoundTiles(p))
     return p.beside_chain && !res ? LnTile::k256Beside : LnTile::k256;
-  // Fewer 128 x 128 tiles than CUs (24-63 positions at the BT4 widths): the
+  // Fewer 128 x 128 tiles than CUs (24-62 positions at the BT4 widths): the
   // 64 x 64 tiles over the whole K that these shapes take without the fold.
   // Consumers up to 2048 wide also up to two rounds of them (FFN1 at 43-62
   // positions, 128 x 128 tiles without the fold; on 256 x 128 ones with it
@@ -1633,7 +1634,7 @@ LnTile LnFoldTile(const GemmParams &p) {
   if (res)
     return LnTile::kNone;
   // Consumers: the small-LDS 64 x 64 tiles beside Q|K|V (any width); narrow
-  // ones (the smolgen compression at 24-63 positions) split over K where
+  // ones (the smolgen compression at 24-62 positions) split over K where
   // the launcher splits them (the split GEMM sums x o gamma and the reduce
   // kernel applies the LayerNorm before the bias), else on those 64 x 64
   // tiles; else 256 x 128 pipelined tiles.
